@@ -1,0 +1,224 @@
+#!/usr/bin/env python
+"""Benchmark of the GLIF_3 V1 cell hot path on one MI355X.
+
+One step = one training pass of the config-2 workload: forward rollout of the
+66k-neuron network over T=500 ms at batch 5 (event-driven synaptic currents + fused
+GLIF_3 step), the firing-rate MSE loss, and BPTT through all 500 steps giving the
+recurrent and LGN weight gradients.  Inputs (LGN spikes, background Poisson counts)
+are resident in HBM before timing.  Prints one JSON line.
+
+The dominant kernel's roofline is measured live: its launches are bracketed by
+HIP events on the stream they run on (libglif's per-kernel timer), and its
+algorithmic bytes per launch are computed from the table sizes and the measured
+activity.  `traffic` comes from rocprofv3 FETCH_SIZE / WRITE_SIZE runs committed
+under profiles/ (null when absent).  The CPU baseline times the C restatement of
+the reference (oracle/) on a bounded prefix of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "neuron-timesteps/s fwd+bwd (66k neurons, B=5, T=500) + achieved HBM GB/s %"
+
+
+def _args():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2, help="benchmark configuration (2: fwd+BPTT)")
+    ap.add_argument("--mode", default="event", choices=["event", "deterministic"])
+    ap.add_argument("--seq-len", type=int, default=None)
+    ap.add_argument("--cpu-steps", type=int, default=10,
+                    help="timesteps of the CPU baseline sample (0: skip)")
+    ap.add_argument("--forward-only", action="store_true")
+    return ap.parse_args()
+
+
+def event_counts(tables, lgn, bkg, spike_count_total):
+    """Synaptic events of one rollout: rec spikes x fan-out, LGN / bkg active x fan-out."""
+    import numpy as np
+    N = tables.n_neurons
+    rec_fan = np.bincount(tables.rec.col % N, minlength=N).astype(np.float64)
+    lgn_fan = np.bincount(tables.lgn.col, minlength=tables.lgn.n_cols).astype(np.float64)
+    bkg_fan = np.bincount(tables.bkg.col, minlength=tables.bkg.n_cols).astype(np.float64)
+    e_rec = float(spike_count_total.astype(np.float64).sum(0) @ rec_fan)
+    e_lgn = float((lgn > 0).sum((0, 1)).astype(np.float64) @ lgn_fan)
+    e_bkg = float((bkg > 0).sum((0, 1)).astype(np.float64) @ bkg_fan)
+    return e_rec, e_lgn, e_bkg
+
+
+def load_traffic(name):
+    path = os.path.join(HERE, "profiles", f"{name}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
+def main():
+    args = _args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU data parallelism "
+                                   "is designed but not built (--gpus must be 1)"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from v1_glif_model_amd import _lib
+    from v1_glif_model_amd import synthetic as sy
+    from v1_glif_model_amd.models import V1Column, rate_loss_grad
+
+    cfg = sy.config(args.config)
+    T = args.seq_len or cfg.seq_len
+    B = cfg.batch
+    t_gen = time.time()
+    net = sy.make_network(cfg, seed=0)
+    lgn_np, bkg_np = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
+    targets_np = sy.make_rate_targets(cfg.n_neurons, seed=2)
+    cell = V1Column(net, mode=args.mode, gauss_std=0.5, dampening_factor=0.5,
+                    recurrent_dampening_factor=0.5, voltage_gradient_dampening=0.5,
+                    pseudo_gauss=True, train_input=True)
+    t_gen = time.time() - t_gen
+    dev = cell.device
+    tb = cell.tables
+    N, S = tb.n_neurons, tb.rec.n_syn
+    lgn = torch.tensor(lgn_np, device=dev)
+    bkg = torch.tensor(bkg_np, device=dev)
+    targets = torch.tensor(targets_np, device=dev)
+    ws = cell.workspace(B, T)
+    spike_count = torch.zeros((B, N), dtype=torch.int32, device=dev)
+    zero = cell.zero_state(B)
+    state = [s.clone() for s in zero]
+    want = ("rec", "lgn")
+    fwd_ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    timings = []
+
+    def step():
+        for s, z0 in zip(state, zero):
+            s.copy_(z0)
+        spike_count.zero_()
+        cell.refresh_weights(force=True)
+        fwd_ev[0].record()
+        cell.rollout(lgn, bkg, state=state, record_z=False, record_v=False, spike_count=spike_count,
+                     ws=ws)
+        fwd_ev[1].record()
+        if not args.forward_only:
+            _, gzn = rate_loss_grad(spike_count, targets, T)
+            cell.backward(gz_neuron=gzn, want=want)
+        fwd_ev[2].record()
+        timings.append(fwd_ev)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    sc_host = spike_count.cpu().numpy()
+    dominant = "push" if args.forward_only else "bwd_rec"
+    _lib.prof_enable([dominant])
+    _lib.prof_collect()
+    fwd_ms = bwd_ms = 0.0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+        torch.cuda.synchronize()
+        fwd_ms += fwd_ev[0].elapsed_time(fwd_ev[1])
+        bwd_ms += fwd_ev[1].elapsed_time(fwd_ev[2])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    prof = _lib.prof_collect()
+    _lib.prof_enable([])
+    # one more, untimed step with every kernel class timed, for the breakdown
+    _lib.prof_enable(list(_lib.PROF_KINDS))
+    step()
+    torch.cuda.synchronize()
+    breakdown = {k: {"ms_per_step": round(v[0], 3), "launches": v[1]} for k, v in _lib.prof_collect().items()}
+    _lib.prof_enable([])
+
+    ms_per_step = wall * 1000.0 / args.steps
+    value = B * N * T / (ms_per_step / 1000.0)
+    e_rec, e_lgn, e_bkg = event_counts(tb, lgn_np, bkg_np, sc_host)
+    fwd_ms /= args.steps
+    bwd_ms /= args.steps
+
+    # roofline of the dominant kernel
+    D, nb, nt = tb.max_delay, tb.n_basis, tb.basis.shape[0]
+    Wwin = 3 if 3 * B <= 16 else 1
+    Rg = 4
+    while Rg < Wwin * B:
+        Rg *= 2
+    words = (N + 63) // 64
+    tot_ms, launches = prof.get(dominant, (0.0, 0))
+    if dominant == "bwd_rec":
+        # per launch = one backward window of Wwin timesteps (the last window may be
+        # shorter; launches = ceil((T-2)/Wwin)): the type-phased table (post + weight,
+        # 8 B/synapse) and its (type, column) pointers once, the dz rows of the
+        # window's steps, the G projection read once, spike words, and the dW
+        # read-modify-write of the window's active events
+        steps_per_launch = (T - 2) / max(launches / args.steps, 1)
+        active = e_rec / max(T, 1) * steps_per_launch
+        alg_bytes = (S * 8 + (nt * D * N + 1) * 4 + steps_per_launch * B * D * N * 4 + N * nt * Rg * 4
+                     + (steps_per_launch + D) * B * words * 8 + active * 8)
+        unit_desc = f"bytes per backward window of {Wwin} timesteps"
+    else:
+        active = (e_rec + e_lgn) / max(T, 1)
+        alg_bytes = active * 8 + B * N * nb * 4 * 2
+        unit_desc = "bytes per forward timestep"
+    avg_ms = tot_ms / max(launches, 1)
+    achieved = alg_bytes / (avg_ms / 1000.0) / 1e9 if avg_ms > 0 else 0.0
+    traffic = load_traffic(dominant)
+    roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic.get("bytes_per_launch") if traffic else None,
+                "algorithmic_bytes_per_launch": int(alg_bytes), "basis": unit_desc,
+                "avg_launch_us": round(avg_ms * 1000.0, 2), "launches_timed": launches}
+
+    # CPU baseline: the C restatement on a bounded prefix of the same workload
+    cpu = None
+    if args.cpu_steps > 0:
+        from oracle.cpu import OracleCell
+        Tc = min(args.cpu_steps, T)
+        oc = OracleCell(tb, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.5, pseudo_gauss=True)
+        c0 = time.perf_counter()
+        oz, ov, oref, _ = oc.forward(lgn_np[:Tc], bkg_np[:Tc])
+        if not args.forward_only:
+            rbar = oz.reshape(Tc, B, N).mean((0, 1))
+            gzn = (2.0 / (N * B * Tc)) * (rbar - targets_np)
+            oc.backward(lgn_np[:Tc], bkg_np[:Tc], oz, oref, ov, gz_neuron=gzn.astype(np.float32),
+                        want=("rec", "lgn"))
+        cpu_s = time.perf_counter() - c0
+        cpu = {"value": round(B * N * Tc / cpu_s, 1), "unit": "neuron-timesteps/s", "cores": 1,
+               "kind": "port",
+               "sample": f"oracle/glif_oracle.c single thread, first {Tc} of {T} timesteps of the same "
+                         f"workload (B={B}, N={N}), {'forward only' if args.forward_only else 'forward + BPTT'}, "
+                         f"{cpu_s:.1f} s"}
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "neuron-timesteps/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"config {args.config}: {N} GLIF_3 neurons, {S} recurrent synapses, "
+                               f"B={B}, T={T}, {'forward' if args.forward_only else 'forward + BPTT (rec + LGN dW)'}",
+                   "neurons": N, "recurrent_synapses": S, "lgn_synapses": tb.lgn.n_syn,
+                   "bkg_synapses": tb.bkg.n_syn, "batch": B, "seq_len": T, "mode": args.mode},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(bwd_ms, 3),
+        "synaptic_events_per_s": round((e_rec + e_lgn + e_bkg) / (fwd_ms / 1000.0), 1) if fwd_ms else None,
+        "mean_rate_hz": round(float(sc_host.mean()) / T * 1000.0, 3),
+        "kernel_breakdown_ms": breakdown,
+        "setup_s": round(t_gen, 1),
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

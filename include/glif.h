@@ -1,0 +1,178 @@
+/*
+ * glif.h -- C ABI of libglif, the MI355X (gfx950) implementation of the GLIF_3 V1
+ * cell hot path of JavierGalvan9/V1_GLIF_model (`v1_model_utils/models.py`).
+ *
+ * Conventions
+ *   - Every call returns GLIF_OK (0) or a negative glif_status; glif_last_error()
+ *     returns a thread-local message for the last failing call.  No C++ exception
+ *     crosses this boundary.
+ *   - Device pointers are plain HIP device allocations (e.g. torch tensors' data).
+ *     Host pointers are marked "host".  All device work is stream-ordered on the
+ *     caller's stream (a hipStream_t passed as void*, NULL = default stream); no
+ *     call synchronises the device except glif_table_create / glif_cell_create
+ *     (one-time uploads).
+ *   - Index limits: n_syn < 2^31, n_post and presynaptic ids < 2^24, <= 256
+ *     synapse types, <= 256 delay slots, B <= 32, n_basis <= 8.
+ *
+ * The reference has no FFI: its boundary is the Python op and the Keras cell API.
+ * Each entry point below names the reference function it replaces; the Python
+ * mirror in v1_glif_model_amd/ keeps the reference names and argument order.
+ */
+#ifndef GLIF_H
+#define GLIF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    GLIF_OK = 0,
+    GLIF_EINVAL = -22,   /* bad argument (the reference raises ValueError)       */
+    GLIF_ERANGE = -34,   /* index out of range (models.py:308-314 ValueError)     */
+    GLIF_ENOMEM = -12,   /* host or device allocation failed / workspace too small */
+    GLIF_EHIP = -1000    /* a HIP runtime call failed                            */
+} glif_status;
+
+typedef enum {
+    GLIF_MODE_EVENT = 0,         /* event-driven push of active columns, fp32 atomics      */
+    GLIF_MODE_DETERMINISTIC = 1  /* post-row pull in the reference's accumulation order   */
+} glif_mode;
+
+typedef struct glif_table glif_table;  /* one synapse population, device resident */
+typedef struct glif_cell glif_cell;    /* GLIF_3 parameters + rec/LGN/bkg tables  */
+
+const char *glif_last_error(void);
+int glif_version(void);
+
+/* ---------------------------------------------------------------- A1 ---------
+ * make_pre_ind_table (models.py:343-373 with _validate_inputs :299-315 and
+ * _build_csr_order_numba :317-341): stable counting sort of synapse ids by
+ * presynaptic column.  host in: cols [n_syn] int64 (column 1 of `indices`);
+ * host out: order [n_syn] int32, row_splits [n_source + 1] int32.
+ * GLIF_EINVAL if n_source <= 0, GLIF_ERANGE (bad_index set) on an id outside
+ * [0, n_source). */
+int glif_make_pre_ind_table(const int64_t *cols, int64_t n_syn, int64_t n_source,
+                            int32_t *order, int32_t *row_splits, int64_t *bad_index);
+
+/* ---------------------------------------------------------------- A3 ---------
+ * tf.where(z > 0) (models.py:128, 823-826, 890): row-major list of (row, col)
+ * pairs of a [rows][cols] float32 device array.  device out: pairs [<= rows*cols][2]
+ * int64 and count [1] int64.  Workspace: glif_where_workspace(). */
+size_t glif_where_workspace(int64_t rows, int64_t cols);
+int glif_where_gt0(const float *z, int64_t rows, int64_t cols, int64_t *pairs, int64_t *count,
+                   void *ws, size_t ws_bytes, void *stream);
+
+/* ---------------------------------------------------------------- A2 ---------
+ * Synapse table of one population, built from the arrays V1Column.__init__ keeps
+ * (models.py:625-773).  host in, reference order (sorted by (post, pre)):
+ *   post [n_syn] int64, col [n_syn] int64 (pre + n_post*(delay-1) for the recurrent
+ *   table, pre for LGN/background), syn_id [n_syn] uint8,
+ *   basis [n_types][n_basis] float32 (synaptic_basis_weights).
+ * n_delay_slots = D for the recurrent table (n_cols = D * n_post), 1 for inputs. */
+int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *syn_id,
+                      int64_t n_syn, int32_t n_post, int64_t n_cols, int32_t n_delay_slots,
+                      const float *basis, int32_t n_types, int32_t n_basis, glif_table **out);
+void glif_table_destroy(glif_table *t);
+int64_t glif_table_n_syn(const glif_table *t);
+/* Device pointers owned by the table: the bit-exact A1 result (order int32 [n_syn],
+ * row_splits int32 [n_cols + 1]). */
+int glif_table_pre_ind(const glif_table *t, const int32_t **order, const int32_t **row_splits);
+/* refresh_recurrent_weight_shadow (models.py:966-976): copy the trainable weight
+ * vector w [n_syn] (device, reference order) into the table's column- and
+ * row-grouped copies.  Must be called before use and after every weight update. */
+int glif_table_set_weights(glif_table *t, const float *w, void *stream);
+
+/* ------------------------------------------------------------ A4-A8 ----------
+ * calculate_synaptic_currents (models.py:103-263).
+ * Forward: z [B][n_cols] float32 device (event where z > 0; with counts != 0 the
+ * value scales the weight as the background current does, models.py:917-931);
+ * out: I [B*n_post][n_basis] float32 (overwritten).  mode: glif_mode. */
+size_t glif_syn_workspace(const glif_table *t, int32_t B);
+int glif_syn_fwd(const glif_table *t, const float *z, int32_t B, int32_t counts, int32_t mode,
+                 float *I, void *ws, size_t ws_bytes, void *stream);
+/* Custom gradient (models.py:174-261): dy [B*n_post][n_basis] float32 device;
+ * out dz [B][n_cols] (the gradient w.r.t. rec_z_buf, dense over all synapses; NULL
+ * to skip) and dw [n_syn] (w.r.t. weight_values, reference order; NULL to skip),
+ * both overwritten. */
+int glif_syn_bwd(const glif_table *t, const float *z, const float *dy, int32_t B, int32_t counts,
+                 float *dz, float *dw, void *ws, size_t ws_bytes, void *stream);
+
+/* ------------------------------------------------------------ A11-A17 --------
+ * V1Column (models.py:450-1135) run over T steps on one stream. */
+typedef struct {
+    int32_t n_neurons;
+    int32_t n_delay;            /* max_delay (D) */
+    int32_t n_basis;            /* nb */
+    float dt;
+    float lr_scale;
+    float voltage_gradient_dampening;  /* vgd, models.py:1010 */
+    float recurrent_dampening;         /* rd,  models.py:1081 */
+    float gauss_std;
+    float dampening_factor;
+    int32_t pseudo_gauss;       /* 1: spike_gauss surrogate, 0: triangular spike_function */
+    int32_t hard_reset;
+} glif_cell_config;
+
+/* host in: decay, current_factor [N]; asc_decay, asc_amps [N][2]; t_ref_steps [N]
+ * int32; syn_decay, psc_initial [n_basis].  The tables are borrowed (not owned) and
+ * must outlive the cell; their n_post must equal n_neurons and rec must have
+ * n_delay slots. */
+int glif_cell_create(const glif_cell_config *cfg, const float *decay, const float *current_factor,
+                     const float *asc_decay, const float *asc_amps, const int32_t *t_ref_steps,
+                     const float *syn_decay, const float *psc_initial, glif_table *rec,
+                     glif_table *lgn, glif_table *bkg, glif_cell **out);
+void glif_cell_destroy(glif_cell *c);
+
+/* The state tuple of models.py:1030-1056, device pointers, reference layouts:
+ * z_buf [B][D*N] f32, v [B][N] f32, r [B][N] int16 (refractory steps left),
+ * asc [B][N*2] f32, psc_rise [B][N*nb] f32, psc [B][N*nb] f32. */
+typedef struct {
+    float *z_buf;
+    float *v;
+    int16_t *r;
+    float *asc;
+    float *psc_rise;
+    float *psc;
+} glif_state;
+
+/* Workspace of a T-step rollout at batch B: rings, spike history, saved voltages
+ * and the backward's adjoint buffers.  The same workspace must be passed to the
+ * glif_cell_backward that follows a glif_cell_forward. */
+size_t glif_cell_workspace(const glif_cell *c, int32_t B, int32_t T);
+
+/* Forward rollout (the Keras RNN over V1Column.call, models.py:1317-1322).
+ * device in: lgn [T][B][n_lgn] uint8 (spike where > 0), bkg [T][B][n_bkg] uint8
+ * (Poisson counts; TF's stateless Poisson stream is not reproducible, so counts are
+ * an input).  state: in/out.  out (each may be NULL): z [T][B][N] f32, v [T][B][N]
+ * f32 (the cell outputs), spike_count [B][N] int32 (accumulated). */
+int glif_cell_forward(glif_cell *c, int32_t B, int32_t T, int32_t mode, const uint8_t *lgn,
+                      const uint8_t *bkg, glif_state *state, float *z_out, float *v_out,
+                      int32_t *spike_count, void *ws, size_t ws_bytes, void *stream);
+
+/* BPTT through the last glif_cell_forward on `ws` (zero initial state assumed for
+ * the adjoint; gradients do not flow into the initial state).
+ * device in (each may be NULL): gz [T][B][N] dL/dz, gz_neuron [N] dL/dz broadcast
+ * over (t, b), gv [T][B][N] dL/dv.  out (each may be NULL): dw_rec, dw_lgn, dw_bkg,
+ * gradients of the three weight vectors in reference order (overwritten). */
+int glif_cell_backward(glif_cell *c, int32_t B, int32_t T, const float *gz,
+                       const float *gz_neuron, const float *gv, float *dw_rec, float *dw_lgn,
+                       float *dw_bkg, void *ws, size_t ws_bytes, void *stream);
+
+/* ------------------------------------------------------------ profiling ------
+ * No reference counterpart (the reference times whole steps with time(),
+ * callbacks.py:1442-1449).  Kernel classes: 0 push, 1 step, 2 adj, 3 bwd_rec,
+ * 4 bwd_lgn, 5 bwd_bkg, 6 syn_fwd, 7 syn_bwd.  While bit k of `mask` is set, every
+ * launch of class k is bracketed by two HIP events on its stream.
+ * glif_prof_collect waits for the recorded events and returns, per class, the
+ * summed elapsed milliseconds and the number of launches since the last collect. */
+int glif_prof_enable(uint32_t mask);
+int glif_prof_collect(double *total_ms, int64_t *count, int32_t n);
+const char *glif_prof_name(int32_t kind);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GLIF_H */

@@ -1,0 +1,343 @@
+/*
+ * glif_oracle.c -- CPU restatement of the GLIF_3 V1 cell hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP library
+ * (v1_glif_model_amd/csrc).  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product path never does.
+ *
+ * It restates, in plain C, the arithmetic of JavierGalvan9/V1_GLIF_model
+ * `v1_model_utils/models.py` (paths below are relative to the reference root):
+ *
+ *   orc_csr_build     models.py:317-341 (_build_csr_order_numba): stable counting
+ *                     sort of synapse ids by presynaptic column -> (order, row_splits);
+ *                     models.py:299-315 (_validate_inputs) error behaviour.
+ *   orc_where_gt0     models.py:128 (tf.where(rec_z_buf > 0)): row-major (b, col) list.
+ *   orc_syn_fwd       models.py:126-169 (forward of calculate_synaptic_currents) and the
+ *                     LGN / background twins models.py:814-863, 865-940.  Accumulation
+ *                     order is the sequential UnsortedSegmentSum order of TF's CPU
+ *                     kernel: events in (b, col) order, synapses of a column in
+ *                     ascending synapse index, each term the fp32 product
+ *                     (w * count) * basis[syn_id, r].
+ *   orc_syn_bwd       models.py:174-261 (custom gradient): per receptor r a sparse-dense
+ *                     product over all synapses in SparseTensor order, summed over r
+ *                     (dz); per active event einsum('cr,cr->c') scattered into [S] (dW).
+ *   orc_forward       models.py:979-1028, 1059-1135 (V1Column.call) over T steps.
+ *   orc_backward      reverse-mode derivative of orc_forward as TF's autodiff builds it
+ *                     (stop_gradient on prev_z and on r, straight-through dampening of
+ *                     the spike buffer and of v, refractory-masked surrogate).
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off: every a*b+c rounds twice, as
+ * TF's separate Mul/Add kernels do).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORC_EINVAL (-22)
+#define ORC_ERANGE (-34)
+#define ORC_ENOMEM (-12)
+
+/* ------------------------------------------------------------------ A1 ---- */
+/* Returns 0, or ORC_EINVAL (n_cols <= 0), or ORC_ERANGE with *bad_index set to the
+ * first offending synapse (models.py:308-314 raises ValueError there). */
+int orc_csr_build(const int64_t *cols, int64_t S, int64_t n_cols, int64_t *order,
+                  int64_t *row_splits, int64_t *bad_index)
+{
+    if (n_cols <= 0) return ORC_EINVAL;
+    for (int64_t i = 0; i < S; ++i) {
+        if (cols[i] < 0 || cols[i] >= n_cols) {
+            if (bad_index) *bad_index = i;
+            return ORC_ERANGE;
+        }
+    }
+    memset(row_splits, 0, (size_t)(n_cols + 1) * sizeof(int64_t));
+    for (int64_t i = 0; i < S; ++i) row_splits[cols[i] + 1] += 1;
+    for (int64_t c = 0; c < n_cols; ++c) row_splits[c + 1] += row_splits[c];
+    int64_t *wp = (int64_t *)malloc((size_t)n_cols * sizeof(int64_t));
+    if (!wp) return ORC_ENOMEM;
+    memcpy(wp, row_splits, (size_t)n_cols * sizeof(int64_t));
+    for (int64_t i = 0; i < S; ++i) order[wp[cols[i]]++] = i;
+    free(wp);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ A3 ---- */
+int64_t orc_where_gt0(const float *z, int64_t rows, int64_t cols, int64_t *out)
+{
+    int64_t n = 0;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            if (z[r * cols + c] > 0.0f) {
+                if (out) { out[2 * n] = r; out[2 * n + 1] = c; }
+                ++n;
+            }
+    return n;
+}
+
+/* ------------------------------------------------------------- A4-A6 ---- */
+/* act: [B][n_cols] values, an event where act > 0.  use_count: scale the weight by
+ * the value (background Poisson counts, models.py:917-931); otherwise value 1.
+ * I: [B*n_post][nb], accumulated into (the caller zeroes it). */
+void orc_syn_fwd(int B, int64_t n_post, int64_t n_cols, int nb, const float *act, int use_count,
+                 const int64_t *post, const float *w, const uint8_t *sid, const float *basis,
+                 const int64_t *order, const int64_t *row_splits, float *I)
+{
+    for (int b = 0; b < B; ++b)
+        for (int64_t c = 0; c < n_cols; ++c) {
+            float a = act[(int64_t)b * n_cols + c];
+            if (!(a > 0.0f)) continue;
+            float cnt = use_count ? a : 1.0f;
+            for (int64_t k = row_splits[c]; k < row_splits[c + 1]; ++k) {
+                int64_t s = order[k];
+                float wv = w[s] * cnt;
+                float *dst = I + ((int64_t)b * n_post + post[s]) * nb;
+                const float *bs = basis + (int64_t)sid[s] * nb;
+                for (int r = 0; r < nb; ++r) dst[r] += wv * bs[r];
+            }
+        }
+}
+
+/* ---------------------------------------------------------------- A7-A8 ---- */
+/* dy: [B*n_post][nb].  dz: [B][n_cols] (written, may be NULL).  dW: [S] accumulated
+ * (may be NULL).  act/use_count as in orc_syn_fwd (events for dW only).
+ * scratch: [B][n_cols] floats when dz != NULL. */
+void orc_syn_bwd(int B, int64_t n_post, int64_t n_cols, int nb, int64_t S, const float *act,
+                 int use_count, const int64_t *post, const int64_t *col, const float *w,
+                 const uint8_t *sid, const float *basis, const int64_t *order,
+                 const int64_t *row_splits, const float *dy, float *dz, float *dW, float *scratch)
+{
+    if (dz) {
+        memset(dz, 0, sizeof(float) * (size_t)B * (size_t)n_cols);
+        for (int r = 0; r < nb; ++r) {
+            memset(scratch, 0, sizeof(float) * (size_t)B * (size_t)n_cols);
+            for (int64_t s = 0; s < S; ++s) {
+                float wr = w[s] * basis[(int64_t)sid[s] * nb + r];
+                for (int b = 0; b < B; ++b)
+                    scratch[(int64_t)b * n_cols + col[s]] +=
+                        dy[((int64_t)b * n_post + post[s]) * nb + r] * wr;
+            }
+            for (int64_t i = 0; i < (int64_t)B * n_cols; ++i) dz[i] += scratch[i];
+        }
+    }
+    if (dW) {
+        for (int b = 0; b < B; ++b)
+            for (int64_t c = 0; c < n_cols; ++c) {
+                float a = act[(int64_t)b * n_cols + c];
+                if (!(a > 0.0f)) continue;
+                for (int64_t k = row_splits[c]; k < row_splits[c + 1]; ++k) {
+                    int64_t s = order[k];
+                    const float *g = dy + ((int64_t)b * n_post + post[s]) * nb;
+                    const float *bs = basis + (int64_t)sid[s] * nb;
+                    float e = g[0] * bs[0];
+                    for (int r = 1; r < nb; ++r) e += g[r] * bs[r];
+                    if (use_count) e = e * a;
+                    dW[s] += e;
+                }
+            }
+    }
+}
+
+/* ---------------------------------------------------------------- cell ---- */
+typedef struct {
+    int64_t S, n_cols;
+    const int64_t *post, *col, *order, *row_splits;
+    const float *w;
+    const uint8_t *sid;
+} orc_table;
+
+typedef struct {
+    int64_t N, D;
+    int32_t nb, n_types;
+    const float *decay, *cf;            /* [N] */
+    const float *asc_decay, *asc_amps;  /* [N][2] */
+    const int32_t *tref;                /* [N] */
+    const float *syn_decay, *psc_initial; /* [nb] */
+    const float *basis;                 /* [n_types][nb] */
+    float dt, lr_scale, vgd, rd, gauss_std, damp;
+    int32_t pseudo_gauss, hard_reset;
+    orc_table rec, lgn, bkg;
+} orc_cell;
+
+static float surrogate(const orc_cell *c, float vsc)
+{
+    if (c->pseudo_gauss) {
+        float q = -(vsc * vsc) / (c->gauss_std * c->gauss_std);
+        return expf(q) * c->damp;
+    }
+    float a = 1.0f - fabsf(vsc);
+    return c->damp * (a > 0.0f ? a : 0.0f);
+}
+
+/* State layout is the reference's (models.py:1030-1056):
+ *   zbuf [B][D*N] (slot d-1 holds z_{t-d}), v [B][N], r [B][N], asc [B][N*2],
+ *   R (psc_rise) [B][N*nb], P (psc) [B][N*nb].
+ * Inputs per step: lgn [T][B][n_lgn] uint8 (spike > 0), bkg [T][B][n_bkg] uint8 counts.
+ * Outputs (each may be NULL): z_out, ref_out [T][B][N] uint8; v_out [T][B][N] float. */
+int orc_forward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint8_t *bkg,
+                float *zbuf, float *v, int32_t *r, float *asc, float *R, float *P,
+                uint8_t *z_out, float *v_out, uint8_t *ref_out)
+{
+    const int64_t N = c->N, D = c->D;
+    const int nb = c->nb;
+    const int64_t BN = (int64_t)B * N;
+    float *Irec = (float *)calloc((size_t)BN * nb, sizeof(float));
+    float *Ilgn = (float *)calloc((size_t)BN * nb, sizeof(float));
+    float *Ibkg = (float *)calloc((size_t)BN * nb, sizeof(float));
+    float *xl = (float *)malloc(sizeof(float) * (size_t)B * (size_t)(c->lgn.n_cols + 1));
+    float *xb = (float *)malloc(sizeof(float) * (size_t)B * (size_t)(c->bkg.n_cols + 1));
+    float *znew = (float *)malloc(sizeof(float) * (size_t)N);
+    if (!Irec || !Ilgn || !Ibkg || !xl || !xb || !znew) {
+        free(Irec); free(Ilgn); free(Ibkg); free(xl); free(xb); free(znew);
+        return ORC_ENOMEM;
+    }
+    float dtsd[64];
+    for (int q = 0; q < nb; ++q) dtsd[q] = c->dt * c->syn_decay[q];
+    float vgd = c->vgd < 0.0f ? 0.0f : (c->vgd > 1.0f ? 1.0f : c->vgd);
+    float om = 1.0f - vgd;
+
+    for (int t = 0; t < T; ++t) {
+        memset(Irec, 0, sizeof(float) * (size_t)BN * nb);
+        memset(Ilgn, 0, sizeof(float) * (size_t)BN * nb);
+        memset(Ibkg, 0, sizeof(float) * (size_t)BN * nb);
+        orc_syn_fwd(B, N, D * N, nb, zbuf, 0, c->rec.post, c->rec.w, c->rec.sid, c->basis,
+                    c->rec.order, c->rec.row_splits, Irec);
+        for (int64_t i = 0; i < (int64_t)B * c->lgn.n_cols; ++i)
+            xl[i] = (float)lgn[(int64_t)t * B * c->lgn.n_cols + i];
+        orc_syn_fwd(B, N, c->lgn.n_cols, nb, xl, 0, c->lgn.post, c->lgn.w, c->lgn.sid, c->basis,
+                    c->lgn.order, c->lgn.row_splits, Ilgn);
+        for (int64_t i = 0; i < (int64_t)B * c->bkg.n_cols; ++i)
+            xb[i] = (float)bkg[(int64_t)t * B * c->bkg.n_cols + i];
+        orc_syn_fwd(B, N, c->bkg.n_cols, nb, xb, 1, c->bkg.post, c->bkg.w, c->bkg.sid, c->basis,
+                    c->bkg.order, c->bkg.row_splits, Ibkg);
+
+        for (int b = 0; b < B; ++b) {
+            for (int64_t n = 0; n < N; ++n) {
+                const int64_t bn = (int64_t)b * N + n;
+                float zp = zbuf[(int64_t)b * D * N + n];
+                float *Rn = R + bn * nb, *Pn = P + bn * nb, *An = asc + bn * 2;
+                float sumP = Pn[0];
+                for (int q = 1; q < nb; ++q) sumP = sumP + Pn[q];
+                float c1 = sumP + (An[0] + An[1]);
+                for (int q = 0; q < nb; ++q) {
+                    float in = ((Irec[bn * nb + q] + Ilgn[bn * nb + q]) + Ibkg[bn * nb + q]) * c->lr_scale;
+                    float Rold = Rn[q];
+                    Rn[q] = Rold * c->syn_decay[q] + in * c->psc_initial[q];
+                    Pn[q] = Pn[q] * c->syn_decay[q] + dtsd[q] * Rold;
+                }
+                for (int j = 0; j < 2; ++j)
+                    An[j] = c->asc_decay[n * 2 + j] * An[j] + zp * c->asc_amps[n * 2 + j];
+                float vv = v[bn];
+                float dv = vv * om + vv * vgd;
+                float vn = (c->decay[n] * dv + c->cf[n] * c1) - zp;
+                int32_t rn = r[bn] + (int32_t)zp * c->tref[n] - 1;
+                if (rn < 0) rn = 0;
+                if (c->hard_reset && rn > 0) vn = 0.0f;
+                float z = (rn > 0) ? 0.0f : ((vn - 1.0f) > 0.0f ? 1.0f : 0.0f);
+                v[bn] = vn;
+                r[bn] = rn;
+                if (z_out) z_out[(int64_t)t * BN + bn] = (uint8_t)z;
+                if (v_out) v_out[(int64_t)t * BN + bn] = vn;
+                if (ref_out) ref_out[(int64_t)t * BN + bn] = (uint8_t)(rn > 0);
+                znew[n] = z;
+            }
+            /* new_z_buf = concat([new_z, z_buf[:, :-N]]) (models.py:1117) */
+            float *zb = zbuf + (int64_t)b * D * N;
+            memmove(zb + N, zb, sizeof(float) * (size_t)((D - 1) * N));
+            memcpy(zb, znew, sizeof(float) * (size_t)N);
+        }
+    }
+    free(Irec); free(Ilgn); free(Ibkg); free(xl); free(xb); free(znew);
+    return 0;
+}
+
+/* BPTT through orc_forward.  Saved forward data: z [T][B][N], ref (r_t > 0)
+ * [T][B][N] uint8, v [T][B][N] float (all from orc_forward with zero initial
+ * state), inputs lgn/bkg as in orc_forward.
+ * Loss gradients: gz_loss [T][B][N] (or NULL) plus gz_neuron [N] broadcast over
+ * (t, b) (or NULL); gv_loss [T][B][N] (or NULL).
+ * Outputs: dW_rec [S_rec], dW_lgn [S_lgn], dW_bkg [S_bkg] accumulated (each may be
+ * NULL); gz_out [T][B][N] total spike gradient (may be NULL). */
+int orc_backward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint8_t *bkg,
+                 const uint8_t *zs, const uint8_t *refs, const float *vs,
+                 const float *gz_loss, const float *gz_neuron, const float *gv_loss,
+                 float *dW_rec, float *dW_lgn, float *dW_bkg, float *gz_out)
+{
+    const int64_t N = c->N, D = c->D;
+    const int nb = c->nb;
+    const int64_t BN = (int64_t)B * N, DN = D * N;
+    float *gVp = (float *)calloc((size_t)BN, sizeof(float));
+    float *gP = (float *)calloc((size_t)BN * nb, sizeof(float));
+    float *gR = (float *)calloc((size_t)BN * nb, sizeof(float));
+    float *dy = (float *)calloc((size_t)BN * nb, sizeof(float));
+    float *ring = (float *)calloc((size_t)(D + 1) * BN, sizeof(float));
+    float *dz = (float *)malloc(sizeof(float) * (size_t)B * (size_t)DN);
+    float *scr = (float *)malloc(sizeof(float) * (size_t)B * (size_t)DN);
+    float *act = (float *)malloc(sizeof(float) * (size_t)B * (size_t)DN);
+    int64_t nin = c->lgn.n_cols > c->bkg.n_cols ? c->lgn.n_cols : c->bkg.n_cols;
+    float *xin = (float *)malloc(sizeof(float) * (size_t)B * (size_t)(nin + 1));
+    if (!gVp || !gP || !gR || !dy || !ring || !dz || !scr || !act || !xin) {
+        free(gVp); free(gP); free(gR); free(dy); free(ring); free(dz); free(scr); free(act); free(xin);
+        return ORC_ENOMEM;
+    }
+    float dtsd[64];
+    for (int q = 0; q < nb; ++q) dtsd[q] = c->dt * c->syn_decay[q];
+    float vgd = c->vgd < 0.0f ? 0.0f : (c->vgd > 1.0f ? 1.0f : c->vgd);
+    float om = 1.0f - vgd;
+    float rd = c->rd < 0.0f ? 0.0f : (c->rd > 1.0f ? 1.0f : c->rd);
+    /* straight_through_dampen(z_buf, 1 - rd): the backward scale is 1 - (1 - rd) */
+    float zscale = 1.0f - (1.0f - rd);
+
+    for (int t = T - 1; t >= 0; --t) {
+        float *slot = ring + (int64_t)(t % (D + 1)) * BN;
+        for (int b = 0; b < B; ++b)
+            for (int64_t n = 0; n < N; ++n) {
+                const int64_t bn = (int64_t)b * N + n, tbn = (int64_t)t * BN + bn;
+                float gz = slot[bn];
+                if (gz_loss) gz = gz + gz_loss[tbn];
+                if (gz_neuron) gz = gz + gz_neuron[n];
+                if (gz_out) gz_out[tbn] = gz;
+                slot[bn] = 0.0f;
+                float psi = refs[tbn] ? 0.0f : surrogate(c, vs[tbn] - 1.0f);
+                float gV = gz * psi;
+                if (gv_loss) gV = gV + gv_loss[tbn];
+                gV = gV + (gVp[bn] * c->decay[n]) * om;
+                float gVnext = gVp[bn];   /* gV'_{t+1} */
+                gVp[bn] = (c->hard_reset && refs[tbn]) ? 0.0f : gV;
+                for (int q = 0; q < nb; ++q) {
+                    float gPn = gP[bn * nb + q], gRn = gR[bn * nb + q];
+                    gP[bn * nb + q] = gPn * c->syn_decay[q] + gVnext * c->cf[n];
+                    gR[bn * nb + q] = gRn * c->syn_decay[q] + gPn * dtsd[q];
+                    dy[bn * nb + q] = (gR[bn * nb + q] * c->psc_initial[q]) * c->lr_scale;
+                }
+            }
+        /* recurrent: rec_z_buf at step t holds z_{t-d} in slot d-1 */
+        for (int b = 0; b < B; ++b)
+            for (int64_t d = 1; d <= D; ++d)
+                for (int64_t n = 0; n < N; ++n)
+                    act[(int64_t)b * DN + (d - 1) * N + n] =
+                        (t - d >= 0) ? (float)zs[(int64_t)(t - d) * BN + (int64_t)b * N + n] : 0.0f;
+        orc_syn_bwd(B, N, DN, nb, c->rec.S, act, 0, c->rec.post, c->rec.col, c->rec.w, c->rec.sid,
+                    c->basis, c->rec.order, c->rec.row_splits, dy, dz, dW_rec, scr);
+        for (int b = 0; b < B; ++b)
+            for (int64_t d = 1; d <= D && t - d >= 0; ++d) {
+                float *dst = ring + (int64_t)((t - d) % (D + 1)) * BN + (int64_t)b * N;
+                const float *src = dz + (int64_t)b * DN + (d - 1) * N;
+                for (int64_t n = 0; n < N; ++n) dst[n] = dst[n] + src[n] * zscale;
+            }
+        if (dW_lgn) {
+            for (int64_t i = 0; i < (int64_t)B * c->lgn.n_cols; ++i)
+                xin[i] = (float)lgn[(int64_t)t * B * c->lgn.n_cols + i];
+            orc_syn_bwd(B, N, c->lgn.n_cols, nb, c->lgn.S, xin, 0, c->lgn.post, c->lgn.col, c->lgn.w,
+                        c->lgn.sid, c->basis, c->lgn.order, c->lgn.row_splits, dy, NULL, dW_lgn, NULL);
+        }
+        if (dW_bkg) {
+            for (int64_t i = 0; i < (int64_t)B * c->bkg.n_cols; ++i)
+                xin[i] = (float)bkg[(int64_t)t * B * c->bkg.n_cols + i];
+            orc_syn_bwd(B, N, c->bkg.n_cols, nb, c->bkg.S, xin, 1, c->bkg.post, c->bkg.col, c->bkg.w,
+                        c->bkg.sid, c->basis, c->bkg.order, c->bkg.row_splits, dy, NULL, dW_bkg, NULL);
+        }
+    }
+    free(gVp); free(gP); free(gR); free(dy); free(ring); free(dz); free(scr); free(act); free(xin);
+    return 0;
+}

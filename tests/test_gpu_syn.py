@@ -1,0 +1,130 @@
+"""GPU parity of the synaptic-current operator (A1, A3-A8) against the CPU oracle.
+
+Bars: compaction and CSR/CSC bit-exact; deterministic forward bit-exact with the
+oracle's reference-order fp32 sum; event (atomic) forward and the backward within
+1e-5 relative / 1e-6 absolute (scaled, where a value is a sum with cancellation,
+by the sum of absolute terms -- see each test).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cpu as orc
+from oracle import dense
+from tests.helpers import device_to_numpy, network, tiny_config
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(seed=0, dense_basis=True, **kw):
+    from v1_glif_model_amd.ops import SynapseTable
+    cfg = tiny_config(**kw)
+    net, tb = network(cfg, seed=seed, dense_basis=dense_basis)
+    t = SynapseTable(tb.rec.indices, tb.rec.syn_id, (tb.n_neurons, tb.rec.n_cols), tb.basis,
+                     n_delay_slots=tb.max_delay)
+    w = torch.tensor(tb.rec.weight, device="cuda")
+    t.set_weights(w)
+    return tb, t, w
+
+
+def _spikes(rng, B, cols, p):
+    return (rng.random((B, cols)) < p).astype(np.float32)
+
+
+def test_pre_ind_table_on_device_matches_reference_build():
+    """The table's device order/row_splits equal the reference's numpy fallback."""
+    tb, t, _ = _setup()
+    o_ptr, r_ptr = t.pre_ind_device()
+    S, C = tb.rec.n_syn, tb.rec.n_cols
+    ref_o, ref_r = dense.csr_build_numpy(tb.rec.col, C)
+    np.testing.assert_array_equal(device_to_numpy(o_ptr, S, np.int32), ref_o)
+    np.testing.assert_array_equal(device_to_numpy(r_ptr, C + 1, np.int32), ref_r)
+
+
+@pytest.mark.parametrize("rows,cols,p", [(1, 1, 1.0), (3, 1000, 0.01), (5, 5000, 0.3), (2, 70001, 0.001),
+                                         (4, 0, 0.5), (0, 10, 0.5)])
+def test_where_matches_argwhere(rows, cols, p):
+    from v1_glif_model_amd.ops import where_gt0
+    rng = np.random.default_rng(rows * 7919 + cols)
+    z = (rng.random((rows, cols)) < p).astype(np.float32) * rng.choice([1.0, 0.5, 2.0], (rows, cols)).astype(np.float32)
+    if rows and cols:
+        z[0, -1] = -1.0  # negative values are not events
+    got = where_gt0(torch.tensor(z, device="cuda")).cpu().numpy()
+    np.testing.assert_array_equal(got, np.argwhere(z > 0))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_syn_fwd_deterministic_is_bit_exact(seed, B):
+    tb, t, _ = _setup(seed=seed)
+    rng = np.random.default_rng(100 + seed)
+    z = _spikes(rng, B, tb.rec.n_cols, 0.05)
+    got = t.forward(torch.tensor(z, device="cuda"), mode="deterministic").cpu().numpy()
+    ref = orc.syn_fwd(tb.rec, z, tb.basis)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("B", [1, 5, 17])
+def test_syn_fwd_event_within_tolerance(B):
+    tb, t, _ = _setup(seed=2)
+    rng = np.random.default_rng(7)
+    z = _spikes(rng, B, tb.rec.n_cols, 0.05)
+    got = t.forward(torch.tensor(z, device="cuda"), mode="event").cpu().numpy()
+    ref = orc.syn_fwd(tb.rec, z, tb.basis)
+    scale = dense.syn_fwd_abs(tb.rec, z, tb.basis)
+    assert np.max(np.abs(got - ref) - 1e-5 * scale) <= 1e-6
+    exact = dense.syn_fwd_f64(tb.rec, z, tb.basis)
+    assert np.max(np.abs(got - exact) - 1e-5 * scale) <= 1e-6
+
+
+def test_syn_fwd_counts_scale_weights():
+    """Background form: events carry a count and the weight is scaled by it."""
+    tb, t, _ = _setup(seed=3)
+    rng = np.random.default_rng(9)
+    z = rng.poisson(0.3, (2, tb.rec.n_cols)).astype(np.float32)
+    for mode in ("deterministic", "event"):
+        got = t.forward(torch.tensor(z, device="cuda"), counts=True, mode=mode).cpu().numpy()
+        ref = orc.syn_fwd(tb.rec, z, tb.basis, use_count=True)
+        if mode == "deterministic":
+            np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+        else:
+            scale = dense.syn_fwd_abs(tb.rec, z, tb.basis, use_count=True)
+            assert np.max(np.abs(got - ref) - 1e-5 * scale) <= 1e-6
+
+
+@pytest.mark.parametrize("B", [1, 5, 9])
+def test_syn_bwd_matches_oracle(B):
+    tb, t, _ = _setup(seed=4)
+    rng = np.random.default_rng(11)
+    z = _spikes(rng, B, tb.rec.n_cols, 0.05)
+    dy = rng.normal(0, 1, (B * tb.n_neurons, tb.n_basis)).astype(np.float32)
+    dz, dw = t.backward(torch.tensor(z, device="cuda"), torch.tensor(dy, device="cuda"))
+    dz, dw = dz.cpu().numpy(), dw.cpu().numpy()
+    rdz, rdw = orc.syn_bwd(tb.rec, z, tb.basis, dy)
+    dz64, dw64, dz_abs, dw_abs = dense.syn_bwd_f64(tb.rec, z, tb.basis, dy)
+    for got, ref, ex, sc, what in ((dz, rdz, dz64, dz_abs, "dz"), (dw, rdw, dw64, dw_abs, "dW")):
+        assert np.max(np.abs(got - ref) - 1e-5 * sc) <= 1e-6, what
+        assert np.max(np.abs(got - ex) - 1e-5 * sc) <= 1e-6, what
+
+
+def test_calculate_synaptic_currents_autograd():
+    from v1_glif_model_amd.ops import calculate_synaptic_currents, make_pre_ind_table
+    cfg = tiny_config()
+    net, tb = network(cfg, seed=5, dense_basis=True)
+    pre = make_pre_ind_table(tb.rec.indices, n_source_neurons=tb.rec.n_cols)
+    rng = np.random.default_rng(3)
+    B = 4
+    z = torch.tensor(_spikes(rng, B, tb.rec.n_cols, 0.05), device="cuda", requires_grad=True)
+    w = torch.tensor(tb.rec.weight, device="cuda", requires_grad=True)
+    basis = torch.tensor(tb.basis)
+    I = calculate_synaptic_currents(z, tb.rec.indices, w, w, (tb.n_neurons, tb.rec.n_cols), basis,
+                                    tb.rec.syn_id, pre)
+    dy = torch.tensor(rng.normal(0, 1, tuple(I.shape)).astype(np.float32), device="cuda")
+    (I * dy).sum().backward()
+    ref_I = orc.syn_fwd(tb.rec, z.detach().cpu().numpy(), tb.basis)
+    scale = dense.syn_fwd_abs(tb.rec, z.detach().cpu().numpy(), tb.basis)
+    assert np.max(np.abs(I.detach().cpu().numpy() - ref_I) - 1e-5 * scale) <= 1e-6
+    rdz, rdw = orc.syn_bwd(tb.rec, z.detach().cpu().numpy(), tb.basis, dy.cpu().numpy())
+    _, _, dz_abs, dw_abs = dense.syn_bwd_f64(tb.rec, z.detach().cpu().numpy(), tb.basis, dy.cpu().numpy())
+    assert np.max(np.abs(z.grad.cpu().numpy() - rdz) - 1e-5 * dz_abs) <= 1e-6
+    assert np.max(np.abs(w.grad.cpu().numpy() - rdw) - 1e-5 * dw_abs) <= 1e-6

@@ -1,0 +1,275 @@
+"""Pins of the CPU oracle (no GPU).
+
+The reference ships no tests or golden vectors, so every oracle function is pinned
+here against something that does not share its code:
+  * CSR build      == the reference's own numpy fallback (models.py:360-365), bit for bit;
+  * compaction     == np.argwhere (same row-major order as tf.where), bit for bit;
+  * op forward     == float64 brute force within the fp32 bound; linearity, zero
+                      input, identity-basis routing;
+  * op backward    == float64 brute force; adjoint identity <dy, I(z)> = <dz, z>;
+                      exact directional derivative in W;
+  * GLIF step      == closed forms (membrane decay, alpha PSC, ASC decay,
+                      refractory counts, strict threshold);
+  * BPTT           == float64 PyTorch autograd restatement of V1Column.call.
+A planted mistake in any of these formulas fails at least one test.
+"""
+import copy
+import dataclasses
+
+import numpy as np
+import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from oracle import cpu as orc
+from oracle import dense
+from tests.helpers import network, tiny_config
+from v1_glif_model_amd import synthetic as sy
+
+
+# ---------------------------------------------------------------- A1 -------
+@settings(max_examples=60, deadline=None)
+@given(st.integers(1, 50), st.lists(st.integers(0, 49), max_size=300))
+def test_csr_build_matches_reference_numpy_fallback(n_cols, cols):
+    cols = np.array([c % n_cols for c in cols], dtype=np.int64)
+    o, r = orc.csr_build(cols, n_cols)
+    eo, er = dense.csr_build_numpy(cols, n_cols)
+    np.testing.assert_array_equal(o, eo)
+    np.testing.assert_array_equal(r, er)
+
+
+def test_csr_build_edge_cases():
+    o, r = orc.csr_build(np.zeros(0, np.int64), 4)           # S = 0: all columns empty
+    assert o.size == 0 and np.array_equal(r, np.zeros(5))
+    o, r = orc.csr_build(np.full(7, 2), 3)                    # one populated column
+    np.testing.assert_array_equal(o, np.arange(7))
+    np.testing.assert_array_equal(r, [0, 0, 0, 7])
+    with pytest.raises(ValueError, match="out of bounds"):
+        orc.csr_build(np.array([0, 3]), 3)                    # max id + 1
+    with pytest.raises(ValueError, match="out of bounds"):
+        orc.csr_build(np.array([-1]), 3)
+    with pytest.raises(ValueError, match="must be > 0"):
+        orc.csr_build(np.array([0]), 0)
+
+
+# ---------------------------------------------------------------- A3 -------
+@pytest.mark.parametrize("shape,p", [((1, 1), 1.0), ((3, 100), 0.1), ((5, 1000), 0.01), ((2, 0), 0.5)])
+def test_where_matches_argwhere(shape, p):
+    rng = np.random.default_rng(shape[1])
+    z = (rng.random(shape) < p).astype(np.float32)
+    np.testing.assert_array_equal(orc.where_gt0(z), np.argwhere(z > 0))
+
+
+# ------------------------------------------------------------- A4-A6 -------
+def _op_case(seed=0, B=3, p=0.05, dense_basis=True):
+    cfg = tiny_config()
+    _, tb = network(cfg, seed=seed, dense_basis=dense_basis)
+    rng = np.random.default_rng(seed + 10)
+    z = (rng.random((B, tb.rec.n_cols)) < p).astype(np.float32)
+    return tb, z, rng
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_syn_fwd_matches_float64_bruteforce(seed):
+    tb, z, _ = _op_case(seed)
+    got = orc.syn_fwd(tb.rec, z, tb.basis)
+    exact = dense.syn_fwd_f64(tb.rec, z, tb.basis)
+    scale = dense.syn_fwd_abs(tb.rec, z, tb.basis)
+    assert np.all(np.abs(got - exact) <= 1e-6 * scale + 1e-12)
+
+
+def test_syn_fwd_counts_match_bruteforce():
+    tb, _, rng = _op_case(3)
+    z = rng.poisson(0.3, (2, tb.rec.n_cols)).astype(np.float32)
+    got = orc.syn_fwd(tb.rec, z, tb.basis, use_count=True)
+    exact = dense.syn_fwd_f64(tb.rec, z, tb.basis, use_count=True)
+    scale = dense.syn_fwd_abs(tb.rec, z, tb.basis, use_count=True)
+    assert np.all(np.abs(got - exact) <= 1e-6 * scale + 1e-12)
+    # a count of 2 is two events of 1 (linearity in the count)
+    z1 = np.minimum(z, 1.0)
+    two = orc.syn_fwd(tb.rec, 2 * z1, tb.basis, use_count=True)
+    one = orc.syn_fwd(tb.rec, z1, tb.basis, use_count=True)
+    np.testing.assert_allclose(two, 2 * one, rtol=1e-6, atol=1e-9)
+
+
+def test_syn_fwd_invariants():
+    tb, z, rng = _op_case(4, dense_basis=False)
+    # zero input -> zero current
+    assert not np.any(orc.syn_fwd(tb.rec, np.zeros_like(z), tb.basis))
+    # identity basis: one synapse routes to exactly its syn_id receptor, value w
+    one = copy.deepcopy(tb.rec)
+    k = 17
+    zz = np.zeros((1, tb.rec.n_cols), np.float32)
+    zz[0, one.col[k]] = 1.0
+    keep = one.col == one.col[k]
+    one.weight = np.where(np.arange(one.n_syn) == k, one.weight, 0).astype(np.float32)
+    I = orc.syn_fwd(one, zz, tb.basis).reshape(tb.n_neurons, tb.n_basis)
+    nz = np.argwhere(I != 0)
+    assert nz.tolist() == [[one.post[k], one.syn_id[k]]] and I[one.post[k], one.syn_id[k]] == one.weight[k]
+    assert keep.sum() >= 1
+    # linearity in W
+    w2 = copy.deepcopy(tb.rec)
+    w2.weight = (tb.rec.weight * 2).astype(np.float32)
+    np.testing.assert_array_equal(orc.syn_fwd(w2, z, tb.basis), 2 * orc.syn_fwd(tb.rec, z, tb.basis))
+
+
+# ------------------------------------------------------------- A7-A8 -------
+@pytest.mark.parametrize("seed", [0, 1])
+def test_syn_bwd_matches_float64_bruteforce(seed):
+    tb, z, rng = _op_case(seed)
+    dy = rng.normal(0, 1, (z.shape[0] * tb.n_neurons, tb.n_basis)).astype(np.float32)
+    dz, dw = orc.syn_bwd(tb.rec, z, tb.basis, dy)
+    dz64, dw64, dza, dwa = dense.syn_bwd_f64(tb.rec, z, tb.basis, dy)
+    assert np.all(np.abs(dz - dz64) <= 1e-6 * dza + 1e-12)
+    assert np.all(np.abs(dw - dw64) <= 1e-6 * dwa + 1e-12)
+
+
+def test_syn_bwd_adjoint_identity_and_directional_derivative():
+    tb, z, rng = _op_case(5)
+    B = z.shape[0]
+    dy = rng.normal(0, 1, (B * tb.n_neurons, tb.n_basis))
+    # <dy, I(z)> = <dz, z> for binary z: the spike gradient is the adjoint of the op
+    I64 = dense.syn_fwd_f64(tb.rec, z, tb.basis)
+    dz, dw = orc.syn_bwd(tb.rec, z, tb.basis, dy.astype(np.float32))
+    lhs = float(np.sum(dy * I64))
+    rhs = float(np.sum(dz.astype(np.float64) * z))
+    assert abs(lhs - rhs) <= 1e-5 * (np.sum(np.abs(dy) * dense.syn_fwd_abs(tb.rec, z, tb.basis)) + 1e-12)
+    # <dy, I(W + eps d)> - <dy, I(W)> = eps <dW, d>  (the op is linear in W)
+    d = rng.normal(0, 1, tb.rec.n_syn)
+    eps = 0.5
+    w2 = copy.deepcopy(tb.rec)
+    w2.weight = tb.rec.weight.astype(np.float64) + eps * d
+    lhs = float(np.sum(dy * dense.syn_fwd_f64(w2, z, tb.basis)) - lhs * 0 - np.sum(dy * I64))
+    rhs = eps * float(np.dot(dw.astype(np.float64), d))
+    assert abs(lhs - rhs) <= 1e-5 * (abs(lhs) + 1e-9) + 1e-6
+
+
+# ----------------------------------------------------------- GLIF step -----
+def _isolated_cell(N=4, nb=3, D=2, **kw):
+    """A cell whose tables hold a single LGN synapse; everything else silent."""
+    cfg = dataclasses.replace(tiny_config(n=N, fanin=1, delays=D, n_lgn=1, lgn_fanin=1, n_bkg=1,
+                                          bkg_fanin=1), n_basis=nb, n_syn_types=nb)
+    net, tb = network(cfg, seed=3)
+    tb.rec.weight[:] = 0
+    tb.bkg.weight[:] = 0
+    return tb
+
+
+def test_membrane_decays_geometrically_without_input():
+    tb = _isolated_cell()
+    tb.lgn.weight[:] = 0
+    oc = orc.OracleCell(tb)
+    st = oc.zero_state(1)
+    st["v"][:] = 0.7
+    T = 12
+    _, v, _, _ = oc.forward(np.zeros((T, 1, 1), np.uint8), np.zeros((T, 1, 1), np.uint8), state=st)
+    for n in range(tb.n_neurons):
+        expect = 0.7 * tb.decay[n].astype(np.float64) ** np.arange(1, T + 1)
+        np.testing.assert_allclose(v[:, 0, n], expect, rtol=2e-6)
+
+
+def test_psc_is_the_sampled_alpha_function():
+    """One unit impulse into basis r: R_k = p0 sd^k, P_k = k dt p0 sd^k (peak 1 at tau)."""
+    tb = _isolated_cell(nb=3)
+    nb = tb.n_basis
+    post = int(tb.lgn.post[0])
+    w = 1.0
+    for r in range(nb):
+        tb2 = copy.deepcopy(tb)
+        tb2.basis = np.eye(nb, dtype=np.float32)
+        tb2.lgn.weight = np.where(tb2.lgn.post == post, np.float32(w), np.float32(0)).astype(np.float32)
+        tb2.lgn.syn_id[:] = r
+        oc = orc.OracleCell(tb2)
+        T = 40
+        x = np.zeros((T, 1, 1), np.uint8)
+        x[0, 0, 0] = 1
+        st = oc.zero_state(1)
+        traces = []
+        for t in range(T):
+            _, _, _, st = oc.forward(x[t:t + 1], np.zeros((1, 1, 1), np.uint8), state=st)
+            traces.append((st["psc_rise"][0, post * nb + r], st["psc"][0, post * nb + r]))
+        Rk, Pk = np.array(traces).T
+        k = np.arange(T)
+        p0, sd = np.float64(tb.psc_initial[r]), np.float64(tb.syn_decay[r])
+        np.testing.assert_allclose(Rk, p0 * sd ** k, rtol=1e-5)
+        np.testing.assert_allclose(Pk, k * tb.dt * p0 * sd ** k, rtol=1e-5, atol=1e-12)
+        tau = -tb.dt / np.log(sd)
+        if tau < T - 2:
+            # alpha(t) = (e / tau) t exp(-t / tau) peaks at 1 when t = tau
+            assert abs(np.max(Pk) - 1.0) < 0.05
+
+
+def test_refractory_counter_and_asc_after_a_forced_spike():
+    tb = _isolated_cell(N=3)
+    tb.lgn.weight[:] = 0
+    tb.t_ref_steps[:] = [1, 2, 5]
+    oc = orc.OracleCell(tb)
+    st = oc.zero_state(1)
+    st["zbuf"][0, :tb.n_neurons] = 1.0     # every neuron spiked at t = -1
+    st["v"][:] = 0.2
+    T = 8
+    z, v, ref, st2 = oc.forward(np.zeros((T, 1, 1), np.uint8), np.zeros((T, 1, 1), np.uint8), state=st)
+    # r_0 = max(0 + 1 * tref - 1, 0); then counts down by one per step
+    for n, tr in enumerate([1, 2, 5]):
+        expect = [max(tr - 1 - t, 0) > 0 for t in range(T)]
+        np.testing.assert_array_equal(ref[:, 0, n].astype(bool), expect)
+    # soft reset: V_0 = decay * 0.2 + 0 - 1
+    np.testing.assert_allclose(v[0, 0], tb.decay * np.float32(0.2) - 1.0, rtol=1e-6)
+    # ASC: A_0 = amp, then A_t = ad^t amp
+    # (the step reads the old ASC into c, so check the state after T steps)
+    expect = tb.asc_amps.astype(np.float64) * tb.asc_decay.astype(np.float64) ** (T - 1)
+    np.testing.assert_allclose(st2["asc"][0].reshape(-1, 2), expect, rtol=1e-5)
+
+
+def test_threshold_is_strict():
+    tb = _isolated_cell(N=2)
+    tb.lgn.weight[:] = 0
+    tb.decay[:] = 1.0
+    tb.current_factor[:] = 0.0
+    oc = orc.OracleCell(tb)
+    st = oc.zero_state(1)
+    st["v"][0] = [1.0, np.nextafter(np.float32(1.0), np.float32(2.0))]
+    z, _, _, _ = oc.forward(np.zeros((1, 1, 1), np.uint8), np.zeros((1, 1, 1), np.uint8), state=st)
+    assert z[0, 0].tolist() == [0, 1]
+
+
+# ----------------------------------------------------------------- BPTT ----
+@pytest.mark.parametrize("pseudo_gauss,hard_reset,rd,vgd", [
+    (True, False, 0.5, 0.5), (False, False, 0.5, 0.5), (True, True, 0.5, 0.5),
+    (True, False, 0.2, 0.0), (False, False, 1.0, 0.3)])
+def test_bptt_matches_autograd_restatement(pseudo_gauss, hard_reset, rd, vgd):
+    torch = pytest.importorskip("torch")
+    torch.set_num_threads(4)
+    from oracle import torch_ref
+    cfg = tiny_config(n=120, fanin=20, n_lgn=40, rs=2.0, ins=3.0)
+    _, tb = network(cfg, seed=1, dense_basis=True)
+    T, B = 30, 2
+    lgn, bkg = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
+    kw = dict(pseudo_gauss=pseudo_gauss, hard_reset=hard_reset, rd=rd, vgd=vgd, gauss_std=0.5, damp=0.5)
+    oc = orc.OracleCell(tb, **kw)
+    z, v, ref, _ = oc.forward(lgn, bkg)
+    assert z.sum() > 0
+    rng = np.random.default_rng(5)
+    gz = rng.normal(0, 1, z.shape).astype(np.float32)
+    gv = rng.normal(0, 0.1, z.shape).astype(np.float32)
+    og = oc.backward(lgn, bkg, z, ref, v, gz_loss=gz, gv_loss=gv)
+    tg, tv = torch_ref.bptt(tb, lgn, bkg, z, gz, gv, **kw)
+    assert np.max(np.abs(tv - v)) < 1e-5
+    for k in ("rec", "lgn", "bkg"):
+        scale = np.max(np.abs(tg[k]))
+        assert scale > 0
+        assert np.max(np.abs(og[k] - tg[k])) <= 1e-5 * scale, k
+
+
+def test_bptt_per_neuron_loss_gradient_equals_dense():
+    cfg = tiny_config(n=100, fanin=15, n_lgn=30, rs=2.0)
+    _, tb = network(cfg, seed=2, dense_basis=True)
+    T, B = 20, 2
+    lgn, bkg = sy.make_inputs(cfg, seed=2, seq_len=T, batch=B)
+    oc = orc.OracleCell(tb)
+    z, v, ref, _ = oc.forward(lgn, bkg)
+    gn = np.random.default_rng(1).normal(0, 1, tb.n_neurons).astype(np.float32)
+    a = oc.backward(lgn, bkg, z, ref, v, gz_neuron=gn)
+    b = oc.backward(lgn, bkg, z, ref, v, gz_loss=np.broadcast_to(gn, z.shape).copy())
+    for k in a:
+        np.testing.assert_array_equal(a[k], b[k])

@@ -1,0 +1,904 @@
+// The GLIF_3 cell over T steps (V1Column.call, models.py:1059-1135) and its BPTT.
+//
+// Forward, per step t (one stream, no host round trip):
+//   event mode:   k_push(t)   rec spikes of steps t-1..t-D (ring of active lists)
+//                             and the step's LGN (column, batch-mask) list are
+//                             streamed through the column-grouped tables and added
+//                             into I with fp32 atomics;
+//                 k_step(t)   background pull, GLIF_3 update, spike bits, the
+//                             step's active list; I is re-zeroed after reading.
+//   deterministic: k_step(t)  pulls rec, LGN and background per post row in the
+//                             reference's accumulation order, then the same update.
+// Backward, in windows of Wwin reverse ticks t0, t0-1, .. (lagged adjoint, k_adj):
+//   k_adj         per tick t: gz_t -> gV_t -> gP_{t-1} -> gR_{t-2} -> G_{t-2}
+//   k_bwd_rec     dz of the window's steps t0-2, t0-3, .. over every recurrent
+//                 column (+ dW of active columns), one table pass per window
+//   k_bwd_in      dW of the LGN / background events of the window's steps
+// A window is legal because dz_s depends only on dz_{>= s+3}: a spike reaches the
+// rise current one step later, the PSC the next, the voltage the one after.
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "compact.h"
+#include "glif_internal.h"
+#include "prof.h"
+#include "syn_kernels.h"
+
+namespace glif {
+
+// ------------------------------------------------------------------ state ----
+struct CellWs {
+    float *I;
+    uint64_t *zbits;    // [(T + D)][B][W]   slot t + D holds z_t
+    uint64_t *refbits;  // [T][B][W]         r_t > 0
+    float *vsave;       // [T][B][N]
+    int32_t *rlist;     // [(D + 1)][B * N]  active (b << 24 | n) of step s in slot (s + D) % (D + 1)
+    int32_t *rcount;    // [D + 1]
+    int64_t *lgn_off;   // [T + 1]           per-step LGN (column, batch-mask) lists
+    int32_t *lgn_pre;   // [T * n_lgn]
+    uint32_t *lgn_mask;
+    int64_t *lw_off;    // [n_win + 1]       per-backward-window LGN lists
+    int32_t *lw_pre;
+    uint32_t *lw_mask;
+    int64_t *kw_off;    // [n_win + 1]       per-backward-window background lists
+    int32_t *kw_pre;
+    uint32_t *kw_mask;
+    uint8_t *bkg_cnt;   // [T][B][n_bkg]
+    void *scratch;
+    float *dZ;          // [ring][B][D * N]
+    float *G;           // [n_types][N][R]
+    float *gV;          // [B][N]
+    float *gP, *gR;     // [nb][B][N]
+    float *dw_rec;      // type-phased order
+    float *dw_lgn, *dw_bkg;  // column-grouped order
+};
+
+// Backward window width (reverse ticks per table pass) and G row length.
+static int win_width(int B) { return 3 * B <= 16 ? 3 : 1; }
+static int n_windows(int T, int Wwin) { return T >= 3 ? (T - 2 + Wwin - 1) / Wwin : 0; }
+static int ring_size(const Cell *c) { return c->D + 6; }
+
+static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *bytes) {
+    Carver cv(ws, SIZE_MAX);
+    CellWs w{};
+    const int64_t BN = static_cast<int64_t>(B) * c->N;
+    const int64_t nl = c->lgn->n_cols, nk = c->bkg->n_cols;
+    w.I = cv.take<float>(BN * c->nb);
+    w.zbits = cv.take<uint64_t>(static_cast<size_t>(T + c->D) * B * c->W);
+    w.refbits = cv.take<uint64_t>(static_cast<size_t>(T) * B * c->W);
+    w.vsave = cv.take<float>(static_cast<size_t>(T) * BN);
+    w.rlist = cv.take<int32_t>(static_cast<size_t>(c->D + 1) * BN);
+    w.rcount = cv.take<int32_t>(c->D + 1);
+    w.lgn_off = cv.take<int64_t>(T + 1);
+    w.lgn_pre = cv.take<int32_t>(static_cast<size_t>(T) * nl);
+    w.lgn_mask = cv.take<uint32_t>(static_cast<size_t>(T) * nl);
+    const int Wwin = win_width(B), nwin = std::max(n_windows(T, Wwin), 1);
+    w.lw_off = cv.take<int64_t>(nwin + 1);
+    w.lw_pre = cv.take<int32_t>(static_cast<size_t>(nwin) * nl);
+    w.lw_mask = cv.take<uint32_t>(static_cast<size_t>(nwin) * nl);
+    w.kw_off = cv.take<int64_t>(nwin + 1);
+    w.kw_pre = cv.take<int32_t>(static_cast<size_t>(nwin) * nk);
+    w.kw_mask = cv.take<uint32_t>(static_cast<size_t>(nwin) * nk);
+    w.bkg_cnt = cv.take<uint8_t>(static_cast<size_t>(T) * B * nk);
+    w.scratch = cv.take<char>(std::max(compact_scratch_bytes(T, nl), compact_scratch_bytes(T, nk)));
+    w.dZ = cv.take<float>(static_cast<size_t>(ring_size(c)) * B * c->D * c->N);
+    w.G = cv.take<float>(static_cast<size_t>(c->N) * c->n_types * g_row(Wwin, B));
+    w.gV = cv.take<float>(BN);
+    w.gP = cv.take<float>(BN * c->nb);
+    w.gR = cv.take<float>(BN * c->nb);
+    w.dw_rec = cv.take<float>(std::max<int64_t>(c->rec->n_syn, 1));
+    w.dw_lgn = cv.take<float>(std::max<int64_t>(c->lgn->n_syn, 1));
+    w.dw_bkg = cv.take<float>(std::max<int64_t>(c->bkg->n_syn, 1));
+    if (bytes) *bytes = cv.off;
+    return w;
+}
+
+static CellConst make_const(const Cell *c, int B) {
+    CellConst k{};
+    k.N = c->N;
+    k.Np = c->Np;
+    k.W = c->W;
+    k.D = c->D;
+    k.nb = c->nb;
+    k.n_types = c->n_types;
+    k.B = B;
+    k.Bp = batch_pad(B);
+    k.lr = c->cfg.lr_scale;
+    float vgd = std::min(1.0f, std::max(0.0f, c->cfg.voltage_gradient_dampening));
+    k.vgd = vgd;
+    k.om = 1.0f - vgd;
+    float rd = std::min(1.0f, std::max(0.0f, c->cfg.recurrent_dampening));
+    // straight_through_dampen(z_buf, 1 - rd) scales the spike-buffer gradient by 1 - (1 - rd)
+    k.rd_scale = 1.0f - (1.0f - rd);
+    k.gauss_std = c->cfg.gauss_std;
+    k.damp = c->cfg.dampening_factor;
+    k.dt = c->cfg.dt;
+    k.pseudo_gauss = c->cfg.pseudo_gauss;
+    k.hard_reset = c->cfg.hard_reset;
+    for (int q = 0; q < c->nb; ++q) {
+        k.sd[q] = c->syn_decay[q];
+        k.p0[q] = c->psc_initial[q];
+        k.dtsd[q] = c->dtsd[q];
+    }
+    return k;
+}
+
+__device__ inline int ring_slot(int s, int D) { return (s + D) % (D + 1); }
+
+__device__ inline bool zbit(const uint64_t *zbits, int slot, int b, int B, int W, int n) {
+    return (zbits[(static_cast<int64_t>(slot) * B + b) * W + (n >> 6)] >> (n & 63)) & 1ull;
+}
+
+// ---------------------------------------------------------- history init ----
+// z_buf [B][D*N] (slot d-1 = z_{-d}) -> spike bits (slot D-d) and, in event mode,
+// the active lists of steps -1..-D.
+__global__ void __launch_bounds__(kBlock)
+    k_init_history(const float *__restrict__ z_buf, CellConst k, uint64_t *__restrict__ zbits,
+                   int32_t *__restrict__ rlist, int32_t *__restrict__ rcount, int event) {
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t per_slot = static_cast<int64_t>(k.B) * k.Np;
+    if (gt >= per_slot * k.D) return;
+    const int d = static_cast<int>(gt / per_slot) + 1;
+    const int b = static_cast<int>((gt % per_slot) / k.Np);
+    const int n = static_cast<int>(gt % k.Np);
+    const int lane = threadIdx.x & (kWave - 1);
+    bool z = n < k.N && z_buf[static_cast<int64_t>(b) * k.D * k.N + static_cast<int64_t>(d - 1) * k.N + n] > 0.0f;
+    const uint64_t bits = __ballot(z);
+    const int slot = k.D - d;
+    if (lane == 0) zbits[(static_cast<int64_t>(slot) * k.B + b) * k.W + (n >> 6)] = bits;
+    if (event) {
+        int base = 0;
+        if (lane == 0 && bits) base = atomicAdd(&rcount[slot], __popcll(bits));
+        base = __shfl(base, 0, kWave);
+        if (z) {
+            const int rank = __popcll(bits & ((1ull << lane) - 1ull));
+            rlist[static_cast<int64_t>(slot) * k.B * k.N + base + rank] = (b << 24) | n;
+        }
+    }
+}
+
+// z_buf out = [z_{T-1}, ..., z_{T-D}].
+__global__ void __launch_bounds__(kBlock)
+    k_write_zbuf(float *__restrict__ z_buf, CellConst k, int T, const uint64_t *__restrict__ zbits) {
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t per_slot = static_cast<int64_t>(k.B) * k.N;
+    if (gt >= per_slot * k.D) return;
+    const int d = static_cast<int>(gt / per_slot) + 1;
+    const int b = static_cast<int>((gt % per_slot) / k.N);
+    const int n = static_cast<int>(gt % k.N);
+    const bool z = zbit(zbits, T - d + k.D, b, k.B, k.W, n);
+    z_buf[static_cast<int64_t>(b) * k.D * k.N + static_cast<int64_t>(d - 1) * k.N + n] = z ? 1.0f : 0.0f;
+}
+
+// ------------------------------------------------------------ event push ----
+struct PushArgs {
+    int32_t t, D, N, B, nb, n_types, chunks_rec, chunks_lgn;
+    const int32_t *rlist;
+    int32_t *rcount;
+    const int32_t *rec_colptr;
+    const uint32_t *rec_ps;
+    const float *rec_w;
+    const int64_t *lgn_off;
+    const int32_t *lgn_pre;
+    const uint32_t *lgn_mask;
+    const int32_t *lgn_colptr;
+    const uint32_t *lgn_ps;
+    const float *lgn_w;
+    const float *basis;
+    float *I;
+};
+
+// Work units: (item, chunk).  Items are the spikes of steps t-1..t-D (each one
+// column of the recurrent table) followed by the step's LGN columns.  A chunk is
+// L * kChunkIters synapses of the item's column, so long columns spread over
+// several sub-waves.
+constexpr int kChunkIters = 4;
+
+template <int L>
+__global__ void __launch_bounds__(kBlock) k_push(PushArgs a) {
+    extern __shared__ float basis_lds[];
+    load_basis_lds(basis_lds, a.basis, a.n_types * a.nb);
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.rcount[ring_slot(a.t, a.D)] = 0;
+    int64_t n_rec = 0;
+    for (int d = 1; d <= a.D; ++d) n_rec += a.rcount[ring_slot(a.t - d, a.D)];
+    const int64_t l0 = a.lgn_off[a.t], n_lgn = a.lgn_off[a.t + 1] - l0;
+    const int64_t units = n_rec * a.chunks_rec + n_lgn * a.chunks_lgn;
+    const int lane_s = threadIdx.x % L;
+    const int64_t n_subs = static_cast<int64_t>(gridDim.x) * blockDim.x / L;
+    const int64_t BN = static_cast<int64_t>(a.B) * a.N;
+    for (int64_t u = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / L; u < units;
+         u += n_subs) {
+        if (u < n_rec * a.chunks_rec) {
+            int64_t it = u / a.chunks_rec;
+            const int ch = static_cast<int>(u % a.chunks_rec);
+            int d = 1;
+            for (; d <= a.D; ++d) {
+                const int64_t c = a.rcount[ring_slot(a.t - d, a.D)];
+                if (it < c) break;
+                it -= c;
+            }
+            const int32_t e = a.rlist[static_cast<int64_t>(ring_slot(a.t - d, a.D)) * BN + it];
+            const int b = e >> 24;
+            const int32_t col = (e & static_cast<int32_t>(kLow24)) + (d - 1) * a.N;
+            const int32_t lo = a.rec_colptr[col] + ch * L * kChunkIters;
+            const int32_t hi = min(a.rec_colptr[col + 1], lo + L * kChunkIters);
+            push_column<L>(lane_s, lo, hi, 1u << b, MultOne{}, a.rec_ps, a.rec_w, basis_lds, a.nb, a.N,
+                           a.I);
+        } else {
+            const int64_t v = u - n_rec * a.chunks_rec;
+            const int64_t it = l0 + v / a.chunks_lgn;
+            const int ch = static_cast<int>(v % a.chunks_lgn);
+            const int32_t c = a.lgn_pre[it];
+            const int32_t lo = a.lgn_colptr[c] + ch * L * kChunkIters;
+            const int32_t hi = min(a.lgn_colptr[c + 1], lo + L * kChunkIters);
+            push_column<L>(lane_s, lo, hi, a.lgn_mask[it], MultOne{}, a.lgn_ps, a.lgn_w, basis_lds,
+                           a.nb, a.N, a.I);
+        }
+    }
+}
+
+// ------------------------------------------------------------- GLIF step ----
+struct StepArgs {
+    CellConst k;
+    int32_t t;
+    float *v;
+    int16_t *r;
+    float *asc;
+    float *R;
+    float *P;
+    const float *decay, *cf, *ad, *amp;
+    const int32_t *tref;
+    float *I;
+    uint64_t *zbits;
+    uint64_t *refbits;
+    float *vsave;
+    float *z_out, *v_out;
+    int32_t *spike_count;
+    int32_t *rlist, *rcount;
+    const int32_t *rec_row;
+    const uint32_t *rec_pd;
+    const uint8_t *rec_sid;
+    const float *rec_w;
+    const int32_t *lgn_row;
+    const uint32_t *lgn_pd;
+    const uint8_t *lgn_sid;
+    const float *lgn_w;
+    const uint8_t *lgn_x;  // [B][n_lgn] of step t
+    int32_t n_lgn;
+    const int32_t *bkg_row;
+    const uint32_t *bkg_pd;
+    const uint8_t *bkg_sid;
+    const float *bkg_w;
+    const uint8_t *bkg_x;  // [B][n_bkg] of step t
+    int32_t n_bkg;
+    const float *basis;
+};
+
+// One GLIF_3 update per thread (b, n), models.py:979-1028 and 1059-1135:
+//   I      = ((I_rec + I_lgn) + I_bkg) * lr_scale
+//   R'     = R * sd + I * p0                P' = P * sd + (dt * sd) * R
+//   A'     = ad * A + z_prev * amp          c  = sum_r P + (A_0 + A_1)   (old P, A)
+//   V'     = (decay * (V * (1 - vgd) + V * vgd) + cf * c) - z_prev
+//   r'     = max(r + z_prev * tref - 1, 0); hard reset: V' = 0 while r' > 0
+//   z      = r' > 0 ? 0 : (V' - 1 > 0)
+template <bool DET>
+__global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
+    extern __shared__ float basis_lds[];
+    const CellConst &k = a.k;
+    load_basis_lds(basis_lds, a.basis, k.n_types * k.nb);
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gt >= static_cast<int64_t>(k.B) * k.Np) return;  // whole waves only (Np % 64 == 0)
+    const int b = static_cast<int>(gt / k.Np);
+    const int n = static_cast<int>(gt % k.Np);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nb = k.nb;
+    const int t = a.t;
+    bool spike = false, refr = false;
+    if (n < k.N) {
+        const int64_t bn = static_cast<int64_t>(b) * k.N + n;
+        float Irl[kMaxBasis], Ib[kMaxBasis];
+        for (int q = 0; q < nb; ++q) Ib[q] = 0.0f;
+        if (DET) {
+            float Ir[kMaxBasis], Il[kMaxBasis];
+            for (int q = 0; q < nb; ++q) Ir[q] = Il[q] = 0.0f;
+            for (int32_t j = a.rec_row[n], je = a.rec_row[n + 1]; j < je; ++j) {
+                const uint32_t q = a.rec_pd[j];
+                const int d = static_cast<int>(q >> 24) + 1;
+                if (!zbit(a.zbits, t - d + k.D, b, k.B, k.W, static_cast<int>(q & kLow24))) continue;
+                const float wv = a.rec_w[j];
+                const float *bs = basis_lds + a.rec_sid[j] * nb;
+                for (int r = 0; r < nb; ++r) Ir[r] = Ir[r] + wv * bs[r];
+            }
+            const uint8_t *xl = a.lgn_x + static_cast<int64_t>(b) * a.n_lgn;
+            for (int32_t j = a.lgn_row[n], je = a.lgn_row[n + 1]; j < je; ++j) {
+                if (xl[a.lgn_pd[j] & kLow24] == 0) continue;
+                const float wv = a.lgn_w[j];
+                const float *bs = basis_lds + a.lgn_sid[j] * nb;
+                for (int r = 0; r < nb; ++r) Il[r] = Il[r] + wv * bs[r];
+            }
+            for (int q = 0; q < nb; ++q) Irl[q] = Ir[q] + Il[q];
+        } else {
+            float *Ip = a.I + bn * nb;
+            for (int q = 0; q < nb; ++q) {
+                Irl[q] = Ip[q];
+                Ip[q] = 0.0f;
+            }
+        }
+        const uint8_t *xb = a.bkg_x + static_cast<int64_t>(b) * a.n_bkg;
+        for (int32_t j = a.bkg_row[n], je = a.bkg_row[n + 1]; j < je; ++j) {
+            const uint8_t cnt = xb[a.bkg_pd[j] & kLow24];
+            if (cnt == 0) continue;
+            const float wv = a.bkg_w[j] * static_cast<float>(cnt);
+            const float *bs = basis_lds + a.bkg_sid[j] * nb;
+            for (int r = 0; r < nb; ++r) Ib[r] = Ib[r] + wv * bs[r];
+        }
+
+        const float zp = zbit(a.zbits, t - 1 + k.D, b, k.B, k.W, n) ? 1.0f : 0.0f;
+        float *Rp = a.R + bn * nb;
+        float *Pp = a.P + bn * nb;
+        float *Ap = a.asc + bn * 2;
+        float Pold[kMaxBasis];
+        for (int q = 0; q < nb; ++q) Pold[q] = Pp[q];
+        float sumP = Pold[0];
+        for (int q = 1; q < nb; ++q) sumP = sumP + Pold[q];
+        const float A0 = Ap[0], A1 = Ap[1];
+        const float c1 = sumP + (A0 + A1);
+        for (int q = 0; q < nb; ++q) {
+            const float in = (Irl[q] + Ib[q]) * k.lr;
+            const float Rold = Rp[q];
+            Rp[q] = Rold * k.sd[q] + in * k.p0[q];
+            Pp[q] = Pold[q] * k.sd[q] + k.dtsd[q] * Rold;
+        }
+        Ap[0] = a.ad[2 * n] * A0 + zp * a.amp[2 * n];
+        Ap[1] = a.ad[2 * n + 1] * A1 + zp * a.amp[2 * n + 1];
+        const float vv = a.v[bn];
+        const float dv = vv * k.om + vv * k.vgd;
+        float vn = (a.decay[n] * dv + a.cf[n] * c1) - zp;
+        int rn = static_cast<int>(a.r[bn]) + static_cast<int>(zp) * a.tref[n] - 1;
+        rn = rn < 0 ? 0 : rn;
+        refr = rn > 0;
+        if (k.hard_reset && refr) vn = 0.0f;
+        spike = !refr && (vn - 1.0f) > 0.0f;
+        a.v[bn] = vn;
+        a.r[bn] = static_cast<int16_t>(rn);
+        const int64_t tbn = static_cast<int64_t>(t) * k.B * k.N + bn;
+        a.vsave[tbn] = vn;
+        if (a.z_out) a.z_out[tbn] = spike ? 1.0f : 0.0f;
+        if (a.v_out) a.v_out[tbn] = vn;
+        if (a.spike_count && spike) a.spike_count[bn] += 1;
+    }
+    const uint64_t zb = __ballot(spike), rb = __ballot(refr);
+    const int64_t word = static_cast<int64_t>(b) * k.W + (n >> 6);
+    if (lane == 0) {
+        a.zbits[static_cast<int64_t>(t + k.D) * k.B * k.W + word] = zb;
+        a.refbits[static_cast<int64_t>(t) * k.B * k.W + word] = rb;
+    }
+    if (!DET) {
+        const int slot = ring_slot(t, k.D);
+        int base = 0;
+        if (lane == 0 && zb) base = atomicAdd(&a.rcount[slot], __popcll(zb));
+        base = __shfl(base, 0, kWave);
+        if (spike) {
+            const int rank = __popcll(zb & ((1ull << lane) - 1ull));
+            a.rlist[static_cast<int64_t>(slot) * k.B * k.N + base + rank] = (b << 24) | n;
+        }
+    }
+}
+
+// --------------------------------------------------------------- adjoint ----
+struct AdjArgs {
+    CellConst k;
+    int32_t t0, nw, T, ring, R;
+    const float *vsave;
+    const uint64_t *refbits;
+    const float *gz, *gz_neuron, *gv;
+    const float *dZ;
+    float *gV, *gP, *gR;
+    const float *decay, *cf;
+    float *G;
+    const float *basis;
+};
+
+// Lagged reverse ticks t = t0, t0-1, .., t0-nw+1 (nw <= window width; every t >= 2).
+// Carried per (b, n): gV'_{t+1}, gP_t, gR_{t-1}.
+//   gz_t   = sum_{d=D..1, t+d <= T-3} rd * dZ_{t+d}[b][(d-1)N + n]  + dL/dz_t
+//   gV_t   = gz_t * psi(V_t - 1) [r_t == 0] + dL/dV_t + (gV'_{t+1} * decay) * (1 - vgd)
+//   gV'_t  = hard_reset && r_t > 0 ? 0 : gV_t
+//   gP_{t-1} = gP_t * sd + gV'_t * cf              (P_{t-1} feeds P_t and V_t)
+//   gR_{t-2} = gR_{t-1} * sd + gP_{t-1} * (dt*sd)  (R_{t-2} feeds R_{t-1} and P_{t-1})
+//   dy_{t-2} = (gR_{t-2} * p0) * lr_scale;  G[s][n][w*B + b] = sum_r dy_r basis[s][r]
+// dZ_s for s >= T-2 is zero (nothing downstream of I_{T-2}, I_{T-1} is observed).
+// The ticks of one window only read dZ of earlier (later-in-time) windows.
+__global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
+    extern __shared__ float basis_lds[];
+    const CellConst &k = a.k;
+    load_basis_lds(basis_lds, a.basis, k.n_types * k.nb);
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t BN = static_cast<int64_t>(k.B) * k.N;
+    if (gt >= BN) return;
+    // batch fastest: neighbouring lanes write neighbouring G entries
+    const int n = static_cast<int>(gt / k.B);
+    const int b = static_cast<int>(gt - static_cast<int64_t>(n) * k.B);
+    const int64_t bn = static_cast<int64_t>(b) * k.N + n;
+    const int nb = k.nb;
+    const int64_t DN = static_cast<int64_t>(k.D) * k.N;
+    float gVc = a.gV[bn];
+    float gP[kMaxBasis], gR[kMaxBasis];
+    for (int q = 0; q < nb; ++q) {
+        gP[q] = a.gP[static_cast<int64_t>(q) * BN + bn];
+        gR[q] = a.gR[static_cast<int64_t>(q) * BN + bn];
+    }
+    const float decay = a.decay[n], cfn = a.cf[n];
+    for (int w = 0; w < a.nw; ++w) {
+        const int t = a.t0 - w;
+        float gz = 0.0f;
+        for (int d = k.D; d >= 1; --d) {
+            const int s = t + d;
+            if (s > a.T - 3) continue;
+            gz = gz + a.dZ[(static_cast<int64_t>(s % a.ring) * k.B + b) * DN + static_cast<int64_t>(d - 1) * k.N + n] *
+                          k.rd_scale;
+        }
+        const int64_t tbn = static_cast<int64_t>(t) * BN + bn;
+        if (a.gz) gz = gz + a.gz[tbn];
+        if (a.gz_neuron) gz = gz + a.gz_neuron[n];
+        const bool refr = (a.refbits[(static_cast<int64_t>(t) * k.B + b) * k.W + (n >> 6)] >> (n & 63)) & 1ull;
+        float psi = 0.0f;
+        if (!refr) {
+            const float vsc = a.vsave[tbn] - 1.0f;
+            if (k.pseudo_gauss) {
+                const float q = -(vsc * vsc) / (k.gauss_std * k.gauss_std);
+                psi = expf(q) * k.damp;
+            } else {
+                const float m = 1.0f - fabsf(vsc);
+                psi = k.damp * (m > 0.0f ? m : 0.0f);
+            }
+        }
+        float gV = gz * psi;
+        if (a.gv) gV = gV + a.gv[tbn];
+        gV = gV + (gVc * decay) * k.om;
+        gVc = (k.hard_reset && refr) ? 0.0f : gV;
+        float dy[kMaxBasis];
+        for (int q = 0; q < nb; ++q) {
+            gP[q] = gP[q] * k.sd[q] + gVc * cfn;
+            gR[q] = gR[q] * k.sd[q] + gP[q] * k.dtsd[q];
+            dy[q] = (gR[q] * k.p0[q]) * k.lr;
+        }
+        const int e = w * k.B + b;
+        for (int s = 0; s < k.n_types; ++s) {
+            const float *bs = basis_lds + s * nb;
+            float g = dy[0] * bs[0];
+            for (int r = 1; r < nb; ++r) g = g + dy[r] * bs[r];
+            a.G[(static_cast<int64_t>(s) * k.N + n) * a.R + e] = g;
+        }
+    }
+    a.gV[bn] = gVc;
+    for (int q = 0; q < nb; ++q) {
+        a.gP[static_cast<int64_t>(q) * BN + bn] = gP[q];
+        a.gR[static_cast<int64_t>(q) * BN + bn] = gR[q];
+    }
+}
+
+// ------------------------------------------------------ backward synapses ----
+// Recurrent activity of element e = w*B + b of column c = pre + N*(d-1) in the
+// window of steps s0, s0-1, ..: the spike z_{s0-w-d}[b][pre] (models.py:128 on the
+// spike buffer of step s0-w); dz of that element goes to the ring slot of step s0-w.
+struct ActWin {
+    const uint64_t *zbits;
+    float *dZ;
+    int64_t n_cols;
+    int32_t s0, B, D, W, n_pre, ring;
+    __device__ bool on(int64_t c, int e) const {
+        const int w = e / B, b = e - w * B;
+        const int d1 = static_cast<int>(c / n_pre);
+        const int pre = static_cast<int>(c - static_cast<int64_t>(d1) * n_pre);
+        return zbit(zbits, s0 - w - (d1 + 1) + D, b, B, W, pre);
+    }
+    __device__ float mult(int64_t, int) const { return 1.0f; }
+    __device__ float *out(int64_t c, int e) const {
+        const int w = e / B, b = e - w * B;
+        return dZ + (static_cast<int64_t>((s0 - w) % ring) * B + b) * n_cols + c;
+    }
+};
+
+template <int LG>
+__global__ void __launch_bounds__(kBlock) k_bwd_rec(ColArgs a, ActWin act) {
+    bwd_cols_lg<LG, 2>(a, act);
+}
+
+struct BwdInArgs {
+    int32_t j, s0, B, R, n_post, chunks;
+    int64_t n_in;
+    const int64_t *off;
+    const int32_t *pre;
+    const uint32_t *mask;
+    const uint8_t *cnt;  // [T][B][n_in] (background counts) or nullptr (spikes)
+    const int32_t *col_ptr;
+    const uint32_t *ps;
+    const float *G;
+    float *dw;           // column-grouped order, accumulated
+};
+
+// dW of one window's input events (A8 for LGN, models.py:814-863 autodiff, and the
+// background source): item (column, mask over w*B + b) -> every synapse k of the
+// column adds G[sid][post][e] * mult for the set elements e in ascending order
+// (reverse time, then batch), the order in which the reference's per-step
+// gradients accumulate.
+template <bool COUNTS>
+__global__ void __launch_bounds__(kBlock) k_bwd_in(BwdInArgs a) {
+    constexpr int L = kWave;
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int lane_s = threadIdx.x % L;
+    const int64_t n_subs = static_cast<int64_t>(gridDim.x) * blockDim.x / L;
+    const int64_t i0 = a.off[a.j], units = (a.off[a.j + 1] - i0) * a.chunks;
+    for (int64_t u = gt / L; u < units; u += n_subs) {
+        const int64_t it = i0 + u / a.chunks;
+        const int ch = static_cast<int>(u % a.chunks);
+        const int32_t c = a.pre[it];
+        const uint32_t m = a.mask[it];
+        const int32_t lo = a.col_ptr[c] + ch * L * kChunkIters;
+        const int32_t hi = min(a.col_ptr[c + 1], lo + L * kChunkIters);
+        for (int32_t k = lo + lane_s; k < hi; k += L) {
+            const uint32_t p = a.ps[k];
+            const float *g = a.G + (static_cast<int64_t>(p >> 24) * a.n_post + (p & kLow24)) * a.R;
+            float d = a.dw[k];
+            uint32_t mm = m;
+            while (mm) {
+                const int e = __ffs(mm) - 1;
+                mm &= mm - 1;
+                if (COUNTS) {
+                    const int w = e / a.B, b = e - w * a.B;
+                    d += g[e] * static_cast<float>(a.cnt[(static_cast<int64_t>(a.s0 - w) * a.B + b) * a.n_in + c]);
+                } else {
+                    d += g[e];
+                }
+            }
+            a.dw[k] = d;
+        }
+    }
+}
+
+// ------------------------------------------------------------ launchers ----
+static void launch_bwd_rec(const ColArgs &ca, const ActWin &act, hipStream_t s) {
+    const int LG = ca.R / 4;
+    const dim3 grid(ceil_div(ca.n_cols * LG, kBlock));
+    if (LG == 1) hipLaunchKernelGGL(k_bwd_rec<1>, grid, dim3(kBlock), 0, s, ca, act);
+    else if (LG == 2) hipLaunchKernelGGL(k_bwd_rec<2>, grid, dim3(kBlock), 0, s, ca, act);
+    else if (LG == 4) hipLaunchKernelGGL(k_bwd_rec<4>, grid, dim3(kBlock), 0, s, ca, act);
+    else hipLaunchKernelGGL(k_bwd_rec<8>, grid, dim3(kBlock), 0, s, ca, act);
+}
+
+static void launch_bwd_in(const BwdInArgs &ia, int64_t max_units, hipStream_t s) {
+    const dim3 grid(grid_subwaves(max_units, kWave));
+    if (ia.cnt)
+        hipLaunchKernelGGL(k_bwd_in<true>, grid, dim3(kBlock), 0, s, ia);
+    else
+        hipLaunchKernelGGL(k_bwd_in<false>, grid, dim3(kBlock), 0, s, ia);
+}
+
+static int chunks_for(const Table *t, int L) {
+    return std::max(1, ceil_div(std::max(t->max_col_len, 1), static_cast<int64_t>(L) * kChunkIters));
+}
+
+}  // namespace glif
+
+using namespace glif;
+
+extern "C" {
+
+int glif_cell_create(const glif_cell_config *cfg, const float *decay, const float *current_factor,
+                     const float *asc_decay, const float *asc_amps, const int32_t *t_ref_steps,
+                     const float *syn_decay, const float *psc_initial, glif_table *rec, glif_table *lgn,
+                     glif_table *bkg, glif_cell **out) {
+    if (!cfg || !out || !rec || !lgn || !bkg || !decay || !current_factor || !asc_decay || !asc_amps ||
+        !t_ref_steps || !syn_decay || !psc_initial)
+        return fail(GLIF_EINVAL, "NULL argument");
+    *out = nullptr;
+    Table *tr = reinterpret_cast<Table *>(rec), *tl = reinterpret_cast<Table *>(lgn),
+          *tb = reinterpret_cast<Table *>(bkg);
+    const int N = cfg->n_neurons, D = cfg->n_delay, nb = cfg->n_basis;
+    if (N <= 0 || N >= (1 << 24)) return fail(GLIF_EINVAL, "n_neurons must be in [1, 2^24)");
+    if (D <= 0 || D > 256) return fail(GLIF_EINVAL, "n_delay must be in [1, 256]");
+    if (nb <= 0 || nb > kMaxBasis) return fail(GLIF_EINVAL, "n_basis must be in [1, 8]");
+    if (tr->n_post != N || tl->n_post != N || tb->n_post != N)
+        return fail(GLIF_EINVAL, "table n_post differs from n_neurons");
+    if (tr->n_slots != D || tr->n_cols != static_cast<int64_t>(D) * N)
+        return fail(GLIF_EINVAL, "recurrent table must have n_delay slots of n_neurons columns");
+    if (tl->n_slots != 1 || tb->n_slots != 1) return fail(GLIF_EINVAL, "input tables take no delays");
+    for (Table *t : {tr, tl, tb}) {
+        if (t->n_basis != nb || t->n_types != tr->n_types ||
+            std::memcmp(t->basis_host, tr->basis_host, sizeof(float) * tr->n_types * nb) != 0)
+            return fail(GLIF_EINVAL, "all tables must share one basis table");
+    }
+    for (int i = 0; i < N; ++i)
+        if (t_ref_steps[i] < 1 || t_ref_steps[i] > 32767)
+            return fail(GLIF_EINVAL, "t_ref_steps must be in [1, 32767]");
+    Cell *c = new Cell();
+    c->cfg = *cfg;
+    c->N = N;
+    c->Np = (N + kWave - 1) / kWave * kWave;
+    c->W = c->Np / kWave;
+    c->D = D;
+    c->nb = nb;
+    c->n_types = tr->n_types;
+    for (int q = 0; q < nb; ++q) {
+        c->syn_decay[q] = syn_decay[q];
+        c->psc_initial[q] = psc_initial[q];
+        c->dtsd[q] = cfg->dt * syn_decay[q];
+    }
+    c->rec = tr;
+    c->lgn = tl;
+    c->bkg = tb;
+    auto up = [](auto **dst, const auto *src, size_t n) -> hipError_t {
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(dst), n * sizeof(**dst));
+        if (e != hipSuccess) return e;
+        return hipMemcpy(*dst, src, n * sizeof(**dst), hipMemcpyHostToDevice);
+    };
+    hipError_t e;
+    if ((e = up(&c->decay, decay, N)) != hipSuccess || (e = up(&c->cf, current_factor, N)) != hipSuccess ||
+        (e = up(&c->asc_decay, asc_decay, 2 * static_cast<size_t>(N))) != hipSuccess ||
+        (e = up(&c->asc_amps, asc_amps, 2 * static_cast<size_t>(N))) != hipSuccess ||
+        (e = up(&c->tref, t_ref_steps, N)) != hipSuccess) {
+        glif_cell_destroy(reinterpret_cast<glif_cell *>(c));
+        return hip_fail(e, "cell upload");
+    }
+    *out = reinterpret_cast<glif_cell *>(c);
+    return GLIF_OK;
+}
+
+void glif_cell_destroy(glif_cell *cc) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c) return;
+    for (void *p : {static_cast<void *>(c->decay), static_cast<void *>(c->cf),
+                    static_cast<void *>(c->asc_decay), static_cast<void *>(c->asc_amps),
+                    static_cast<void *>(c->tref)})
+        if (p) (void)hipFree(p);
+    delete c;
+}
+
+size_t glif_cell_workspace(const glif_cell *cc, int32_t B, int32_t T) {
+    if (!cc || B <= 0 || T <= 0) return 0;
+    size_t bytes = 0;
+    carve_cell(nullptr, reinterpret_cast<const Cell *>(cc), B, T, &bytes);
+    return bytes;
+}
+
+int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const uint8_t *lgn,
+                      const uint8_t *bkg, glif_state *st, float *z_out, float *v_out,
+                      int32_t *spike_count, void *ws, size_t ws_bytes, void *stream) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c || !lgn || !bkg || !st || !st->z_buf || !st->v || !st->r || !st->asc || !st->psc_rise || !st->psc)
+        return fail(GLIF_EINVAL, "NULL argument");
+    if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
+    if (T <= 0) return fail(GLIF_EINVAL, "T must be > 0");
+    if (mode != GLIF_MODE_EVENT && mode != GLIF_MODE_DETERMINISTIC) return fail(GLIF_EINVAL, "unknown mode");
+    if (!ws || ws_bytes < glif_cell_workspace(cc, B, T)) return fail(GLIF_ENOMEM, "workspace too small");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    CellWs w = carve_cell(ws, c, B, T, nullptr);
+    const CellConst k = make_const(c, B);
+    const bool event = mode == GLIF_MODE_EVENT;
+    const Table *tr = c->rec, *tl = c->lgn, *tb = c->bkg;
+    int rc;
+
+    // input lists (LGN push in the forward, LGN / background dW in the backward)
+    if ((rc = build_batch_mask_lists(lgn, T, B, tl->n_cols, w.lgn_off, w.lgn_pre, w.lgn_mask, w.scratch, s)))
+        return rc;
+    const int Wwin = win_width(B), nwin = n_windows(T, Wwin);
+    if (nwin > 0) {
+        if ((rc = build_window_mask_lists(lgn, T, B, tl->n_cols, Wwin, nwin, w.lw_off, w.lw_pre, w.lw_mask,
+                                          w.scratch, s)))
+            return rc;
+        if ((rc = build_window_mask_lists(bkg, T, B, tb->n_cols, Wwin, nwin, w.kw_off, w.kw_pre, w.kw_mask,
+                                          w.scratch, s)))
+            return rc;
+    }
+    GLIF_HIP(hipMemcpyAsync(w.bkg_cnt, bkg, static_cast<size_t>(T) * B * tb->n_cols, hipMemcpyDeviceToDevice, s));
+    // spike history of the initial state
+    if ((rc = launch_fill_u32(w.rcount, 0u, c->D + 1, s))) return rc;
+    const int64_t n_init = static_cast<int64_t>(c->D) * B * c->Np;
+    hipLaunchKernelGGL(k_init_history, dim3(ceil_div(n_init, kBlock)), dim3(kBlock), 0, s, st->z_buf, k,
+                       w.zbits, w.rlist, w.rcount, event ? 1 : 0);
+    GLIF_HIP(hipGetLastError());
+    if (event && (rc = launch_fill_u32(w.I, 0u, static_cast<size_t>(B) * c->N * c->nb, s))) return rc;
+
+    const size_t lds = sizeof(float) * c->n_types * c->nb;
+    StepArgs sa{};
+    sa.k = k;
+    sa.v = st->v;
+    sa.r = st->r;
+    sa.asc = st->asc;
+    sa.R = st->psc_rise;
+    sa.P = st->psc;
+    sa.decay = c->decay;
+    sa.cf = c->cf;
+    sa.ad = c->asc_decay;
+    sa.amp = c->asc_amps;
+    sa.tref = c->tref;
+    sa.I = w.I;
+    sa.zbits = w.zbits;
+    sa.refbits = w.refbits;
+    sa.vsave = w.vsave;
+    sa.z_out = z_out;
+    sa.v_out = v_out;
+    sa.spike_count = spike_count;
+    sa.rlist = w.rlist;
+    sa.rcount = w.rcount;
+    sa.rec_row = tr->row_ptr;
+    sa.rec_pd = tr->pd;
+    sa.rec_sid = tr->sid_row;
+    sa.rec_w = tr->w_row;
+    sa.lgn_row = tl->row_ptr;
+    sa.lgn_pd = tl->pd;
+    sa.lgn_sid = tl->sid_row;
+    sa.lgn_w = tl->w_row;
+    sa.n_lgn = static_cast<int32_t>(tl->n_cols);
+    sa.bkg_row = tb->row_ptr;
+    sa.bkg_pd = tb->pd;
+    sa.bkg_sid = tb->sid_row;
+    sa.bkg_w = tb->w_row;
+    sa.n_bkg = static_cast<int32_t>(tb->n_cols);
+    sa.basis = tr->basis;
+
+    PushArgs pa{};
+    pa.D = c->D;
+    pa.N = c->N;
+    pa.B = B;
+    pa.nb = c->nb;
+    pa.n_types = c->n_types;
+    const int Lp = 64;
+    pa.chunks_rec = chunks_for(tr, Lp);
+    pa.chunks_lgn = chunks_for(tl, Lp);
+    pa.rlist = w.rlist;
+    pa.rcount = w.rcount;
+    pa.rec_colptr = tr->col_ptr;
+    pa.rec_ps = tr->ps;
+    pa.rec_w = tr->w_col;
+    pa.lgn_off = w.lgn_off;
+    pa.lgn_pre = w.lgn_pre;
+    pa.lgn_mask = w.lgn_mask;
+    pa.lgn_colptr = tl->col_ptr;
+    pa.lgn_ps = tl->ps;
+    pa.lgn_w = tl->w_col;
+    pa.basis = tr->basis;
+    pa.I = w.I;
+    const int push_grid = 2048;
+    const dim3 step_grid(ceil_div(static_cast<int64_t>(B) * c->Np, kBlock));
+
+    for (int t = 0; t < T; ++t) {
+        sa.t = t;
+        sa.lgn_x = lgn + static_cast<int64_t>(t) * B * tl->n_cols;
+        sa.bkg_x = bkg + static_cast<int64_t>(t) * B * tb->n_cols;
+        if (event) {
+            pa.t = t;
+            {
+                ProfScope p(kProfPush, s);
+                hipLaunchKernelGGL((k_push<Lp>), dim3(push_grid), dim3(kBlock), lds, s, pa);
+            }
+            ProfScope p(kProfStep, s);
+            hipLaunchKernelGGL((k_step<false>), step_grid, dim3(kBlock), lds, s, sa);
+        } else {
+            ProfScope p(kProfStep, s);
+            hipLaunchKernelGGL((k_step<true>), step_grid, dim3(kBlock), lds, s, sa);
+        }
+    }
+    GLIF_HIP(hipGetLastError());
+    const int64_t n_out = static_cast<int64_t>(c->D) * B * c->N;
+    hipLaunchKernelGGL(k_write_zbuf, dim3(ceil_div(n_out, kBlock)), dim3(kBlock), 0, s, st->z_buf, k, T,
+                       w.zbits);
+    GLIF_HIP(hipGetLastError());
+    return GLIF_OK;
+}
+
+int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, const float *gz_neuron,
+                       const float *gv, float *dw_rec, float *dw_lgn, float *dw_bkg, void *ws,
+                       size_t ws_bytes, void *stream) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c) return fail(GLIF_EINVAL, "NULL cell");
+    if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
+    if (T <= 0) return fail(GLIF_EINVAL, "T must be > 0");
+    if (!ws || ws_bytes < glif_cell_workspace(cc, B, T)) return fail(GLIF_ENOMEM, "workspace too small");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    CellWs w = carve_cell(ws, c, B, T, nullptr);
+    const CellConst k = make_const(c, B);
+    const Table *tr = c->rec, *tl = c->lgn, *tb = c->bkg;
+    const int64_t BN = static_cast<int64_t>(B) * c->N;
+    int rc;
+    if ((rc = launch_fill_u32(w.gV, 0u, BN, s)) || (rc = launch_fill_u32(w.gP, 0u, BN * c->nb, s)) ||
+        (rc = launch_fill_u32(w.gR, 0u, BN * c->nb, s)))
+        return rc;
+    // padding elements of each G row stay zero
+    if ((rc = launch_fill_u32(w.G, 0u, static_cast<size_t>(c->N) * c->n_types * g_row(win_width(B), B), s)))
+        return rc;
+    if (dw_rec && (rc = launch_fill_u32(w.dw_rec, 0u, tr->n_syn, s))) return rc;
+    if (dw_lgn && (rc = launch_fill_u32(w.dw_lgn, 0u, tl->n_syn, s))) return rc;
+    if (dw_bkg && (rc = launch_fill_u32(w.dw_bkg, 0u, tb->n_syn, s))) return rc;
+
+    const size_t lds = sizeof(float) * c->n_types * c->nb;
+    const int Wwin = win_width(B), ring = ring_size(c), Rg = g_row(Wwin, B);
+    AdjArgs aa{};
+    aa.k = k;
+    aa.T = T;
+    aa.ring = ring;
+    aa.R = Rg;
+    aa.vsave = w.vsave;
+    aa.refbits = w.refbits;
+    aa.gz = gz;
+    aa.gz_neuron = gz_neuron;
+    aa.gv = gv;
+    aa.dZ = w.dZ;
+    aa.gV = w.gV;
+    aa.gP = w.gP;
+    aa.gR = w.gR;
+    aa.decay = c->decay;
+    aa.cf = c->cf;
+    aa.G = w.G;
+    aa.basis = tr->basis;
+
+    ColArgs ca{tr->n_cols, c->N, c->n_types, 0, Rg, tr->ph_ptr, tr->ph_pc, tr->ph_w, w.G, 1,
+               dw_rec ? w.dw_rec : nullptr};
+    ActWin act{w.zbits, w.dZ, tr->n_cols, 0, B, c->D, c->W, c->N, ring};
+
+    BwdInArgs la{}, ka{};
+    la.B = ka.B = B;
+    la.R = ka.R = Rg;
+    la.n_post = ka.n_post = c->N;
+    la.G = ka.G = w.G;
+    la.chunks = chunks_for(tl, kWave);
+    la.n_in = tl->n_cols;
+    la.off = w.lw_off;
+    la.pre = w.lw_pre;
+    la.mask = w.lw_mask;
+    la.cnt = nullptr;
+    la.col_ptr = tl->col_ptr;
+    la.ps = tl->ps;
+    la.dw = w.dw_lgn;
+    ka.chunks = chunks_for(tb, kWave);
+    ka.n_in = tb->n_cols;
+    ka.off = w.kw_off;
+    ka.pre = w.kw_pre;
+    ka.mask = w.kw_mask;
+    ka.cnt = w.bkg_cnt;
+    ka.col_ptr = tb->col_ptr;
+    ka.ps = tb->ps;
+    ka.dw = w.dw_bkg;
+    const int64_t lgn_units = tl->n_cols * static_cast<int64_t>(la.chunks);
+    const int64_t bkg_units = tb->n_cols * static_cast<int64_t>(ka.chunks);
+
+    const dim3 adj_grid(ceil_div(BN, kBlock));
+    int j = 0;
+    for (int t0 = T - 1; t0 >= 2; t0 -= Wwin, ++j) {
+        const int nw = std::min(Wwin, t0 - 1);
+        const int s0 = t0 - 2;
+        aa.t0 = t0;
+        aa.nw = nw;
+        {
+            ProfScope p(kProfAdj, s);
+            hipLaunchKernelGGL(k_adj, adj_grid, dim3(kBlock), lds, s, aa);
+        }
+        ca.n_elem = nw * B;
+        act.s0 = s0;
+        {
+            ProfScope p(kProfBwdRec, s);
+            launch_bwd_rec(ca, act, s);
+        }
+        if (dw_lgn) {
+            la.j = j;
+            la.s0 = s0;
+            ProfScope p(kProfBwdLgn, s);
+            launch_bwd_in(la, lgn_units, s);
+        }
+        if (dw_bkg) {
+            ka.j = j;
+            ka.s0 = s0;
+            ProfScope p(kProfBwdBkg, s);
+            launch_bwd_in(ka, bkg_units, s);
+        }
+    }
+    GLIF_HIP(hipGetLastError());
+    if (dw_rec && (rc = launch_scatter_f32(dw_rec, w.dw_rec, tr->ph_order, tr->n_syn, s))) return rc;
+    if (dw_lgn && (rc = launch_scatter_f32(dw_lgn, w.dw_lgn, tl->order, tl->n_syn, s))) return rc;
+    if (dw_bkg && (rc = launch_scatter_f32(dw_bkg, w.dw_bkg, tb->order, tb->n_syn, s))) return rc;
+    return GLIF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,114 @@
+// Internal declarations of libglif (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/glif.h"
+
+namespace glif {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kMaxBasis = 8;
+constexpr int kMaxBatch = 32;
+constexpr uint32_t kLow24 = 0x00FFFFFFu;
+
+// ---- error plumbing -------------------------------------------------------
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+int hip_fail(hipError_t e, const char *what);
+
+#define GLIF_HIP(call)                                   \
+    do {                                                 \
+        hipError_t e_ = (call);                          \
+        if (e_ != hipSuccess) return hip_fail(e_, #call); \
+    } while (0)
+
+// ---- device-resident synapse table (one population) -----------------------
+// Column-grouped ("CSC", the reference's pre_ind_table) and post-grouped ("CSR")
+// copies of the same synapses.  Index k runs over the column-grouped order,
+// j over the post-grouped order.
+struct Table {
+    int64_t n_syn = 0;
+    int32_t n_post = 0;
+    int64_t n_cols = 0;
+    int32_t n_slots = 1;   // delay slots D (cols = pre + n_post * (d - 1))
+    int32_t n_pre = 0;     // n_cols / n_slots
+    int32_t n_types = 0;
+    int32_t n_basis = 0;
+    int32_t max_col_len = 0;
+    float *basis = nullptr;       // [n_types][n_basis]
+    // column-grouped
+    int32_t *col_ptr = nullptr;   // [n_cols + 1]  == row_splits
+    int32_t *order = nullptr;     // [n_syn]       synapse id at position k
+    uint32_t *ps = nullptr;       // [n_syn]       post | syn_id << 24
+    float *w_col = nullptr;       // [n_syn]       weight at position k
+    // post-grouped, each row in ascending (col, synapse id)
+    int32_t *row_ptr = nullptr;   // [n_post + 1]
+    int32_t *perm = nullptr;      // [n_syn]       synapse id at position j
+    uint32_t *pd = nullptr;       // [n_syn]       pre | (delay - 1) << 24
+    uint8_t *sid_row = nullptr;   // [n_syn]
+    float *w_row = nullptr;       // [n_syn]
+    // type-phased: ordered by (syn_id, column, synapse id)
+    int32_t *ph_ptr = nullptr;    // [n_types * n_cols + 1]
+    int32_t *ph_order = nullptr;  // [n_syn]       synapse id at position k
+    uint32_t *ph_pc = nullptr;    // [n_syn]       post | (column % 256) << 24
+    float *ph_w = nullptr;        // [n_syn]
+    float *basis_host = nullptr;  // host copy [n_types][n_basis]
+};
+
+// ---- cell ------------------------------------------------------------------
+struct Cell {
+    glif_cell_config cfg{};
+    int32_t N = 0, Np = 0, W = 0;   // neurons, padded to 64, 64-bit words per row
+    int32_t D = 0, nb = 0, n_types = 0;
+    float *decay = nullptr, *cf = nullptr;   // [N]
+    float *asc_decay = nullptr, *asc_amps = nullptr;  // [N*2]
+    int32_t *tref = nullptr;                 // [N]
+    float syn_decay[kMaxBasis]{}, psc_initial[kMaxBasis]{}, dtsd[kMaxBasis]{};
+    Table *rec = nullptr, *lgn = nullptr, *bkg = nullptr;
+};
+
+// Small per-cell constants passed by value to kernels.
+struct CellConst {
+    int32_t N, Np, W, D, nb, n_types, B, Bp;
+    float lr, vgd, om, rd_scale, gauss_std, damp, dt;
+    int32_t pseudo_gauss, hard_reset;
+    float sd[kMaxBasis], p0[kMaxBasis], dtsd[kMaxBasis];
+};
+
+// ---- workspace carving ------------------------------------------------------
+struct Carver {
+    char *base;
+    size_t off = 0;
+    size_t cap;
+    Carver(void *b, size_t c) : base(static_cast<char *>(b)), cap(c) {}
+    template <typename T>
+    T *take(size_t n) {
+        off = (off + 255) & ~size_t(255);
+        T *p = reinterpret_cast<T *>(base ? base + off : nullptr);
+        off += n * sizeof(T);
+        return p;
+    }
+    bool ok() const { return off <= cap; }
+};
+
+// ---- launch helpers (defined in the .hip files) ----------------------------
+int launch_fill_u32(void *p, uint32_t value, size_t n, hipStream_t s);
+int launch_gather_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s);
+int launch_scatter_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s);
+
+inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
+
+// Batch padded to the float4 groups of G (4, 8, 16 or 32).
+int batch_pad(int B);
+// Lanes per column for the column-grouped kernels (16, 32 or 64).
+int sub_wave_for(const Table *t);
+// Blocks for `items` sub-waves of L lanes (capped; kernels grid-stride).
+int grid_subwaves(int64_t items, int L);
+
+}  // namespace glif

@@ -1,0 +1,222 @@
+// Op-level entry points of calculate_synaptic_currents (models.py:103-263):
+// forward (event push or deterministic pull) and the custom gradient.
+#include <algorithm>
+
+#include "compact.h"
+#include "glif_internal.h"
+#include "prof.h"
+#include "syn_kernels.h"
+
+namespace glif {
+
+// ---------------------------------------------------------------- forward ----
+// Deterministic pull: thread per (b, post) walks the post's row in ascending
+// (column, synapse id) -- the order in which TF's CPU UnsortedSegmentSum meets the
+// events of this (b, post) -- and writes I[b][post][:] (models.py:141-169).
+template <bool COUNTS>
+__global__ void __launch_bounds__(kBlock)
+    k_syn_pull_dense(const float *__restrict__ z, int32_t B, int64_t n_cols, int32_t n_post,
+                     int32_t n_pre, const int32_t *__restrict__ row_ptr,
+                     const uint32_t *__restrict__ pd, const uint8_t *__restrict__ sid,
+                     const float *__restrict__ w, const float *__restrict__ basis, int n_types,
+                     int nb, float *__restrict__ I) {
+    extern __shared__ float basis_lds[];
+    load_basis_lds(basis_lds, basis, n_types * nb);
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gt >= static_cast<int64_t>(B) * n_post) return;
+    const int b = static_cast<int>(gt / n_post);
+    const int32_t n = static_cast<int32_t>(gt % n_post);
+    float acc[kMaxBasis];
+    for (int r = 0; r < nb; ++r) acc[r] = 0.0f;
+    const float *zb = z + static_cast<int64_t>(b) * n_cols;
+    for (int32_t j = row_ptr[n]; j < row_ptr[n + 1]; ++j) {
+        const uint32_t q = pd[j];
+        const int64_t c = static_cast<int64_t>(q & kLow24) + static_cast<int64_t>(q >> 24) * n_pre;
+        const float a = zb[c];
+        if (!(a > 0.0f)) continue;
+        const float wv = COUNTS ? w[j] * a : w[j];
+        const float *bs = basis_lds + sid[j] * nb;
+        for (int r = 0; r < nb; ++r) acc[r] = acc[r] + wv * bs[r];
+    }
+    float *dst = I + gt * nb;
+    for (int r = 0; r < nb; ++r) dst[r] = acc[r];
+}
+
+// Event push over a (column, batch-mask) list.
+template <int L, bool COUNTS>
+__global__ void __launch_bounds__(kBlock)
+    k_syn_push_list(const int32_t *__restrict__ cols, const uint32_t *__restrict__ masks,
+                    const int64_t *__restrict__ n_items, const float *__restrict__ z, int64_t n_cols,
+                    const int32_t *__restrict__ col_ptr, const uint32_t *__restrict__ ps,
+                    const float *__restrict__ w, const float *__restrict__ basis, int n_types, int nb,
+                    int32_t n_post, float *__restrict__ I) {
+    extern __shared__ float basis_lds[];
+    load_basis_lds(basis_lds, basis, n_types * nb);
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int lane_s = threadIdx.x % L;
+    const int64_t n_subs = static_cast<int64_t>(gridDim.x) * blockDim.x / L;
+    const int64_t total = *n_items;
+    for (int64_t it = gt / L; it < total; it += n_subs) {
+        const int32_t c = cols[it];
+        const uint32_t m = masks[it];
+        if (COUNTS)
+            push_column<L>(lane_s, col_ptr[c], col_ptr[c + 1], m, MultF32{z + c, n_cols}, ps, w,
+                           basis_lds, nb, n_post, I);
+        else
+            push_column<L>(lane_s, col_ptr[c], col_ptr[c + 1], m, MultOne{}, ps, w, basis_lds, nb,
+                           n_post, I);
+    }
+}
+
+// ---------------------------------------------------------------- backward ----
+__global__ void __launch_bounds__(kBlock)
+    k_make_G(const float *__restrict__ dy, int32_t B, int32_t n_post, int Bp,
+             const float *__restrict__ basis, int n_types, int nb, float *__restrict__ G) {
+    extern __shared__ float basis_lds[];
+    load_basis_lds(basis_lds, basis, n_types * nb);
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gt >= static_cast<int64_t>(B) * n_post) return;
+    const int b = static_cast<int>(gt / n_post);
+    const int64_t n = gt % n_post;
+    float d[kMaxBasis];
+    for (int r = 0; r < nb; ++r) d[r] = dy[gt * nb + r];
+    write_G(G, n, b, Bp, d, basis_lds, n_types, nb, n_post);
+}
+
+template <int LG>
+__global__ void __launch_bounds__(kBlock) k_syn_bwd_cols(ColArgs a, ActDense act) {
+    bwd_cols_lg<LG, 2>(a, act);
+}
+
+int sub_wave_for(const Table *t) {  // lanes per column: ~ the mean column length
+    double avg = t->n_cols ? static_cast<double>(t->n_syn) / t->n_cols : 0.0;
+    return avg <= 24.0 ? 16 : (avg <= 48.0 ? 32 : 64);
+}
+
+int grid_subwaves(int64_t items, int L) {
+    int64_t per_block = kBlock / L;
+    int64_t g = (items + per_block - 1) / per_block;
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(g, 32768)));
+}
+
+int batch_pad(int B) { return B <= 4 ? 4 : (B <= 8 ? 8 : (B <= 16 ? 16 : 32)); }
+
+struct SynWs {
+    int64_t *row_off;
+    int32_t *cols;
+    uint32_t *masks;
+    float *G;
+    float *dw_col;
+    void *scratch;
+};
+
+static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes) {
+    Carver cv(ws, SIZE_MAX);
+    SynWs w{};
+    w.row_off = cv.take<int64_t>(2);
+    w.cols = cv.take<int32_t>(t->n_cols);
+    w.masks = cv.take<uint32_t>(t->n_cols);
+    w.G = cv.take<float>(static_cast<size_t>(t->n_post) * t->n_types * batch_pad(B));
+    w.dw_col = cv.take<float>(std::max<int64_t>(t->n_syn, 1));
+    w.scratch = cv.take<char>(compact_scratch_bytes(1, t->n_cols));
+    if (bytes) *bytes = cv.off;
+    return w;
+}
+
+}  // namespace glif
+
+using namespace glif;
+
+extern "C" {
+
+size_t glif_syn_workspace(const glif_table *tt, int32_t B) {
+    if (!tt || B <= 0) return 0;
+    size_t bytes = 0;
+    carve_syn(nullptr, reinterpret_cast<const Table *>(tt), B, &bytes);
+    return bytes;
+}
+
+int glif_syn_fwd(const glif_table *tt, const float *z, int32_t B, int32_t counts, int32_t mode,
+                 float *I, void *ws, size_t ws_bytes, void *stream) {
+    if (!tt || !z || !I) return fail(GLIF_EINVAL, "NULL argument");
+    if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
+    const Table *t = reinterpret_cast<const Table *>(tt);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    ProfScope prof(kProfSynFwd, s);
+    const size_t lds = sizeof(float) * t->n_types * t->n_basis;
+    const int64_t nI = static_cast<int64_t>(B) * t->n_post;
+    if (mode == GLIF_MODE_DETERMINISTIC) {
+        dim3 grid(ceil_div(nI, kBlock));
+        if (counts)
+            hipLaunchKernelGGL((k_syn_pull_dense<true>), grid, dim3(kBlock), lds, s, z, B, t->n_cols,
+                               t->n_post, t->n_pre, t->row_ptr, t->pd, t->sid_row, t->w_row, t->basis,
+                               t->n_types, t->n_basis, I);
+        else
+            hipLaunchKernelGGL((k_syn_pull_dense<false>), grid, dim3(kBlock), lds, s, z, B, t->n_cols,
+                               t->n_post, t->n_pre, t->row_ptr, t->pd, t->sid_row, t->w_row, t->basis,
+                               t->n_types, t->n_basis, I);
+        GLIF_HIP(hipGetLastError());
+        return GLIF_OK;
+    }
+    if (mode != GLIF_MODE_EVENT) return fail(GLIF_EINVAL, "unknown mode");
+    size_t need = glif_syn_workspace(tt, B);
+    if (!ws || ws_bytes < need) return fail(GLIF_ENOMEM, "workspace too small");
+    SynWs w = carve_syn(ws, t, B, nullptr);
+    int rc = launch_fill_u32(I, 0u, static_cast<size_t>(nI) * t->n_basis, s);
+    if (rc) return rc;
+    rc = build_col_mask_list_f32(z, B, t->n_cols, w.row_off, w.cols, w.masks, w.scratch, s);
+    if (rc) return rc;
+    const int L = sub_wave_for(t);
+    dim3 grid(grid_subwaves(std::min<int64_t>(t->n_cols, 262144), L));
+#define GLIF_PUSH(LL, CC)                                                                           \
+    hipLaunchKernelGGL((k_syn_push_list<LL, CC>), grid, dim3(kBlock), lds, s, w.cols, w.masks,      \
+                       w.row_off + 1, z, t->n_cols, t->col_ptr, t->ps, t->w_col, t->basis,          \
+                       t->n_types, t->n_basis, t->n_post, I)
+    if (L == 16) { if (counts) GLIF_PUSH(16, true); else GLIF_PUSH(16, false); }
+    else if (L == 32) { if (counts) GLIF_PUSH(32, true); else GLIF_PUSH(32, false); }
+    else { if (counts) GLIF_PUSH(64, true); else GLIF_PUSH(64, false); }
+#undef GLIF_PUSH
+    GLIF_HIP(hipGetLastError());
+    return GLIF_OK;
+}
+
+int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t B, int32_t counts,
+                 float *dz, float *dw, void *ws, size_t ws_bytes, void *stream) {
+    if (!tt || !z || !dy) return fail(GLIF_EINVAL, "NULL argument");
+    if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
+    if (!dz && !dw) return GLIF_OK;
+    const Table *t = reinterpret_cast<const Table *>(tt);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    size_t need = glif_syn_workspace(tt, B);
+    if (!ws || ws_bytes < need) return fail(GLIF_ENOMEM, "workspace too small");
+    SynWs w = carve_syn(ws, t, B, nullptr);
+    ProfScope prof(kProfSynBwd, s);
+    const int Bp = batch_pad(B);
+    const size_t lds = sizeof(float) * t->n_types * t->n_basis;
+    int rc;
+    if (B < Bp && (rc = launch_fill_u32(w.G, 0u, static_cast<size_t>(t->n_post) * t->n_types * Bp, s)))
+        return rc;
+    const int64_t nI = static_cast<int64_t>(B) * t->n_post;
+    hipLaunchKernelGGL(k_make_G, dim3(ceil_div(nI, kBlock)), dim3(kBlock), lds, s, dy, B, t->n_post, Bp,
+                       t->basis, t->n_types, t->n_basis, w.G);
+    GLIF_HIP(hipGetLastError());
+    if (dw && (rc = launch_fill_u32(w.dw_col, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
+    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, Bp, t->ph_ptr, t->ph_pc, t->ph_w, w.G,
+               dz ? 1 : 0, dw ? w.dw_col : nullptr};
+    ActDense act{z, dz, t->n_cols, counts};
+    const int LG = Bp / 4;
+    const dim3 grid(ceil_div(t->n_cols * LG, kBlock));
+    if (LG == 1)
+        hipLaunchKernelGGL(k_syn_bwd_cols<1>, grid, dim3(kBlock), 0, s, ca, act);
+    else if (LG == 2)
+        hipLaunchKernelGGL(k_syn_bwd_cols<2>, grid, dim3(kBlock), 0, s, ca, act);
+    else if (LG == 4)
+        hipLaunchKernelGGL(k_syn_bwd_cols<4>, grid, dim3(kBlock), 0, s, ca, act);
+    else
+        hipLaunchKernelGGL(k_syn_bwd_cols<8>, grid, dim3(kBlock), 0, s, ca, act);
+    GLIF_HIP(hipGetLastError());
+    if (dw) return launch_scatter_f32(dw, w.dw_col, t->ph_order, t->n_syn, s);
+    return GLIF_OK;
+}
+
+}  // extern "C"

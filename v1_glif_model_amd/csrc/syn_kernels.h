@@ -1,0 +1,248 @@
+// Device code of the synaptic-current operator (calculate_synaptic_currents,
+// models.py:103-263), shared by the op-level entry points (syn.hip) and the
+// T-step cell (cell.hip).
+//
+// Layouts
+//   column-grouped table (Table::col_ptr/ps/w_col): the synapses of presynaptic
+//     column c are k in [col_ptr[c], col_ptr[c+1]); ps[k] = post | syn_id << 24.
+//   post-grouped table (Table::row_ptr/pd/sid_row/w_row): the synapses of post n
+//     are j in [row_ptr[n], row_ptr[n+1]) in ascending (column, synapse id);
+//     pd[j] = pre | (delay - 1) << 24.
+//   I  [B][n_post][nb]  (the reference's i_rec_flat [B*N, nb]).
+//   type-phased table (Table::ph_ptr/ph_pc/ph_w): synapses ordered by (syn_id,
+//     column, synapse id); the type-s synapses of column c are
+//     k in [ph_ptr[s * n_cols + c], ph_ptr[s * n_cols + c + 1]);
+//     ph_pc[k] = post | (c % kPhaseCols) << 24.
+//   I  [B][n_post][nb]  (the reference's i_rec_flat [B*N, nb]).
+//   G  [n_types][n_post][Bp]: G[s][post][b] = sum_r dy[b][post][r] * basis[s][r],
+//     the per-synapse-type projection of dy that both dz and dW need; one type's
+//     slice (n_post * Bp floats, ~2 MB at 66k neurons) fits an XCD's L2.
+#pragma once
+
+#include "glif_internal.h"
+
+namespace glif {
+
+// Products and sums are kept as separate roundings (the library is built with
+// -ffp-contract=off) so the deterministic path matches the reference's
+// Mul-then-UnsortedSegmentSum arithmetic bit for bit.
+
+__device__ inline void load_basis_lds(float *lds, const float *basis, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) lds[i] = basis[i];
+    __syncthreads();
+}
+
+// Per-batch weight multipliers of an event: 1 for spikes, the Poisson count for
+// the background source (models.py:917-931), the dense input value for the
+// op-level entry points called with counts.
+struct MultOne {
+    static constexpr bool kOne = true;
+    __device__ float operator()(int) const { return 1.0f; }
+};
+struct MultU8 {
+    static constexpr bool kOne = false;
+    const uint8_t *p;
+    int64_t stride;
+    __device__ float operator()(int b) const { return static_cast<float>(p[b * stride]); }
+};
+struct MultF32 {
+    static constexpr bool kOne = false;
+    const float *p;
+    int64_t stride;
+    __device__ float operator()(int b) const { return p[b * stride]; }
+};
+
+// ---- event-driven push of one column ------------------------------------------
+// The L lanes of a sub-wave stream column c's synapses and add
+// (w * mult_b) * basis[syn_id][r] into I[b][post][r] with fp32 atomics for every
+// batch entry b in `bmask`.  mult_b = 1 for spikes, the Poisson count for the
+// background source.  Zero products are skipped: adding +/-0 never changes a sum
+// that starts at +0.
+template <int L, class Mult>
+__device__ inline void push_column(int lane_s, int32_t lo, int32_t hi, uint32_t bmask,
+                                   Mult mult, const uint32_t *__restrict__ ps,
+                                   const float *__restrict__ w, const float *basis_lds, int nb,
+                                   int32_t n_post, float *__restrict__ I) {
+    for (int32_t k = lo + lane_s; k < hi; k += L) {
+        const uint32_t p = ps[k];
+        const float wk = w[k];
+        const int32_t post = static_cast<int32_t>(p & kLow24);
+        const float *bs = basis_lds + (p >> 24) * nb;
+        uint32_t m = bmask;
+        while (m) {
+            const int b = __ffs(m) - 1;
+            m &= m - 1;
+            const float wv = Mult::kOne ? wk : wk * mult(b);
+            float *dst = I + (static_cast<int64_t>(b) * n_post + post) * nb;
+            for (int r = 0; r < nb; ++r) {
+                const float v = wv * bs[r];
+                if (v != 0.0f) unsafeAtomicAdd(dst + r, v);
+            }
+        }
+    }
+}
+
+// ---- fused backward of one column (A7 + A8) --------------------------------------
+// dz[b] = sum_k w[k] * G[post_k][sid_k][b]   (returned reduced over the sub-wave)
+// dw_col[k] += sum_{b in bmask, ascending} G[post_k][sid_k][b] * mult_b
+template <int L, int BQ, bool WANT_DZ, class Mult>
+__device__ inline void bwd_column(int lane_s, int32_t lo, int32_t hi, uint32_t bmask,
+                                  Mult mult, const uint32_t *__restrict__ ps,
+                                  const float *__restrict__ w, const float *__restrict__ G,
+                                  int32_t n_post, float *__restrict__ dw_col, float (&acc)[4 * BQ]) {
+#pragma unroll
+    for (int i = 0; i < 4 * BQ; ++i) acc[i] = 0.0f;
+    for (int32_t k = lo + lane_s; k < hi; k += L) {
+        const uint32_t p = ps[k];
+        const float4 *g4 = reinterpret_cast<const float4 *>(
+            G + (static_cast<int64_t>(p >> 24) * n_post + (p & kLow24)) * (4 * BQ));
+        float g[4 * BQ];
+#pragma unroll
+        for (int q = 0; q < BQ; ++q) {
+            const float4 v = g4[q];
+            g[4 * q + 0] = v.x;
+            g[4 * q + 1] = v.y;
+            g[4 * q + 2] = v.z;
+            g[4 * q + 3] = v.w;
+        }
+        if (WANT_DZ) {
+            const float wk = w[k];
+#pragma unroll
+            for (int i = 0; i < 4 * BQ; ++i) acc[i] += wk * g[i];
+        }
+        if (bmask) {
+            float a = dw_col[k];
+#pragma unroll
+            for (int b = 0; b < 4 * BQ; ++b)
+                if (bmask & (1u << b)) a += Mult::kOne ? g[b] : g[b] * mult(b);
+            dw_col[k] = a;
+        }
+    }
+    if (WANT_DZ) {
+#pragma unroll
+        for (int i = 0; i < 4 * BQ; ++i) {
+            float v = acc[i];
+#pragma unroll
+            for (int o = L / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+            acc[i] = v;
+        }
+    }
+}
+
+// G[s][post][b] = sum_r dy[b][post][r] * basis[s][r]  (sequential r, the order of
+// einsum('cr,cr->c') in models.py:232).
+__device__ inline void write_G(float *__restrict__ G, int64_t post, int b, int Bp, const float *dy,
+                               const float *basis_lds, int n_types, int nb, int32_t n_post) {
+    for (int s = 0; s < n_types; ++s) {
+        const float *bs = basis_lds + s * nb;
+        float e = dy[0] * bs[0];
+        for (int r = 1; r < nb; ++r) e = e + dy[r] * bs[r];
+        G[(static_cast<int64_t>(s) * n_post + post) * Bp + b] = e;
+    }
+}
+
+// ---- column backward (A7 + A8): dz of every column, dW of its active events -----
+// G rows hold R floats: n_elem = W*B used elements (W consecutive reverse timesteps
+// x B batch entries; element e = w*B + b), zero padding after.  A group of LG = R/4
+// lanes owns one column: all lanes walk the column's synapses (type by type, the
+// type-phased order) and lane q accumulates elements 4q..4q+3 of w * G[sid][post].
+// One G row is then one cache line fetched per synapse per W timesteps.  Each
+// synapse is touched by one lane group, so dW needs no atomics; dz and dW
+// accumulate in a fixed order (deterministic).
+struct ColArgs {
+    int64_t n_cols;
+    int32_t n_post, n_types, n_elem, R;
+    const int32_t *ph_ptr;
+    const uint32_t *ph_pc;
+    const float *ph_w;
+    const float *G;   // [n_types][n_post][R]
+    int32_t want_dz;
+    float *dw;        // [n_syn] type-phased order, accumulated; or nullptr
+};
+
+// Op-level activity: z [B][n_cols] dense, element e = b.
+struct ActDense {
+    const float *z;
+    float *dz;        // [B][n_cols]
+    int64_t n_cols;
+    int32_t counts;
+    __device__ bool on(int64_t c, int e) const { return z[e * n_cols + c] > 0.0f; }
+    __device__ float mult(int64_t c, int e) const { return counts ? z[e * n_cols + c] : 1.0f; }
+    __device__ float *out(int64_t c, int e) const { return dz + e * n_cols + c; }
+};
+
+template <int LG, int U, class Act>
+__device__ inline void bwd_cols_lg(const ColArgs &a, const Act &act) {
+    constexpr int R = 4 * LG;
+    const int q = threadIdx.x % LG;
+    const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / LG;
+    if (c >= a.n_cols) return;  // the whole lane group leaves together
+    uint32_t bits = 0;
+    float mult[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (a.dw) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * q + i;
+            if (e < a.n_elem && act.on(c, e)) {
+                bits |= 1u << i;
+                mult[i] = act.mult(c, e);
+            }
+        }
+    }
+    uint32_t any = bits;
+#pragma unroll
+    for (int o = 1; o < LG; o <<= 1) any |= __shfl_xor(any, o, kWave);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < a.n_types; ++s) {
+        const int64_t pi = static_cast<int64_t>(s) * a.n_cols + c;
+        const int32_t lo = a.ph_ptr[pi], hi = a.ph_ptr[pi + 1];
+        const float *Gs = a.G + static_cast<int64_t>(s) * a.n_post * R;
+        for (int32_t k = lo; k < hi; k += U) {
+            uint32_t pc[U];
+            float wk[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool ok = k + u < hi;
+                pc[u] = ok ? a.ph_pc[k + u] : 0u;
+                wk[u] = ok ? a.ph_w[k + u] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (k + u >= hi) break;  // uniform within the lane group
+                const float4 g = reinterpret_cast<const float4 *>(Gs + static_cast<int64_t>(pc[u] & kLow24) * R)[q];
+                if (a.want_dz) {
+                    acc[0] += wk[u] * g.x;
+                    acc[1] += wk[u] * g.y;
+                    acc[2] += wk[u] * g.z;
+                    acc[3] += wk[u] * g.w;
+                }
+                if (any) {
+                    float p = 0.0f;
+                    if (bits & 1u) p += g.x * mult[0];
+                    if (bits & 2u) p += g.y * mult[1];
+                    if (bits & 4u) p += g.z * mult[2];
+                    if (bits & 8u) p += g.w * mult[3];
+#pragma unroll
+                    for (int o = 1; o < LG; o <<= 1) p += __shfl_xor(p, o, kWave);
+                    if (q == 0) a.dw[k + u] += p;
+                }
+            }
+        }
+    }
+    if (a.want_dz) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * q + i;
+            if (e < a.n_elem) *act.out(c, e) = acc[i];
+        }
+    }
+}
+
+// Row length (floats) of G for B batch entries over W timesteps: a power of two >= 4.
+__host__ __device__ inline int g_row(int W, int B) {
+    int r = 4;
+    while (r < W * B) r <<= 1;
+    return r;
+}
+
+}  // namespace glif

@@ -1,0 +1,260 @@
+// Synapse tables: the one-time host build of the column- and post-grouped
+// orders (A1/A2), their upload, the weight-shadow refresh, and shared helpers.
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "glif_internal.h"
+
+namespace glif {
+
+// ---------------------------------------------------------------- errors ----
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return GLIF_EHIP;
+}
+
+// --------------------------------------------------------------- kernels ----
+__global__ void k_fill_u32(uint32_t *__restrict__ p, uint32_t v, size_t n) {
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (; i < n; i += stride) p[i] = v;
+}
+
+__global__ void k_gather_f32(float *__restrict__ dst, const float *__restrict__ src,
+                             const int32_t *__restrict__ idx, int64_t n) {
+    int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (; i < n; i += stride) dst[i] = src[idx[i]];
+}
+
+__global__ void k_scatter_f32(float *__restrict__ dst, const float *__restrict__ src,
+                              const int32_t *__restrict__ idx, int64_t n) {
+    int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (; i < n; i += stride) dst[idx[i]] = src[i];
+}
+
+static int grid_for(int64_t n) {
+    int64_t g = (n + kBlock - 1) / kBlock;
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(g, 8192)));
+}
+
+int launch_fill_u32(void *p, uint32_t value, size_t n, hipStream_t s) {
+    if (n == 0) return GLIF_OK;
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(static_cast<int64_t>(n))), dim3(kBlock), 0, s,
+                       static_cast<uint32_t *>(p), value, n);
+    GLIF_HIP(hipGetLastError());
+    return GLIF_OK;
+}
+
+int launch_gather_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s) {
+    if (n == 0) return GLIF_OK;
+    hipLaunchKernelGGL(k_gather_f32, dim3(grid_for(n)), dim3(kBlock), 0, s, dst, src, idx, n);
+    GLIF_HIP(hipGetLastError());
+    return GLIF_OK;
+}
+
+int launch_scatter_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s) {
+    if (n == 0) return GLIF_OK;
+    hipLaunchKernelGGL(k_scatter_f32, dim3(grid_for(n)), dim3(kBlock), 0, s, dst, src, idx, n);
+    GLIF_HIP(hipGetLastError());
+    return GLIF_OK;
+}
+
+// ------------------------------------------------------------ host builds ----
+// Stable counting sort of synapse ids by key (models.py:317-341): order holds, for
+// each key in ascending order, the ids with that key in ascending id order.
+static void counting_sort(const int64_t *key, const int32_t *ids, int64_t n, int64_t n_keys,
+                          int32_t *splits, int32_t *order) {
+    std::fill(splits, splits + n_keys + 1, 0);
+    for (int64_t i = 0; i < n; ++i) splits[key[ids ? ids[i] : i] + 1] += 1;
+    for (int64_t c = 0; c < n_keys; ++c) splits[c + 1] += splits[c];
+    std::vector<int32_t> wp(splits, splits + n_keys);
+    for (int64_t i = 0; i < n; ++i) {
+        int32_t id = ids ? ids[i] : static_cast<int32_t>(i);
+        order[wp[key[id]]++] = id;
+    }
+}
+
+template <typename T>
+static int upload(T **dst, const T *src, size_t n) {
+    GLIF_HIP(hipMalloc(reinterpret_cast<void **>(dst), std::max<size_t>(n, 1) * sizeof(T)));
+    if (n) GLIF_HIP(hipMemcpy(*dst, src, n * sizeof(T), hipMemcpyHostToDevice));
+    return GLIF_OK;
+}
+
+static void free_table(Table *t) {
+    if (!t) return;
+    void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
+                    t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pc, t->ph_w};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    delete[] t->basis_host;
+    delete t;
+}
+
+}  // namespace glif
+
+using namespace glif;
+
+extern "C" {
+
+const char *glif_last_error(void) { return g_last_error.c_str(); }
+
+int glif_version(void) { return 1; }
+
+int glif_make_pre_ind_table(const int64_t *cols, int64_t n_syn, int64_t n_source, int32_t *order,
+                            int32_t *row_splits, int64_t *bad_index) {
+    if (n_source <= 0)
+        return fail(GLIF_EINVAL, "`n_source_neurons` must be > 0, got " + std::to_string(n_source) + ".");
+    if (n_syn < 0 || n_syn > INT32_MAX || n_source > INT32_MAX)
+        return fail(GLIF_EINVAL, "table too large for int32 order/row_splits");
+    for (int64_t i = 0; i < n_syn; ++i) {
+        if (cols[i] < 0 || cols[i] >= n_source) {
+            if (bad_index) *bad_index = i;
+            return fail(GLIF_ERANGE, "Presynaptic index " + std::to_string(cols[i]) +
+                                         " is out of bounds for `n_source_neurons=" +
+                                         std::to_string(n_source) + "`.");
+        }
+    }
+    counting_sort(cols, nullptr, n_syn, n_source, row_splits, order);
+    return GLIF_OK;
+}
+
+int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *syn_id, int64_t n_syn,
+                      int32_t n_post, int64_t n_cols, int32_t n_delay_slots, const float *basis,
+                      int32_t n_types, int32_t n_basis, glif_table **out) {
+    if (!out) return fail(GLIF_EINVAL, "out is NULL");
+    *out = nullptr;
+    if (n_syn < 0 || n_syn >= INT32_MAX) return fail(GLIF_EINVAL, "n_syn must be in [0, 2^31-1)");
+    if (n_post <= 0 || n_post >= (1 << 24)) return fail(GLIF_EINVAL, "n_post must be in [1, 2^24)");
+    if (n_delay_slots <= 0 || n_delay_slots > 256) return fail(GLIF_EINVAL, "n_delay_slots must be in [1, 256]");
+    if (n_cols <= 0 || n_cols % n_delay_slots != 0 || n_cols / n_delay_slots >= (1 << 24) ||
+        n_cols >= INT32_MAX)
+        return fail(GLIF_EINVAL, "n_cols must be a positive multiple of n_delay_slots with n_cols/D < 2^24");
+    if (n_delay_slots > 1 && n_cols != static_cast<int64_t>(n_delay_slots) * n_post)
+        return fail(GLIF_EINVAL, "recurrent table needs n_cols == n_delay_slots * n_post");
+    if (n_types <= 0 || n_types > 256) return fail(GLIF_EINVAL, "n_types must be in [1, 256]");
+    if (n_basis <= 0 || n_basis > kMaxBasis) return fail(GLIF_EINVAL, "n_basis must be in [1, 8]");
+    const int32_t n_pre = static_cast<int32_t>(n_cols / n_delay_slots);
+    for (int64_t i = 0; i < n_syn; ++i) {
+        if (post[i] < 0 || post[i] >= n_post)
+            return fail(GLIF_ERANGE, "postsynaptic index " + std::to_string(post[i]) + " out of range");
+        if (col[i] < 0 || col[i] >= n_cols)
+            return fail(GLIF_ERANGE, "Presynaptic index " + std::to_string(col[i]) +
+                                         " is out of bounds for `n_source_neurons=" +
+                                         std::to_string(n_cols) + "`.");
+        if (syn_id[i] >= n_types)
+            return fail(GLIF_ERANGE, "syn_id " + std::to_string(syn_id[i]) + " >= n_types");
+    }
+
+    // column-grouped order (A1, bit-exact with models.py:317-341)
+    std::vector<int32_t> col_ptr(n_cols + 1), order(n_syn);
+    counting_sort(col, nullptr, n_syn, n_cols, col_ptr.data(), order.data());
+    // post-grouped order with each row in ascending (col, id): a stable sort of the
+    // column-grouped order by post
+    std::vector<int32_t> row_ptr(static_cast<size_t>(n_post) + 1), perm(n_syn);
+    counting_sort(post, order.data(), n_syn, n_post, row_ptr.data(), perm.data());
+
+    // type-phased order: stable counting sort by syn_id * n_cols + column
+    const int64_t n_ph = static_cast<int64_t>(n_types) * n_cols;
+    if (n_ph >= INT32_MAX) return fail(GLIF_EINVAL, "n_types * n_cols must be < 2^31");
+    std::vector<int64_t> ph_key(n_syn);
+    for (int64_t i = 0; i < n_syn; ++i) ph_key[i] = static_cast<int64_t>(syn_id[i]) * n_cols + col[i];
+    std::vector<int32_t> ph_ptr(n_ph + 1), ph_order(n_syn);
+    counting_sort(ph_key.data(), nullptr, n_syn, n_ph, ph_ptr.data(), ph_order.data());
+    std::vector<uint32_t> ph_pc(n_syn);
+    for (int64_t k = 0; k < n_syn; ++k) {
+        int32_t s = ph_order[k];
+        ph_pc[k] = static_cast<uint32_t>(post[s]) | (static_cast<uint32_t>(col[s] % 256) << 24);
+    }
+
+    std::vector<uint32_t> ps(n_syn), pd(n_syn);
+    std::vector<uint8_t> sid_row(n_syn);
+    int32_t max_len = 0;
+    for (int64_t c = 0; c < n_cols; ++c) max_len = std::max(max_len, col_ptr[c + 1] - col_ptr[c]);
+    for (int64_t k = 0; k < n_syn; ++k) {
+        int32_t s = order[k];
+        ps[k] = static_cast<uint32_t>(post[s]) | (static_cast<uint32_t>(syn_id[s]) << 24);
+    }
+    for (int64_t j = 0; j < n_syn; ++j) {
+        int32_t s = perm[j];
+        int64_t c = col[s];
+        uint32_t d1 = static_cast<uint32_t>(c / n_pre), pre = static_cast<uint32_t>(c % n_pre);
+        pd[j] = pre | (d1 << 24);
+        sid_row[j] = syn_id[s];
+    }
+
+    Table *t = new Table();
+    t->n_syn = n_syn;
+    t->n_post = n_post;
+    t->n_cols = n_cols;
+    t->n_slots = n_delay_slots;
+    t->n_pre = n_pre;
+    t->n_types = n_types;
+    t->n_basis = n_basis;
+    t->max_col_len = max_len;
+    t->basis_host = new float[static_cast<size_t>(n_types) * n_basis];
+    std::memcpy(t->basis_host, basis, sizeof(float) * n_types * n_basis);
+    int rc = GLIF_OK;
+    if ((rc = upload(&t->basis, basis, static_cast<size_t>(n_types) * n_basis)) ||
+        (rc = upload(&t->col_ptr, col_ptr.data(), col_ptr.size())) ||
+        (rc = upload(&t->order, order.data(), order.size())) ||
+        (rc = upload(&t->ps, ps.data(), ps.size())) ||
+        (rc = upload(&t->row_ptr, row_ptr.data(), row_ptr.size())) ||
+        (rc = upload(&t->perm, perm.data(), perm.size())) ||
+        (rc = upload(&t->pd, pd.data(), pd.size())) ||
+        (rc = upload(&t->sid_row, sid_row.data(), sid_row.size())) ||
+        (rc = upload(&t->ph_ptr, ph_ptr.data(), ph_ptr.size())) ||
+        (rc = upload(&t->ph_order, ph_order.data(), ph_order.size())) ||
+        (rc = upload(&t->ph_pc, ph_pc.data(), ph_pc.size()))) {
+        free_table(t);
+        return rc;
+    }
+    for (float **wp : {&t->w_col, &t->w_row, &t->ph_w}) {
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(wp), std::max<int64_t>(n_syn, 1) * sizeof(float));
+        if (e != hipSuccess) {
+            free_table(t);
+            return hip_fail(e, "hipMalloc(weights)");
+        }
+        if (n_syn) (void)hipMemset(*wp, 0, n_syn * sizeof(float));
+    }
+    *out = reinterpret_cast<glif_table *>(t);
+    return GLIF_OK;
+}
+
+void glif_table_destroy(glif_table *t) { free_table(reinterpret_cast<Table *>(t)); }
+
+int64_t glif_table_n_syn(const glif_table *t) {
+    return t ? reinterpret_cast<const Table *>(t)->n_syn : -1;
+}
+
+int glif_table_pre_ind(const glif_table *tt, const int32_t **order, const int32_t **row_splits) {
+    if (!tt || !order || !row_splits) return fail(GLIF_EINVAL, "NULL argument");
+    const Table *t = reinterpret_cast<const Table *>(tt);
+    *order = t->order;
+    *row_splits = t->col_ptr;
+    return GLIF_OK;
+}
+
+int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
+    if (!tt || !w) return fail(GLIF_EINVAL, "NULL argument");
+    Table *t = reinterpret_cast<Table *>(tt);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = launch_gather_f32(t->w_col, w, t->order, t->n_syn, s);
+    if (rc) return rc;
+    if ((rc = launch_gather_f32(t->ph_w, w, t->ph_order, t->n_syn, s))) return rc;
+    return launch_gather_f32(t->w_row, w, t->perm, t->n_syn, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,241 @@
+"""V1Column: the GLIF_3 recurrent cell of `v1_model_utils/models.py:450-1135` on libglif.
+
+Same constructor arguments, state tuple, per-step ``call`` and Keras-RNN-style
+rollout as the reference; the T-step loop and its BPTT run as HIP kernels on one
+stream (libglif ``glif_cell_forward`` / ``glif_cell_backward``).
+
+Differences from the reference, by necessity:
+* ``tau_basis`` and ``synaptic_basis_weights`` come from the network dictionary
+  (keys ``tau_basis`` / ``basis``) instead of ``synaptic_data/tau_basis.npy`` and the
+  network's pickle (models.py:518, 614-622).
+* The background Poisson counts are an input (``bkg`` tensors): TF's stateless
+  Poisson stream (models.py:865-887) cannot be reproduced.  ``call`` samples them
+  with torch when they are not given.
+* The refractory state is int16 (the reference uses int8, int16 above 127 steps).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import check, lib, ptr, stream_ptr
+from .ops import MODES, SynapseTable
+from .tables import build_cell_tables
+
+__all__ = ["V1Column", "RSNNRollout", "rate_loss_grad"]
+
+
+class V1Column:
+    """models.py:450 V1Column with the same keyword arguments (plus ``mode``)."""
+
+    def __init__(self, network, lgn_input=None, bkg_input=None, dt=1.0, gauss_std=0.5,
+                 dampening_factor=0.3, recurrent_dampening_factor=0.5,
+                 voltage_gradient_dampening=0.5, input_weight_scale=1.0, recurrent_weight_scale=1.0,
+                 lr_scale=1.0, spike_gradient=False, max_delay=0, batch_size=1, bkg_firing_rate=250,
+                 pseudo_gauss=False, train_recurrent=True, train_recurrent_per_type=True,
+                 train_input=False, train_noise=True, noise_seed=0, hard_reset=False,
+                 current_input=False, mode: str = "event", device="cuda"):
+        _lib.require_gpu()
+        if current_input:
+            raise NotImplementedError("current_input (firing-probability LGN input) is not on the hot path")
+        if mode not in MODES:
+            raise ValueError(f"mode must be one of {sorted(MODES)}")
+        net = network if "network" in network else dict(network=network, lgn_input=lgn_input,
+                                                          bkg_input=bkg_input)
+        self.tables = tb = build_cell_tables(net, dt=dt, max_delay=max_delay, lr_scale=lr_scale,
+                                             recurrent_weight_scale=recurrent_weight_scale,
+                                             input_weight_scale=input_weight_scale)
+        self.device = torch.device(device)
+        self.mode = mode
+        self._n_neurons, self.max_delay, self._n_syn_basis = tb.n_neurons, tb.max_delay, tb.n_basis
+        self.input_dim = tb.lgn.n_cols
+        self.n_bkg = tb.bkg.n_cols
+        self._dt, self._lr_scale = float(dt), float(lr_scale)
+        self._gauss_std, self._dampening_factor = float(gauss_std), float(dampening_factor)
+        self._recurrent_dampening = float(recurrent_dampening_factor)
+        self._voltage_gradient_dampening = float(voltage_gradient_dampening)
+        self._pseudo_gauss, self._hard_reset = bool(pseudo_gauss), bool(hard_reset)
+        self.bkg_spike_prob = bkg_firing_rate * 0.001
+        self.noise_seed = int(noise_seed)
+
+        self.recurrent_dense_shape = (tb.n_neurons, tb.max_delay * tb.n_neurons)
+        self.rec_table = SynapseTable(tb.rec.indices, tb.rec.syn_id, self.recurrent_dense_shape,
+                                      tb.basis, n_delay_slots=tb.max_delay)
+        self.lgn_table = SynapseTable(tb.lgn.indices, tb.lgn.syn_id, (tb.n_neurons, tb.lgn.n_cols),
+                                      tb.basis)
+        self.bkg_table = SynapseTable(tb.bkg.indices, tb.bkg.syn_id, (tb.n_neurons, tb.bkg.n_cols),
+                                      tb.basis)
+        dev = self.device
+        individual = bool(train_recurrent) and not bool(train_recurrent_per_type)
+        # trainable weight vectors in reference order (models.py:663-669, 725-731, 758-764)
+        self.recurrent_weight_values = torch.tensor(tb.rec.weight, device=dev).requires_grad_(
+            bool(train_recurrent))
+        self.input_weight_values = torch.tensor(tb.lgn.weight, device=dev).requires_grad_(bool(train_input))
+        self.bkg_input_weights = torch.tensor(tb.bkg.weight, device=dev).requires_grad_(bool(train_noise))
+        self._individual_training = individual
+        # sign masks for SignedConstraint (models.py:419-427)
+        self.recurrent_weight_positive = torch.tensor(tb.rec.weight >= 0, device=dev)
+        self.input_weight_positive = torch.tensor(tb.lgn.weight >= 0, device=dev)
+        self.bkg_weight_positive = torch.tensor(tb.bkg.weight >= 0, device=dev)
+
+        cfg = _lib.CellConfig(tb.n_neurons, tb.max_delay, tb.n_basis, float(dt), float(lr_scale),
+                              float(voltage_gradient_dampening), float(recurrent_dampening_factor),
+                              float(gauss_std), float(dampening_factor), int(pseudo_gauss),
+                              int(hard_reset))
+        self._keep = [np.ascontiguousarray(a) for a in (
+            tb.decay, tb.current_factor, tb.asc_decay.reshape(-1), tb.asc_amps.reshape(-1),
+            tb.t_ref_steps.astype(np.int32), tb.syn_decay, tb.psc_initial)]
+        h = C.c_void_p()
+        check(lib().glif_cell_create(C.byref(cfg), *[a.ctypes.data_as(C.c_void_p) for a in self._keep],
+                                     self.rec_table.handle, self.lgn_table.handle,
+                                     self.bkg_table.handle, C.byref(h)))
+        self.handle = h
+        self._ws = {}
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            try:
+                lib().glif_cell_destroy(h)
+            except Exception:
+                pass
+            self.handle = None
+
+    # ---- state ---------------------------------------------------------------
+    @property
+    def state_size(self):
+        N, D, nb = self._n_neurons, self.max_delay, self._n_syn_basis
+        return (N * D, N, N, N * 2, N * nb, N * nb, ())
+
+    def zero_state(self, batch_size, dtype=torch.float32):
+        """models.py:1043-1056 (r is int16 here)."""
+        B, N, D, nb, dev = batch_size, self._n_neurons, self.max_delay, self._n_syn_basis, self.device
+        return (torch.zeros((B, N * D), dtype=torch.float32, device=dev),
+                torch.zeros((B, N), dtype=torch.float32, device=dev),
+                torch.zeros((B, N), dtype=torch.int16, device=dev),
+                torch.zeros((B, N * 2), dtype=torch.float32, device=dev),
+                torch.zeros((B, N * nb), dtype=torch.float32, device=dev),
+                torch.zeros((B, N * nb), dtype=torch.float32, device=dev),
+                torch.zeros((B,), dtype=torch.int32, device=dev))
+
+    def refresh_weights(self, force: bool = False):
+        """refresh_recurrent_weight_shadow (models.py:966-976) for all three populations."""
+        self.rec_table.set_weights(self.recurrent_weight_values, force)
+        self.lgn_table.set_weights(self.input_weight_values, force)
+        self.bkg_table.set_weights(self.bkg_input_weights, force)
+
+    def workspace(self, B: int, T: int) -> torch.Tensor:
+        n = int(lib().glif_cell_workspace(self.handle, int(B), int(T)))
+        ws = self._ws.get("ws")
+        if ws is None or ws.numel() < n:
+            self._ws.clear()
+            ws = torch.empty(n, dtype=torch.uint8, device=self.device)
+            self._ws["ws"] = ws
+        return ws
+
+    # ---- forward ---------------------------------------------------------------
+    def _prep_inputs(self, lgn, bkg):
+        lgn = torch.as_tensor(lgn, device=self.device)
+        bkg = torch.as_tensor(bkg, device=self.device)
+        if lgn.dtype != torch.uint8:
+            lgn = (lgn > 0).to(torch.uint8)
+        if bkg.dtype != torch.uint8:
+            if torch.any(bkg > 255):
+                raise ValueError("background counts above 255")
+            bkg = bkg.to(torch.uint8)
+        return lgn.contiguous(), bkg.contiguous()
+
+    def rollout(self, lgn, bkg, state=None, record_z=True, record_v=True, spike_count=None,
+                mode: Optional[str] = None, ws: Optional[torch.Tensor] = None):
+        """Run T steps (the Keras RNN over `call`, models.py:1317-1322).
+
+        lgn [T, B, n_lgn] (spike where > 0), bkg [T, B, n_bkg] Poisson counts.
+        Returns (z [T, B, N] or None, v [T, B, N] or None, new_state).  The state is
+        updated in place (pass a copy to keep it)."""
+        lgn, bkg = self._prep_inputs(lgn, bkg)
+        T, B = int(lgn.shape[0]), int(lgn.shape[1])
+        if lgn.shape[2] != self.input_dim or bkg.shape[:2] != lgn.shape[:2] or bkg.shape[2] != self.n_bkg:
+            raise ValueError("input shapes do not match the network")
+        if state is None:
+            state = self.zero_state(B)
+        st = list(state)
+        for i in range(6):
+            st[i] = st[i].contiguous()
+        N = self._n_neurons
+        z = torch.empty((T, B, N), dtype=torch.float32, device=self.device) if record_z else None
+        v = torch.empty((T, B, N), dtype=torch.float32, device=self.device) if record_v else None
+        self.refresh_weights()
+        if ws is None:
+            ws = self.workspace(B, T)
+        cstate = _lib.State(*[C.c_void_p(t.data_ptr()) for t in st[:6]])
+        check(lib().glif_cell_forward(self.handle, B, T, MODES[mode or self.mode], ptr(lgn), ptr(bkg),
+                                      C.byref(cstate), ptr(z), ptr(v), ptr(spike_count), ptr(ws),
+                                      ws.numel(), stream_ptr(self.device)))
+        st[6] = st[6] + T
+        self._last = (B, T, ws)
+        return z, v, tuple(st)
+
+    def call(self, inputs, state, bkg_counts=None, constants=None):
+        """One step (models.py:1059-1135): returns ((z, v), new_state)."""
+        B = int(inputs.shape[0])
+        if bkg_counts is None:
+            g = torch.Generator(device=self.device)
+            g.manual_seed(self.noise_seed * 1000003 + int(state[6][0].item()))
+            lam = torch.full((B, self.n_bkg), self.bkg_spike_prob, device=self.device)
+            bkg_counts = torch.poisson(lam, generator=g)
+        lgn = inputs[:, :self.input_dim][None]
+        z, v, st = self.rollout(lgn, bkg_counts[None], state=[s.clone() for s in state])
+        return (z[0], v[0]), st
+
+    __call__ = call
+
+    # ---- backward ------------------------------------------------------------
+    def backward(self, gz=None, gz_neuron=None, gv=None, want=("rec", "lgn", "bkg")):
+        """BPTT through the last `rollout` (zero initial adjoint).
+
+        gz / gv: dL/dz, dL/dv [T, B, N] (or None); gz_neuron: dL/dz [N] broadcast over
+        (t, b).  Returns dict of weight gradients in reference order."""
+        B, T, ws = self._last
+        dev = self.device
+        out = {}
+        for name, table in (("rec", self.rec_table), ("lgn", self.lgn_table), ("bkg", self.bkg_table)):
+            out[name] = torch.empty(table.n_syn, dtype=torch.float32, device=dev) if name in want else None
+        prep = lambda t: None if t is None else t.detach().contiguous().float()
+        gz, gz_neuron, gv = prep(gz), prep(gz_neuron), prep(gv)
+        check(lib().glif_cell_backward(self.handle, B, T, ptr(gz), ptr(gz_neuron), ptr(gv),
+                                       ptr(out["rec"]), ptr(out["lgn"]), ptr(out["bkg"]), ptr(ws),
+                                       ws.numel(), stream_ptr(dev)))
+        return out
+
+
+class RSNNRollout(torch.autograd.Function):
+    """Autograd node over a whole rollout: weights -> (z [T,B,N], v [T,B,N])."""
+
+    @staticmethod
+    def forward(ctx, cell: V1Column, lgn, bkg, w_rec, w_lgn, w_bkg):
+        z, v, _ = cell.rollout(lgn, bkg)
+        ctx.cell = cell
+        ctx.want = tuple(n for n, w in (("rec", w_rec), ("lgn", w_lgn), ("bkg", w_bkg)) if w.requires_grad)
+        return z, v
+
+    @staticmethod
+    def backward(ctx, gz, gv):
+        g = ctx.cell.backward(gz=gz, gv=gv, want=ctx.want)
+        return None, None, None, g["rec"], g["lgn"], g["bkg"]
+
+
+def rate_loss_grad(spike_count: torch.Tensor, targets: torch.Tensor, T: int):
+    """L = mean_n (rbar_n - r*_n)^2 with rbar_n = mean_{b,t} z[b, t, n].
+
+    spike_count [B, N] int32.  Returns (L, dL/dz [N]) -- dL/dz is the same for every (t, b)."""
+    B = spike_count.shape[0]
+    N = spike_count.shape[1]
+    rbar = spike_count.sum(0).float() / float(B * T)
+    diff = rbar - targets
+    loss = (diff * diff).mean()
+    gz = diff * (2.0 / (N * B * T))
+    return loss, gz
