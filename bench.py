@@ -40,7 +40,22 @@ def _args():
     ap.add_argument("--cpu-steps", type=int, default=10,
                     help="timesteps of the CPU baseline sample (0: skip)")
     ap.add_argument("--forward-only", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (5 times): the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
+
+
+def copy_calibration(mib):
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read_per_launch": n * 4, "copy_bytes_written_per_launch": n * 4,
+                      "launches": 5}))
 
 
 def event_counts(tables, lgn, bkg, spike_count_total):
@@ -66,6 +81,9 @@ def load_traffic(name):
 
 def main():
     args = _args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU data parallelism "
                                    "is designed but not built (--gpus must be 1)"}))
