@@ -29,7 +29,9 @@ namespace glif {
 
 // ------------------------------------------------------------------ state ----
 struct CellWs {
-    float *I;
+    float *I;           // [nb][B][N]   pushed rec + LGN currents (event mode)
+    float *R, *P;       // [nb][B][N]   psc_rise, psc (receptor-major copies of the state)
+    float *A;           // [2][B][N]    asc
     uint64_t *zbits;    // [(T + D)][B][W]   slot t + D holds z_t
     uint64_t *refbits;  // [T][B][W]         r_t > 0
     float *vsave;       // [T][B][N]
@@ -65,6 +67,9 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     const int64_t BN = static_cast<int64_t>(B) * c->N;
     const int64_t nl = c->lgn->n_cols, nk = c->bkg->n_cols;
     w.I = cv.take<float>(BN * c->nb);
+    w.R = cv.take<float>(BN * c->nb);
+    w.P = cv.take<float>(BN * c->nb);
+    w.A = cv.take<float>(BN * 2);
     w.zbits = cv.take<uint64_t>(static_cast<size_t>(T + c->D) * B * c->W);
     w.refbits = cv.take<uint64_t>(static_cast<size_t>(T) * B * c->W);
     w.vsave = cv.take<float>(static_cast<size_t>(T) * BN);
@@ -171,6 +176,32 @@ __global__ void __launch_bounds__(kBlock)
     z_buf[static_cast<int64_t>(b) * k.D * k.N + static_cast<int64_t>(d - 1) * k.N + n] = z ? 1.0f : 0.0f;
 }
 
+// Reference-layout state (psc_rise/psc [B][N*nb], asc [B][N*2]) <-> the rollout's
+// receptor-major copies ([nb][B][N], [2][B][N]) so every state access of the step
+// kernel is one coalesced row.
+__global__ void __launch_bounds__(kBlock)
+    k_state_layout(float *__restrict__ R_ref, float *__restrict__ P_ref, float *__restrict__ A_ref,
+                   float *__restrict__ R, float *__restrict__ P, float *__restrict__ A, int64_t BN,
+                   int nb, int to_soa) {
+    const int64_t bn = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (bn >= BN) return;
+    for (int q = 0; q < nb; ++q) {
+        if (to_soa) {
+            R[q * BN + bn] = R_ref[bn * nb + q];
+            P[q * BN + bn] = P_ref[bn * nb + q];
+        } else {
+            R_ref[bn * nb + q] = R[q * BN + bn];
+            P_ref[bn * nb + q] = P[q * BN + bn];
+        }
+    }
+    for (int j = 0; j < 2; ++j) {
+        if (to_soa)
+            A[j * BN + bn] = A_ref[bn * 2 + j];
+        else
+            A_ref[bn * 2 + j] = A[j * BN + bn];
+    }
+}
+
 // ------------------------------------------------------------ event push ----
 struct PushArgs {
     int32_t t, D, N, B, nb, n_types, chunks_rec, chunks_lgn;
@@ -223,8 +254,8 @@ __global__ void __launch_bounds__(kBlock) k_push(PushArgs a) {
             const int32_t col = (e & static_cast<int32_t>(kLow24)) + (d - 1) * a.N;
             const int32_t lo = a.rec_colptr[col] + ch * L * kChunkIters;
             const int32_t hi = min(a.rec_colptr[col + 1], lo + L * kChunkIters);
-            push_column<L>(lane_s, lo, hi, 1u << b, MultOne{}, a.rec_ps, a.rec_w, basis_lds, a.nb, a.N,
-                           a.I);
+            push_column<L>(lane_s, lo, hi, 1u << b, MultOne{}, a.rec_ps, a.rec_w, basis_lds, a.nb, a.N, 1,
+                           BN, a.I);
         } else {
             const int64_t v = u - n_rec * a.chunks_rec;
             const int64_t it = l0 + v / a.chunks_lgn;
@@ -233,7 +264,7 @@ __global__ void __launch_bounds__(kBlock) k_push(PushArgs a) {
             const int32_t lo = a.lgn_colptr[c] + ch * L * kChunkIters;
             const int32_t hi = min(a.lgn_colptr[c + 1], lo + L * kChunkIters);
             push_column<L>(lane_s, lo, hi, a.lgn_mask[it], MultOne{}, a.lgn_ps, a.lgn_w, basis_lds,
-                           a.nb, a.N, a.I);
+                           a.nb, a.N, 1, BN, a.I);
         }
     }
 }
@@ -244,9 +275,9 @@ struct StepArgs {
     int32_t t;
     float *v;
     int16_t *r;
-    float *asc;
-    float *R;
-    float *P;
+    float *A;   // [2][B][N]
+    float *R;   // [nb][B][N]
+    float *P;   // [nb][B][N]
     const float *decay, *cf, *ad, *amp;
     const int32_t *tref;
     float *I;
@@ -282,7 +313,7 @@ struct StepArgs {
 //   V'     = (decay * (V * (1 - vgd) + V * vgd) + cf * c) - z_prev
 //   r'     = max(r + z_prev * tref - 1, 0); hard reset: V' = 0 while r' > 0
 //   z      = r' > 0 ? 0 : (V' - 1 > 0)
-template <bool DET>
+template <bool DET, int NB>
 __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
     extern __shared__ float basis_lds[];
     const CellConst &k = a.k;
@@ -292,10 +323,11 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
     const int b = static_cast<int>(gt / k.Np);
     const int n = static_cast<int>(gt % k.Np);
     const int lane = threadIdx.x & (kWave - 1);
-    const int nb = k.nb;
+    constexpr int nb = NB;
     const int t = a.t;
     bool spike = false, refr = false;
     if (n < k.N) {
+        const int64_t BN = static_cast<int64_t>(k.B) * k.N;
         const int64_t bn = static_cast<int64_t>(b) * k.N + n;
         float Irl[kMaxBasis], Ib[kMaxBasis];
         for (int q = 0; q < nb; ++q) Ib[q] = 0.0f;
@@ -319,39 +351,61 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
             }
             for (int q = 0; q < nb; ++q) Irl[q] = Ir[q] + Il[q];
         } else {
-            float *Ip = a.I + bn * nb;
             for (int q = 0; q < nb; ++q) {
-                Irl[q] = Ip[q];
-                Ip[q] = 0.0f;
+                float *Ip = a.I + q * BN + bn;
+                Irl[q] = *Ip;
+                *Ip = 0.0f;
             }
         }
+        // background: every synapse of the row, weight times the Poisson count.  A zero
+        // count adds +/-0, which leaves a sum started at +0 unchanged, so the
+        // branch-free loop equals the reference's event-only sum bit for bit.
         const uint8_t *xb = a.bkg_x + static_cast<int64_t>(b) * a.n_bkg;
-        for (int32_t j = a.bkg_row[n], je = a.bkg_row[n + 1]; j < je; ++j) {
-            const uint8_t cnt = xb[a.bkg_pd[j] & kLow24];
-            if (cnt == 0) continue;
-            const float wv = a.bkg_w[j] * static_cast<float>(cnt);
-            const float *bs = basis_lds + a.bkg_sid[j] * nb;
-            for (int r = 0; r < nb; ++r) Ib[r] = Ib[r] + wv * bs[r];
+        {
+            // 8 synapses at a time: their table entries, then their counts, are loaded
+            // together before the (in-order) accumulation
+            const int32_t j0 = a.bkg_row[n], j1 = a.bkg_row[n + 1];
+            for (int32_t jb = j0; jb < j1; jb += 8) {
+                uint32_t pd[8];
+                float wj[8];
+                int sj[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const bool ok = jb + u < j1;
+                    pd[u] = ok ? a.bkg_pd[jb + u] : 0u;
+                    wj[u] = ok ? a.bkg_w[jb + u] : 0.0f;
+                    sj[u] = ok ? a.bkg_sid[jb + u] : 0;
+                }
+                float cnt[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) cnt[u] = (jb + u < j1) ? static_cast<float>(xb[pd[u] & kLow24]) : 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (jb + u >= j1) break;
+                    const float wv = wj[u] * cnt[u];
+                    const float *bs = basis_lds + sj[u] * nb;
+#pragma unroll
+                    for (int r = 0; r < nb; ++r) Ib[r] = Ib[r] + wv * bs[r];
+                }
+            }
         }
 
         const float zp = zbit(a.zbits, t - 1 + k.D, b, k.B, k.W, n) ? 1.0f : 0.0f;
-        float *Rp = a.R + bn * nb;
-        float *Pp = a.P + bn * nb;
-        float *Ap = a.asc + bn * 2;
         float Pold[kMaxBasis];
-        for (int q = 0; q < nb; ++q) Pold[q] = Pp[q];
+        for (int q = 0; q < nb; ++q) Pold[q] = a.P[q * BN + bn];
         float sumP = Pold[0];
         for (int q = 1; q < nb; ++q) sumP = sumP + Pold[q];
-        const float A0 = Ap[0], A1 = Ap[1];
+        const float A0 = a.A[bn], A1 = a.A[BN + bn];
         const float c1 = sumP + (A0 + A1);
         for (int q = 0; q < nb; ++q) {
             const float in = (Irl[q] + Ib[q]) * k.lr;
-            const float Rold = Rp[q];
-            Rp[q] = Rold * k.sd[q] + in * k.p0[q];
-            Pp[q] = Pold[q] * k.sd[q] + k.dtsd[q] * Rold;
+            float *Rq = a.R + q * BN + bn;
+            const float Rold = *Rq;
+            *Rq = Rold * k.sd[q] + in * k.p0[q];
+            a.P[q * BN + bn] = Pold[q] * k.sd[q] + k.dtsd[q] * Rold;
         }
-        Ap[0] = a.ad[2 * n] * A0 + zp * a.amp[2 * n];
-        Ap[1] = a.ad[2 * n + 1] * A1 + zp * a.amp[2 * n + 1];
+        a.A[bn] = a.ad[2 * n] * A0 + zp * a.amp[2 * n];
+        a.A[BN + bn] = a.ad[2 * n + 1] * A1 + zp * a.amp[2 * n + 1];
         const float vv = a.v[bn];
         const float dv = vv * k.om + vv * k.vgd;
         float vn = (a.decay[n] * dv + a.cf[n] * c1) - zp;
@@ -362,7 +416,7 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
         spike = !refr && (vn - 1.0f) > 0.0f;
         a.v[bn] = vn;
         a.r[bn] = static_cast<int16_t>(rn);
-        const int64_t tbn = static_cast<int64_t>(t) * k.B * k.N + bn;
+        const int64_t tbn = static_cast<int64_t>(t) * BN + bn;
         a.vsave[tbn] = vn;
         if (a.z_out) a.z_out[tbn] = spike ? 1.0f : 0.0f;
         if (a.v_out) a.v_out[tbn] = vn;
@@ -387,6 +441,8 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
 }
 
 // --------------------------------------------------------------- adjoint ----
+constexpr int kDelayUnroll = 8;
+
 struct AdjArgs {
     CellConst k;
     int32_t t0, nw, T, ring, R;
@@ -410,6 +466,7 @@ struct AdjArgs {
 //   dy_{t-2} = (gR_{t-2} * p0) * lr_scale;  G[s][n][w*B + b] = sum_r dy_r basis[s][r]
 // dZ_s for s >= T-2 is zero (nothing downstream of I_{T-2}, I_{T-1} is observed).
 // The ticks of one window only read dZ of earlier (later-in-time) windows.
+template <int NB>
 __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
     extern __shared__ float basis_lds[];
     const CellConst &k = a.k;
@@ -421,7 +478,7 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
     const int n = static_cast<int>(gt / k.B);
     const int b = static_cast<int>(gt - static_cast<int64_t>(n) * k.B);
     const int64_t bn = static_cast<int64_t>(b) * k.N + n;
-    const int nb = k.nb;
+    constexpr int nb = NB;
     const int64_t DN = static_cast<int64_t>(k.D) * k.N;
     float gVc = a.gV[bn];
     float gP[kMaxBasis], gR[kMaxBasis];
@@ -433,11 +490,28 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
     for (int w = 0; w < a.nw; ++w) {
         const int t = a.t0 - w;
         float gz = 0.0f;
-        for (int d = k.D; d >= 1; --d) {
-            const int s = t + d;
-            if (s > a.T - 3) continue;
-            gz = gz + a.dZ[(static_cast<int64_t>(s % a.ring) * k.B + b) * DN + static_cast<int64_t>(d - 1) * k.N + n] *
-                          k.rd_scale;
+        if (k.D <= kDelayUnroll) {
+            // the D ring values are loaded together, then summed from d = D down to 1
+            float zv[kDelayUnroll];
+#pragma unroll
+            for (int d = 1; d <= kDelayUnroll; ++d) {
+                const int s = t + d;
+                zv[d - 1] = (d <= k.D && s <= a.T - 3)
+                                ? a.dZ[(static_cast<int64_t>(s % a.ring) * k.B + b) * DN +
+                                       static_cast<int64_t>(d - 1) * k.N + n]
+                                : 0.0f;
+            }
+#pragma unroll
+            for (int d = kDelayUnroll; d >= 1; --d)
+                if (d <= k.D && t + d <= a.T - 3) gz = gz + zv[d - 1] * k.rd_scale;
+        } else {
+            for (int d = k.D; d >= 1; --d) {
+                const int s = t + d;
+                if (s > a.T - 3) continue;
+                gz = gz + a.dZ[(static_cast<int64_t>(s % a.ring) * k.B + b) * DN +
+                               static_cast<int64_t>(d - 1) * k.N + n] *
+                              k.rd_scale;
+            }
         }
         const int64_t tbn = static_cast<int64_t>(t) * BN + bn;
         if (a.gz) gz = gz + a.gz[tbn];
@@ -488,16 +562,22 @@ struct ActWin {
     float *dZ;
     int64_t n_cols;
     int32_t s0, B, D, W, n_pre, ring;
-    __device__ bool on(int64_t c, int e) const {
-        const int w = e / B, b = e - w * B;
-        const int d1 = static_cast<int>(c / n_pre);
-        const int pre = static_cast<int>(c - static_cast<int64_t>(d1) * n_pre);
-        return zbit(zbits, s0 - w - (d1 + 1) + D, b, B, W, pre);
+    struct Col {
+        int32_t c, pre, slot0;  // slot0: spike-history slot of z_{s0-d}
+    };
+    __device__ Col col(int64_t c64) const {
+        const int32_t c = static_cast<int32_t>(c64);
+        const int32_t d1 = c / n_pre;
+        return Col{c, c - d1 * n_pre, s0 - (d1 + 1) + D};
     }
-    __device__ float mult(int64_t, int) const { return 1.0f; }
-    __device__ float *out(int64_t c, int e) const {
+    __device__ bool on(const Col &ci, int e) const {
         const int w = e / B, b = e - w * B;
-        return dZ + (static_cast<int64_t>((s0 - w) % ring) * B + b) * n_cols + c;
+        return zbit(zbits, ci.slot0 - w, b, B, W, ci.pre);
+    }
+    __device__ float mult(const Col &, int) const { return 1.0f; }
+    __device__ float *out(const Col &ci, int e) const {
+        const int w = e / B, b = e - w * B;
+        return dZ + (static_cast<int64_t>((s0 - w) % ring) * B + b) * n_cols + ci.c;
     }
 };
 
@@ -574,6 +654,27 @@ static void launch_bwd_in(const BwdInArgs &ia, int64_t max_units, hipStream_t s)
         hipLaunchKernelGGL(k_bwd_in<true>, grid, dim3(kBlock), 0, s, ia);
     else
         hipLaunchKernelGGL(k_bwd_in<false>, grid, dim3(kBlock), 0, s, ia);
+}
+
+template <bool DET>
+static void launch_step(const StepArgs &sa, int nb, dim3 grid, size_t lds, hipStream_t s) {
+    switch (nb) {
+#define GLIF_STEP(NB) \
+    case NB: hipLaunchKernelGGL((k_step<DET, NB>), grid, dim3(kBlock), lds, s, sa); break;
+        GLIF_STEP(1) GLIF_STEP(2) GLIF_STEP(3) GLIF_STEP(4) GLIF_STEP(5) GLIF_STEP(6) GLIF_STEP(7) GLIF_STEP(8)
+#undef GLIF_STEP
+        default: break;
+    }
+}
+
+static void launch_adj(const AdjArgs &aa, int nb, dim3 grid, size_t lds, hipStream_t s) {
+    switch (nb) {
+#define GLIF_ADJ(NB) \
+    case NB: hipLaunchKernelGGL((k_adj<NB>), grid, dim3(kBlock), lds, s, aa); break;
+        GLIF_ADJ(1) GLIF_ADJ(2) GLIF_ADJ(3) GLIF_ADJ(4) GLIF_ADJ(5) GLIF_ADJ(6) GLIF_ADJ(7) GLIF_ADJ(8)
+#undef GLIF_ADJ
+        default: break;
+    }
 }
 
 static int chunks_for(const Table *t, int L) {
@@ -700,15 +801,19 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                        w.zbits, w.rlist, w.rcount, event ? 1 : 0);
     GLIF_HIP(hipGetLastError());
     if (event && (rc = launch_fill_u32(w.I, 0u, static_cast<size_t>(B) * c->N * c->nb, s))) return rc;
+    const int64_t BNs = static_cast<int64_t>(B) * c->N;
+    hipLaunchKernelGGL(k_state_layout, dim3(ceil_div(BNs, kBlock)), dim3(kBlock), 0, s, st->psc_rise, st->psc,
+                       st->asc, w.R, w.P, w.A, BNs, c->nb, 1);
+    GLIF_HIP(hipGetLastError());
 
     const size_t lds = sizeof(float) * c->n_types * c->nb;
     StepArgs sa{};
     sa.k = k;
     sa.v = st->v;
     sa.r = st->r;
-    sa.asc = st->asc;
-    sa.R = st->psc_rise;
-    sa.P = st->psc;
+    sa.A = w.A;
+    sa.R = w.R;
+    sa.P = w.P;
     sa.decay = c->decay;
     sa.cf = c->cf;
     sa.ad = c->asc_decay;
@@ -775,12 +880,15 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                 hipLaunchKernelGGL((k_push<Lp>), dim3(push_grid), dim3(kBlock), lds, s, pa);
             }
             ProfScope p(kProfStep, s);
-            hipLaunchKernelGGL((k_step<false>), step_grid, dim3(kBlock), lds, s, sa);
+            launch_step<false>(sa, c->nb, step_grid, lds, s);
         } else {
             ProfScope p(kProfStep, s);
-            hipLaunchKernelGGL((k_step<true>), step_grid, dim3(kBlock), lds, s, sa);
+            launch_step<true>(sa, c->nb, step_grid, lds, s);
         }
     }
+    GLIF_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_state_layout, dim3(ceil_div(BNs, kBlock)), dim3(kBlock), 0, s, st->psc_rise, st->psc,
+                       st->asc, w.R, w.P, w.A, BNs, c->nb, 0);
     GLIF_HIP(hipGetLastError());
     const int64_t n_out = static_cast<int64_t>(c->D) * B * c->N;
     hipLaunchKernelGGL(k_write_zbuf, dim3(ceil_div(n_out, kBlock)), dim3(kBlock), 0, s, st->z_buf, k, T,
@@ -873,7 +981,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         aa.nw = nw;
         {
             ProfScope p(kProfAdj, s);
-            hipLaunchKernelGGL(k_adj, adj_grid, dim3(kBlock), lds, s, aa);
+            launch_adj(aa, c->nb, adj_grid, lds, s);
         }
         ca.n_elem = nw * B;
         act.s0 = s0;

@@ -53,7 +53,8 @@ struct Table {
     uint32_t *pd = nullptr;       // [n_syn]       pre | (delay - 1) << 24
     uint8_t *sid_row = nullptr;   // [n_syn]
     float *w_row = nullptr;       // [n_syn]
-    // type-phased: ordered by (syn_id, column, synapse id)
+    // type-phased: ordered by (syn_id, column, synapse id); the backward walks one
+    // synapse type at a time so the live slice of the dy projection fits the L2
     int32_t *ph_ptr = nullptr;    // [n_types * n_cols + 1]
     int32_t *ph_order = nullptr;  // [n_syn]       synapse id at position k
     uint32_t *ph_pc = nullptr;    // [n_syn]       post | (column % 256) << 24

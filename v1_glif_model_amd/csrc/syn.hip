@@ -61,10 +61,10 @@ __global__ void __launch_bounds__(kBlock)
         const uint32_t m = masks[it];
         if (COUNTS)
             push_column<L>(lane_s, col_ptr[c], col_ptr[c + 1], m, MultF32{z + c, n_cols}, ps, w,
-                           basis_lds, nb, n_post, I);
+                           basis_lds, nb, static_cast<int64_t>(n_post) * nb, nb, 1, I);
         else
             push_column<L>(lane_s, col_ptr[c], col_ptr[c + 1], m, MultOne{}, ps, w, basis_lds, nb,
-                           n_post, I);
+                           static_cast<int64_t>(n_post) * nb, nb, 1, I);
     }
 }
 
@@ -201,8 +201,8 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
                        t->basis, t->n_types, t->n_basis, w.G);
     GLIF_HIP(hipGetLastError());
     if (dw && (rc = launch_fill_u32(w.dw_col, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
-    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, Bp, t->ph_ptr, t->ph_pc, t->ph_w, w.G,
-               dz ? 1 : 0, dw ? w.dw_col : nullptr};
+    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, Bp, t->ph_ptr, t->ph_pc, t->ph_w, w.G, dz ? 1 : 0,
+               dw ? w.dw_col : nullptr};
     ActDense act{z, dz, t->n_cols, counts};
     const int LG = Bp / 4;
     const dim3 grid(ceil_div(t->n_cols * LG, kBlock));
