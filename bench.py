@@ -186,8 +186,10 @@ def main():
                      + (steps_per_launch + D) * B * words * 8 + active * 8)
         unit_desc = f"bytes per backward window of {Wwin} timesteps"
     else:
+        # per launch = one timestep's pushed events: the 8-byte table entry (post |
+        # syn_id, weight) and one 4-byte fp32 atomic each (identity basis)
         active = (e_rec + e_lgn) / max(T, 1)
-        alg_bytes = active * 8 + B * N * nb * 4 * 2
+        alg_bytes = active * 12
         unit_desc = "bytes per forward timestep"
     avg_ms = tot_ms / max(launches, 1)
     achieved = alg_bytes / (avg_ms / 1000.0) / 1e9 if avg_ms > 0 else 0.0

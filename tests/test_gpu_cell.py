@@ -123,5 +123,8 @@ def test_backward_rate_loss_per_neuron_grad():
     g1 = cell.backward(gz_neuron=torch.tensor(gn, device="cuda"))
     dense_gz = np.broadcast_to(gn, (T, B, gn.size)).copy()
     g2 = cell.backward(gz=torch.tensor(dense_gz, device="cuda"))
+    # the recurrent backward sums dz with LDS atomics, so two runs agree to fp32
+    # rounding of the summation order, not bit for bit
     for k in g1:
-        np.testing.assert_array_equal(g1[k].cpu().numpy(), g2[k].cpu().numpy())
+        a, b = g1[k].cpu().numpy(), g2[k].cpu().numpy()
+        assert np.max(np.abs(a - b)) <= 1e-6 * np.max(np.abs(b)), k

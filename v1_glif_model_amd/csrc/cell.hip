@@ -301,6 +301,8 @@ struct StepArgs {
     const uint32_t *bkg_pd;
     const uint8_t *bkg_sid;
     const float *bkg_w;
+    const uint2 *bkg_ell;  // ELL copy of the background table, or nullptr
+    int32_t bkg_ell_len;
     const uint8_t *bkg_x;  // [B][n_bkg] of step t
     int32_t n_bkg;
     const float *basis;
@@ -361,7 +363,27 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
         // count adds +/-0, which leaves a sum started at +0 unchanged, so the
         // branch-free loop equals the reference's event-only sum bit for bit.
         const uint8_t *xb = a.bkg_x + static_cast<int64_t>(b) * a.n_bkg;
-        {
+        if (a.bkg_ell) {
+            // ELL rows: entry j of every post in one coalesced 8-byte load; the padding
+            // ({pre 0, w +0}) adds +0, which leaves the sum unchanged
+            for (int32_t jb = 0; jb < a.bkg_ell_len; jb += 8) {
+                uint2 e[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    e[u] = jb + u < a.bkg_ell_len ? a.bkg_ell[static_cast<int64_t>(jb + u) * k.N + n] : make_uint2(0u, 0u);
+                float cnt[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) cnt[u] = static_cast<float>(xb[e[u].x & kLow24]);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (jb + u >= a.bkg_ell_len) break;
+                    const float wv = __uint_as_float(e[u].y) * cnt[u];
+                    const float *bs = basis_lds + (e[u].x >> 24) * nb;
+#pragma unroll
+                    for (int r = 0; r < nb; ++r) Ib[r] = Ib[r] + wv * bs[r];
+                }
+            }
+        } else {
             // 8 synapses at a time: their table entries, then their counts, are loaded
             // together before the (in-order) accumulation
             const int32_t j0 = a.bkg_row[n], j1 = a.bkg_row[n + 1];
@@ -558,6 +580,7 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
 // window of steps s0, s0-1, ..: the spike z_{s0-w-d}[b][pre] (models.py:128 on the
 // spike buffer of step s0-w); dz of that element goes to the ring slot of step s0-w.
 struct ActWin {
+    static constexpr bool kUnitMult = true;
     const uint64_t *zbits;
     float *dZ;
     int64_t n_cols;
@@ -574,7 +597,7 @@ struct ActWin {
         const int w = e / B, b = e - w * B;
         return zbit(zbits, ci.slot0 - w, b, B, W, ci.pre);
     }
-    __device__ float mult(const Col &, int) const { return 1.0f; }
+    __device__ float mult(int64_t, int) const { return 1.0f; }
     __device__ float *out(const Col &ci, int e) const {
         const int w = e / B, b = e - w * B;
         return dZ + (static_cast<int64_t>((s0 - w) % ring) * B + b) * n_cols + ci.c;
@@ -583,7 +606,7 @@ struct ActWin {
 
 template <int LG>
 __global__ void __launch_bounds__(kBlock) k_bwd_rec(ColArgs a, ActWin act) {
-    bwd_cols_lg<LG, 2>(a, act);
+    bwd_cols<LG, 2>(a, act);
 }
 
 struct BwdInArgs {
@@ -639,8 +662,8 @@ __global__ void __launch_bounds__(kBlock) k_bwd_in(BwdInArgs a) {
 }
 
 // ------------------------------------------------------------ launchers ----
-static void launch_bwd_rec(const ColArgs &ca, const ActWin &act, hipStream_t s) {
-    const int LG = ca.R / 4;
+static void launch_bwd_rec(const ColArgs &ca, int R, const ActWin &act, hipStream_t s) {
+    const int LG = R / 4;
     const dim3 grid(ceil_div(ca.n_cols * LG, kBlock));
     if (LG == 1) hipLaunchKernelGGL(k_bwd_rec<1>, grid, dim3(kBlock), 0, s, ca, act);
     else if (LG == 2) hipLaunchKernelGGL(k_bwd_rec<2>, grid, dim3(kBlock), 0, s, ca, act);
@@ -841,6 +864,8 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     sa.bkg_pd = tb->pd;
     sa.bkg_sid = tb->sid_row;
     sa.bkg_w = tb->w_row;
+    sa.bkg_ell = tb->ell_len ? tb->ell_pw : nullptr;
+    sa.bkg_ell_len = tb->ell_len;
     sa.n_bkg = static_cast<int32_t>(tb->n_cols);
     sa.basis = tr->basis;
 
@@ -923,6 +948,8 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
 
     const size_t lds = sizeof(float) * c->n_types * c->nb;
     const int Wwin = win_width(B), ring = ring_size(c), Rg = g_row(Wwin, B);
+    if (static_cast<int64_t>(c->n_types) * c->N * Rg * 4 >= (int64_t(1) << 32))
+        return fail(GLIF_ERANGE, "n_types * n_neurons * G row * 4 bytes must be < 4 GiB");
     AdjArgs aa{};
     aa.k = k;
     aa.T = T;
@@ -942,8 +969,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     aa.G = w.G;
     aa.basis = tr->basis;
 
-    ColArgs ca{tr->n_cols, c->N, c->n_types, 0, Rg, tr->ph_ptr, tr->ph_pc, tr->ph_w, w.G, 1,
-               dw_rec ? w.dw_rec : nullptr};
+    ColArgs ca{tr->n_cols, c->N, c->n_types, 0, tr->ph_ptr, tr->ph_pw, w.G, 1, dw_rec ? w.dw_rec : nullptr};
     ActWin act{w.zbits, w.dZ, tr->n_cols, 0, B, c->D, c->W, c->N, ring};
 
     BwdInArgs la{}, ka{};
@@ -987,7 +1013,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         act.s0 = s0;
         {
             ProfScope p(kProfBwdRec, s);
-            launch_bwd_rec(ca, act, s);
+            launch_bwd_rec(ca, Rg, act, s);
         }
         if (dw_lgn) {
             la.j = j;

@@ -53,12 +53,18 @@ struct Table {
     uint32_t *pd = nullptr;       // [n_syn]       pre | (delay - 1) << 24
     uint8_t *sid_row = nullptr;   // [n_syn]
     float *w_row = nullptr;       // [n_syn]
-    // type-phased: ordered by (syn_id, column, synapse id); the backward walks one
-    // synapse type at a time so the live slice of the dy projection fits the L2
+    // type-phased (backward): ordered by (syn_id, column, synapse id); the type-s
+    // synapses of column c are k in [ph_ptr[s * n_cols + c], ph_ptr[s * n_cols + c + 1])
+    // ELL copy of the post-grouped table for single-delay (input) tables whose rows
+    // pad to at most twice the synapse count: entry j of post n at j * n_post + n,
+    // {pre | syn_id << 24, weight bits}, padding {0, +0.0f}; rows keep the
+    // post-grouped (column, synapse id) order.  ell_len = 0: not built.
+    int32_t ell_len = 0;
+    uint2 *ell_pw = nullptr;      // [ell_len * n_post]
+    int32_t *ell_src = nullptr;   // [ell_len * n_post] synapse id, -1 for padding
     int32_t *ph_ptr = nullptr;    // [n_types * n_cols + 1]
     int32_t *ph_order = nullptr;  // [n_syn]       synapse id at position k
-    uint32_t *ph_pc = nullptr;    // [n_syn]       post | (column % 256) << 24
-    float *ph_w = nullptr;        // [n_syn]
+    uint2 *ph_pw = nullptr;       // [n_syn]       {post, weight bits}
     float *basis_host = nullptr;  // host copy [n_types][n_basis]
 };
 

@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(kBlock)
 
 template <int LG>
 __global__ void __launch_bounds__(kBlock) k_syn_bwd_cols(ColArgs a, ActDense act) {
-    bwd_cols_lg<LG, 2>(a, act);
+    bwd_cols<LG, 2>(a, act);
 }
 
 int sub_wave_for(const Table *t) {  // lanes per column: ~ the mean column length
@@ -190,8 +190,10 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     size_t need = glif_syn_workspace(tt, B);
     if (!ws || ws_bytes < need) return fail(GLIF_ENOMEM, "workspace too small");
     SynWs w = carve_syn(ws, t, B, nullptr);
-    ProfScope prof(kProfSynBwd, s);
     const int Bp = batch_pad(B);
+    if (static_cast<int64_t>(t->n_types) * t->n_post * Bp * 4 >= (int64_t(1) << 32))
+        return fail(GLIF_ERANGE, "n_types * n_post * padded batch * 4 bytes must be < 4 GiB");
+    ProfScope prof(kProfSynBwd, s);
     const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     int rc;
     if (B < Bp && (rc = launch_fill_u32(w.G, 0u, static_cast<size_t>(t->n_post) * t->n_types * Bp, s)))
@@ -201,19 +203,15 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
                        t->basis, t->n_types, t->n_basis, w.G);
     GLIF_HIP(hipGetLastError());
     if (dw && (rc = launch_fill_u32(w.dw_col, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
-    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, Bp, t->ph_ptr, t->ph_pc, t->ph_w, w.G, dz ? 1 : 0,
-               dw ? w.dw_col : nullptr};
+    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, t->ph_pw, w.G, dz ? 1 : 0, dw ? w.dw_col : nullptr};
     ActDense act{z, dz, t->n_cols, counts};
-    const int LG = Bp / 4;
-    const dim3 grid(ceil_div(t->n_cols * LG, kBlock));
-    if (LG == 1)
-        hipLaunchKernelGGL(k_syn_bwd_cols<1>, grid, dim3(kBlock), 0, s, ca, act);
-    else if (LG == 2)
-        hipLaunchKernelGGL(k_syn_bwd_cols<2>, grid, dim3(kBlock), 0, s, ca, act);
-    else if (LG == 4)
-        hipLaunchKernelGGL(k_syn_bwd_cols<4>, grid, dim3(kBlock), 0, s, ca, act);
-    else
-        hipLaunchKernelGGL(k_syn_bwd_cols<8>, grid, dim3(kBlock), 0, s, ca, act);
+    const dim3 grid(ceil_div(t->n_cols * (Bp / 4), kBlock));
+    switch (Bp / 4) {
+        case 1: hipLaunchKernelGGL(k_syn_bwd_cols<1>, grid, dim3(kBlock), 0, s, ca, act); break;
+        case 2: hipLaunchKernelGGL(k_syn_bwd_cols<2>, grid, dim3(kBlock), 0, s, ca, act); break;
+        case 4: hipLaunchKernelGGL(k_syn_bwd_cols<4>, grid, dim3(kBlock), 0, s, ca, act); break;
+        default: hipLaunchKernelGGL(k_syn_bwd_cols<8>, grid, dim3(kBlock), 0, s, ca, act); break;
+    }
     GLIF_HIP(hipGetLastError());
     if (dw) return launch_scatter_f32(dw, w.dw_col, t->ph_order, t->n_syn, s);
     return GLIF_OK;

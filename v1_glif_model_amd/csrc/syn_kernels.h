@@ -8,10 +8,10 @@
 //   post-grouped table (Table::row_ptr/pd/sid_row/w_row): the synapses of post n
 //     are j in [row_ptr[n], row_ptr[n+1]) in ascending (column, synapse id);
 //     pd[j] = pre | (delay - 1) << 24.
-//   type-phased table (Table::ph_ptr/ph_pc/ph_w): synapses ordered by (syn_id,
-//     column, synapse id); the type-s synapses of column c are
+//   type-phased table (Table::ph_ptr/ph_pw): synapses ordered by (syn_id, column,
+//     synapse id); the type-s synapses of column c are
 //     k in [ph_ptr[s * n_cols + c], ph_ptr[s * n_cols + c + 1]);
-//     ph_pc[k] = post | (c % 256) << 24.
+//     ph_pw[k] = {post, weight bits}.
 //   I  [B][n_post][nb]  (the reference's i_rec_flat [B*N, nb]).
 //   G  [n_types][n_post][R]: G[s][post][e] = sum_r dy[b][post][r] * basis[s][r] for
 //     element e (batch b, possibly of several timesteps), the per-synapse-type
@@ -144,29 +144,37 @@ __device__ inline void write_G(float *__restrict__ G, int64_t post, int b, int B
 }
 
 // ---- column backward (A7 + A8): dz of every column, dW of its active events -----
-// G rows hold R floats: n_elem = W*B used elements (W consecutive reverse timesteps
-// x B batch entries; element e = w*B + b), zero padding after.  A group of LG = R/4
-// lanes owns one column and walks its synapses type by type in the type-phased
-// table (U at a time: U independent table loads, then U independent row gathers);
-// lane q accumulates elements 4q..4q+3 of w * G[s][post].  One G row is one cache
-// line per synapse per W timesteps, and waves that start together work on the
-// same type, so the live part of G is one type's slice (N * R floats).  Measured on
-// MI355X this phasing halves the time against the column-grouped order, where all
-// types' rows are live at once.  Each synapse is touched by one lane group, so dW
-// needs no atomics; dz and dW accumulate in a fixed order.
+// G rows hold R floats: n_elem used elements (for the cell, W consecutive reverse
+// timesteps x B batch entries, e = w*B + b), zero padding after.  A group of
+// LG = R/4 lanes owns one column and walks its synapses type by type in the
+// type-phased table, U at a time (U independent entry loads, then U independent
+// row gathers); lane q accumulates elements 4q..4q+3 of w * G[s][post].  One G row
+// is one 64-byte request per synapse per window, and waves that start together
+// work on the same type.  Each synapse is touched by one lane group: dz and dW
+// accumulate in a fixed order (deterministic) without atomics.
+//
+// Measured on MI355X (16.5M synapses, G of 5 types x 66k posts x 64 B = 21 MB):
+// random row gathers run at ~230 G rows/s from an L2-resident slice (<= ~4 MB) and
+// at ~74 G rows/s from the whole 21 MB (Infinity Cache), and this walk lands near
+// the latter.  Tiling the table so one slice of G stays in L2 needs the waves in
+// strict lockstep; without a grid barrier the tried forms (64-column blocks by
+// phase of type x post chunk with an LDS reduction, resident grids with several
+// columns per group) were slower: their L2 hit rate stayed at 40-60% and the
+// reduction cost more than it saved.  LDS float atomics (ds_add_f32) ran at ~0.3
+// lane-ops per clock per CU, unusable for the dz sums.
 struct ColArgs {
     int64_t n_cols;
-    int32_t n_post, n_types, n_elem, R;
+    int32_t n_post, n_types, n_elem;
     const int32_t *ph_ptr;   // [n_types * n_cols + 1]
-    const uint32_t *ph_pc;   // post | (column % 256) << 24
-    const float *ph_w;
-    const float *G;          // [n_types][n_post][R]
+    const uint2 *ph_pw;      // {post, weight bits}
+    const float *G;          // [n_types][n_post][R], < 4 GiB
     int32_t want_dz;
     float *dw;               // [n_syn] type-phased order, accumulated; or nullptr
 };
 
 // Op-level activity: z [B][n_cols] dense, element e = b.
 struct ActDense {
+    static constexpr bool kUnitMult = false;
     const float *z;
     float *dz;        // [B][n_cols]
     int64_t n_cols;
@@ -174,12 +182,12 @@ struct ActDense {
     using Col = int64_t;
     __device__ Col col(int64_t c) const { return c; }
     __device__ bool on(Col c, int e) const { return z[e * n_cols + c] > 0.0f; }
-    __device__ float mult(Col c, int e) const { return counts ? z[e * n_cols + c] : 1.0f; }
+    __device__ float mult(int64_t c, int e) const { return counts ? z[e * n_cols + c] : 1.0f; }
     __device__ float *out(Col c, int e) const { return dz + e * n_cols + c; }
 };
 
 template <int LG, int U, class Act>
-__device__ inline void bwd_cols_lg(const ColArgs &a, const Act &act) {
+__device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
     constexpr int R = 4 * LG;
     const int q = threadIdx.x % LG;
     const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / LG;
@@ -193,13 +201,15 @@ __device__ inline void bwd_cols_lg(const ColArgs &a, const Act &act) {
             const int e = 4 * q + i;
             if (e < a.n_elem && act.on(ci, e)) {
                 bits |= 1u << i;
-                mult[i] = act.mult(ci, e);
+                if (!Act::kUnitMult) mult[i] = act.mult(c, e);
             }
         }
     }
     uint32_t any = bits;
 #pragma unroll
     for (int o = 1; o < LG; o <<= 1) any |= __shfl_xor(any, o, kWave);
+    const char *Gb = reinterpret_cast<const char *>(a.G) + static_cast<uint32_t>(q) * 16u;
+    const uint32_t type_bytes = static_cast<uint32_t>(a.n_post) * (R * 4u);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // the next type's segment bounds are loaded while the current type is walked
     int32_t nlo = a.ph_ptr[c], nhi = a.ph_ptr[c + 1];
@@ -210,30 +220,22 @@ __device__ inline void bwd_cols_lg(const ColArgs &a, const Act &act) {
             nlo = a.ph_ptr[pi];
             nhi = a.ph_ptr[pi + 1];
         }
-        const float *Gs = a.G + static_cast<int64_t>(s) * a.n_post * R;
+        const char *Gs = Gb + static_cast<uint32_t>(s) * type_bytes;
         for (int32_t k0 = lo; k0 < hi; k0 += U) {
-            uint32_t p[U];
-            float wk[U];
+            uint2 e[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const bool ok = k0 + u < hi;
-                p[u] = ok ? a.ph_pc[k0 + u] : 0u;
-                wk[u] = (ok && a.want_dz) ? a.ph_w[k0 + u] : 0.0f;
-            }
+            for (int u = 0; u < U; ++u) e[u] = a.ph_pw[min(k0 + u, hi - 1)];
             float4 g[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                g[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (k0 + u < hi)
-                    g[u] = reinterpret_cast<const float4 *>(Gs + static_cast<int64_t>(p[u] & kLow24) * R)[q];
-            }
+            for (int u = 0; u < U; ++u) g[u] = *reinterpret_cast<const float4 *>(Gs + e[u].x * (R * 4u));
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (k0 + u >= hi) break;  // uniform within the lane group
-                acc[0] += wk[u] * g[u].x;
-                acc[1] += wk[u] * g[u].y;
-                acc[2] += wk[u] * g[u].z;
-                acc[3] += wk[u] * g[u].w;
+                const float w = a.want_dz ? __uint_as_float(e[u].y) : 0.0f;
+                acc[0] += w * g[u].x;
+                acc[1] += w * g[u].y;
+                acc[2] += w * g[u].z;
+                acc[3] += w * g[u].w;
             }
             if (any) {  // uniform within the lane group
                 // all U partials, then their group reductions, then the loads and the

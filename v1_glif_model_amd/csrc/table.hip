@@ -37,6 +37,20 @@ __global__ void k_gather_f32(float *__restrict__ dst, const float *__restrict__ 
     for (; i < n; i += stride) dst[i] = src[idx[i]];
 }
 
+__global__ void k_gather_pair_w(uint2 *__restrict__ dst, const float *__restrict__ src,
+                                const int32_t *__restrict__ idx, int64_t n) {
+    int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (; i < n; i += stride) dst[i].y = __float_as_uint(src[idx[i]]);
+}
+
+__global__ void k_gather_ell_w(uint2 *__restrict__ dst, const float *__restrict__ src,
+                               const int32_t *__restrict__ idx, int64_t n) {
+    int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (; i < n; i += stride) dst[i].y = idx[i] >= 0 ? __float_as_uint(src[idx[i]]) : 0u;
+}
+
 __global__ void k_scatter_f32(float *__restrict__ dst, const float *__restrict__ src,
                               const int32_t *__restrict__ idx, int64_t n) {
     int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -96,7 +110,7 @@ static int upload(T **dst, const T *src, size_t n) {
 static void free_table(Table *t) {
     if (!t) return;
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
-                    t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pc, t->ph_w};
+                    t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete[] t->basis_host;
@@ -166,17 +180,18 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
     std::vector<int32_t> row_ptr(static_cast<size_t>(n_post) + 1), perm(n_syn);
     counting_sort(post, order.data(), n_syn, n_post, row_ptr.data(), perm.data());
 
-    // type-phased order: stable counting sort by syn_id * n_cols + column
+    // type-phased order for the backward: (syn_id, column, synapse id), by a stable
+    // counting sort of the column-grouped order by syn_id * n_cols + column
     const int64_t n_ph = static_cast<int64_t>(n_types) * n_cols;
     if (n_ph >= INT32_MAX) return fail(GLIF_EINVAL, "n_types * n_cols must be < 2^31");
     std::vector<int64_t> ph_key(n_syn);
     for (int64_t i = 0; i < n_syn; ++i) ph_key[i] = static_cast<int64_t>(syn_id[i]) * n_cols + col[i];
     std::vector<int32_t> ph_ptr(n_ph + 1), ph_order(n_syn);
-    counting_sort(ph_key.data(), nullptr, n_syn, n_ph, ph_ptr.data(), ph_order.data());
-    std::vector<uint32_t> ph_pc(n_syn);
+    counting_sort(ph_key.data(), order.data(), n_syn, n_ph, ph_ptr.data(), ph_order.data());
+    std::vector<uint2> ph_pw(n_syn);
     for (int64_t k = 0; k < n_syn; ++k) {
-        int32_t s = ph_order[k];
-        ph_pc[k] = static_cast<uint32_t>(post[s]) | (static_cast<uint32_t>(col[s] % 256) << 24);
+        ph_pw[k].x = static_cast<uint32_t>(post[ph_order[k]]);
+        ph_pw[k].y = 0u;  // the weight, written by glif_table_set_weights
     }
 
     std::vector<uint32_t> ps(n_syn), pd(n_syn);
@@ -195,6 +210,27 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         sid_row[j] = syn_id[s];
     }
 
+    // ELL copy (input tables: one delay slot, little padding)
+    int32_t ell_len = 0;
+    for (int32_t n = 0; n < n_post; ++n) ell_len = std::max(ell_len, row_ptr[n + 1] - row_ptr[n]);
+    if (n_delay_slots != 1 || ell_len == 0 || static_cast<int64_t>(ell_len) * n_post > 2 * n_syn) ell_len = 0;
+    std::vector<uint2> ell_pw(static_cast<size_t>(ell_len) * n_post);
+    std::vector<int32_t> ell_src(static_cast<size_t>(ell_len) * n_post);
+    for (int32_t j = 0; j < ell_len; ++j)
+        for (int32_t n = 0; n < n_post; ++n) {
+            const size_t i = static_cast<size_t>(j) * n_post + n;
+            const int32_t r = row_ptr[n] + j;
+            if (r < row_ptr[n + 1]) {
+                const int32_t sidx = perm[r];
+                ell_pw[i].x = static_cast<uint32_t>(col[sidx]) | (static_cast<uint32_t>(syn_id[sidx]) << 24);
+                ell_src[i] = sidx;
+            } else {
+                ell_pw[i].x = 0u;
+                ell_src[i] = -1;
+            }
+            ell_pw[i].y = 0u;
+        }
+
     Table *t = new Table();
     t->n_syn = n_syn;
     t->n_post = n_post;
@@ -204,6 +240,7 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
     t->n_types = n_types;
     t->n_basis = n_basis;
     t->max_col_len = max_len;
+    t->ell_len = ell_len;
     t->basis_host = new float[static_cast<size_t>(n_types) * n_basis];
     std::memcpy(t->basis_host, basis, sizeof(float) * n_types * n_basis);
     int rc = GLIF_OK;
@@ -217,11 +254,13 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         (rc = upload(&t->sid_row, sid_row.data(), sid_row.size())) ||
         (rc = upload(&t->ph_ptr, ph_ptr.data(), ph_ptr.size())) ||
         (rc = upload(&t->ph_order, ph_order.data(), ph_order.size())) ||
-        (rc = upload(&t->ph_pc, ph_pc.data(), ph_pc.size()))) {
+        (rc = upload(&t->ph_pw, ph_pw.data(), ph_pw.size())) ||
+        (ell_len && (rc = upload(&t->ell_pw, ell_pw.data(), ell_pw.size()))) ||
+        (ell_len && (rc = upload(&t->ell_src, ell_src.data(), ell_src.size())))) {
         free_table(t);
         return rc;
     }
-    for (float **wp : {&t->w_col, &t->w_row, &t->ph_w}) {
+    for (float **wp : {&t->w_col, &t->w_row}) {
         hipError_t e = hipMalloc(reinterpret_cast<void **>(wp), std::max<int64_t>(n_syn, 1) * sizeof(float));
         if (e != hipSuccess) {
             free_table(t);
@@ -253,7 +292,17 @@ int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = launch_gather_f32(t->w_col, w, t->order, t->n_syn, s);
     if (rc) return rc;
-    if ((rc = launch_gather_f32(t->ph_w, w, t->ph_order, t->n_syn, s))) return rc;
+    if (t->n_syn) {
+        hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(t->n_syn)), dim3(kBlock), 0, s, t->ph_pw, w,
+                           t->ph_order, t->n_syn);
+        GLIF_HIP(hipGetLastError());
+    }
+    if (t->ell_len) {
+        const int64_t n_ell = static_cast<int64_t>(t->ell_len) * t->n_post;
+        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(n_ell)), dim3(kBlock), 0, s, t->ell_pw, w, t->ell_src,
+                           n_ell);
+        GLIF_HIP(hipGetLastError());
+    }
     return launch_gather_f32(t->w_row, w, t->perm, t->n_syn, s);
 }
 
