@@ -225,6 +225,10 @@ __device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
             uint2 e[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) e[u] = a.ph_pw[min(k0 + u, hi - 1)];
+            // an active column's dW values travel with the entries (no extra round trip)
+            float old[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) old[u] = (any && q == 0 && k0 + u < hi) ? a.dw[k0 + u] : 0.0f;
             float4 g[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) g[u] = *reinterpret_cast<const float4 *>(Gs + e[u].x * (R * 4u));
@@ -238,8 +242,8 @@ __device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
                 acc[3] += w * g[u].w;
             }
             if (any) {  // uniform within the lane group
-                // all U partials, then their group reductions, then the loads and the
-                // stores of the U (distinct, group-owned) dW entries
+                // all U partials, then their group reductions, then the stores of the
+                // U (distinct, group-owned) dW entries
                 float pp[U];
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
@@ -255,9 +259,6 @@ __device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
                     for (int u = 0; u < U; ++u) pp[u] += __shfl_xor(pp[u], o, kWave);
                 }
                 if (q == 0) {
-                    float old[U];
-#pragma unroll
-                    for (int u = 0; u < U; ++u) old[u] = (k0 + u < hi) ? a.dw[k0 + u] : 0.0f;
 #pragma unroll
                     for (int u = 0; u < U; ++u)
                         if (k0 + u < hi) a.dw[k0 + u] = old[u] + pp[u];
