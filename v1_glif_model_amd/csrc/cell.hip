@@ -34,6 +34,8 @@ struct CellWs {
     float *A;           // [2][B][N]    asc
     uint64_t *zbits;    // [(T + D)][B][W]   slot t + D holds z_t
     uint64_t *refbits;  // [T][B][W]         r_t > 0
+    uint32_t *zmask;    // [(T + D)][N]      bit b: z_t[b][n] (slot t + D), deterministic pull
+    uint32_t *lmask;    // [T][n_lgn]        bit b: LGN input x_t[b][pre] > 0
     float *vsave;       // [T][B][N]
     int32_t *rlist;     // [(D + 1)][B * N]  active (b << 24 | n) of step s in slot (s + D) % (D + 1)
     int32_t *rcount;    // [D + 1]
@@ -72,6 +74,8 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.A = cv.take<float>(BN * 2);
     w.zbits = cv.take<uint64_t>(static_cast<size_t>(T + c->D) * B * c->W);
     w.refbits = cv.take<uint64_t>(static_cast<size_t>(T) * B * c->W);
+    w.zmask = cv.take<uint32_t>(static_cast<size_t>(T + c->D) * c->N);
+    w.lmask = cv.take<uint32_t>(static_cast<size_t>(T) * nl);
     w.vsave = cv.take<float>(static_cast<size_t>(T) * BN);
     w.rlist = cv.take<int32_t>(static_cast<size_t>(c->D + 1) * BN);
     w.rcount = cv.take<int32_t>(c->D + 1);
@@ -140,7 +144,8 @@ __device__ inline bool zbit(const uint64_t *zbits, int slot, int b, int B, int W
 // the active lists of steps -1..-D.
 __global__ void __launch_bounds__(kBlock)
     k_init_history(const float *__restrict__ z_buf, CellConst k, uint64_t *__restrict__ zbits,
-                   int32_t *__restrict__ rlist, int32_t *__restrict__ rcount, int event) {
+                   int32_t *__restrict__ rlist, int32_t *__restrict__ rcount, int event,
+                   uint32_t *__restrict__ zmask) {
     const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t per_slot = static_cast<int64_t>(k.B) * k.Np;
     if (gt >= per_slot * k.D) return;
@@ -160,6 +165,140 @@ __global__ void __launch_bounds__(kBlock)
             const int rank = __popcll(bits & ((1ull << lane) - 1ull));
             rlist[static_cast<int64_t>(slot) * k.B * k.N + base + rank] = (b << 24) | n;
         }
+    }
+    if (zmask && z) atomicOr(zmask + static_cast<int64_t>(slot) * k.N + n, 1u << b);
+}
+
+// lmask[t][pre] = batch mask of the LGN inputs x_t[b][pre] > 0.
+__global__ void __launch_bounds__(kBlock)
+    k_lgn_mask(const uint8_t *__restrict__ x, int T, int B, int32_t n_in, uint32_t *__restrict__ lmask) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(T) * n_in) return;
+    const int64_t t = i / n_in, pre = i % n_in;
+    uint32_t m = 0;
+    for (int b = 0; b < B; ++b)
+        if (x[(t * B + b) * n_in + pre] > 0) m |= 1u << b;
+    lmask[i] = m;
+}
+
+// ------------------------------------------------------ deterministic pull ----
+// The currents of step t in the reference's order (A6, models.py:141-169 and
+// 841-857 summed as TF's CPU UnsortedSegmentSum meets the events): per (b, post, r)
+// from +0, the recurrent events in ascending (column, synapse id) of the post row,
+// the LGN events likewise, then I = rec + lgn (the background is added by the step
+// kernel).  One half-wave (32 lanes) per post row: the lanes test 32 consecutive
+// row entries at once (coalesced; one 4-byte batch mask per entry gives every
+// batch's spike bit), a ballot finds the active ones, and the active entries are
+// added one by one in row order into accumulator lanes, lane a = b * nb + r (+32g).
+// Only the adds are sequential; at a few Hz ~2.5% of the entries are active.
+struct PullArgs {
+    int32_t t, N, B, D, nb, n_types, n_lgn;
+    const uint32_t *zmask, *lmask;
+    const int32_t *rec_row;
+    const uint32_t *rec_pd;  // pre | (delay - 1) << 24
+    const uint8_t *rec_sid;
+    const float *rec_w;
+    const int32_t *lgn_row;
+    const uint32_t *lgn_pd;
+    const uint8_t *lgn_sid;
+    const float *lgn_w;
+    const float *basis;
+    float *I;  // [nb][B][N]
+};
+
+template <int G, bool REC>
+__device__ inline void pull_row(const PullArgs &a, const float *basis_lds, int lane32, int half, int32_t j0,
+                                int32_t j1, float (&acc)[G]) {
+    constexpr int UC = 4;  // chunks of 32 entries whose loads are issued together
+    const uint32_t *pd = REC ? a.rec_pd : a.lgn_pd;
+    const uint8_t *sid = REC ? a.rec_sid : a.lgn_sid;
+    const float *w = REC ? a.rec_w : a.lgn_w;
+    const int BNB = a.B * a.nb;
+    for (int32_t base = j0; base < j1; base += 32 * UC) {
+        uint32_t e[UC], m[UC];
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int32_t j = base + 32 * u + lane32;
+            e[u] = j < j1 ? pd[j] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int32_t j = base + 32 * u + lane32;
+            m[u] = 0u;
+            if (j < j1) {
+                if (REC) {
+                    const int d = static_cast<int>(e[u] >> 24) + 1;
+                    m[u] = a.zmask[static_cast<int64_t>(a.t - d + a.D) * a.N + (e[u] & kLow24)];
+                } else {
+                    m[u] = a.lmask[static_cast<int64_t>(a.t) * a.n_lgn + (e[u] & kLow24)];
+                }
+            }
+        }
+        // the active lanes fetch their weight and type before the ordered adds
+        float wj[UC];
+        int sj[UC];
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int32_t j = base + 32 * u + lane32;
+            wj[u] = m[u] ? w[j] : 0.0f;
+            sj[u] = m[u] ? sid[j] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            uint32_t act = static_cast<uint32_t>(__ballot(m[u] != 0u) >> (32 * half));
+            while (act) {
+                const int src = __ffs(act) - 1 + 32 * half;
+                act &= act - 1u;
+                const uint32_t mm = static_cast<uint32_t>(__shfl(static_cast<int>(m[u]), src, kWave));
+                const float wv = __shfl(wj[u], src, kWave);
+                const int sv = __shfl(sj[u], src, kWave);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const int ai = lane32 + 32 * g;
+                    if (ai < BNB) {
+                        const int b = ai / a.nb, r = ai - b * a.nb;
+                        if ((mm >> b) & 1u) acc[g] = acc[g] + wv * basis_lds[sv * a.nb + r];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int G>
+__global__ void __launch_bounds__(kBlock) k_pull(PullArgs a) {
+    extern __shared__ float basis_lds[];
+    load_basis_lds(basis_lds, a.basis, a.n_types * a.nb);
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / 32;
+    const int lane32 = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
+    // a half-wave past the last row runs the (empty) loops beside its partner half
+    const bool live = row < a.N;
+    const int32_t n = live ? static_cast<int32_t>(row) : 0;
+    float ar[G], al[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) ar[g] = al[g] = 0.0f;
+    pull_row<G, true>(a, basis_lds, lane32, half, live ? a.rec_row[n] : 0, live ? a.rec_row[n + 1] : 0, ar);
+    pull_row<G, false>(a, basis_lds, lane32, half, live ? a.lgn_row[n] : 0, live ? a.lgn_row[n + 1] : 0, al);
+    if (!live) return;
+    const int64_t BN = static_cast<int64_t>(a.B) * a.N;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int ai = lane32 + 32 * g;
+        if (ai < a.B * a.nb) {
+            const int b = ai / a.nb, r = ai - b * a.nb;
+            a.I[r * BN + static_cast<int64_t>(b) * a.N + n] = ar[g] + al[g];
+        }
+    }
+}
+
+static void launch_pull(const PullArgs &pa, size_t lds, hipStream_t s) {
+    const int G = (pa.B * pa.nb + 31) / 32;
+    const dim3 grid(ceil_div(static_cast<int64_t>(pa.N) * 32, kBlock));
+    switch (G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8) {
+        case 1: hipLaunchKernelGGL(k_pull<1>, grid, dim3(kBlock), lds, s, pa); break;
+        case 2: hipLaunchKernelGGL(k_pull<2>, grid, dim3(kBlock), lds, s, pa); break;
+        case 4: hipLaunchKernelGGL(k_pull<4>, grid, dim3(kBlock), lds, s, pa); break;
+        default: hipLaunchKernelGGL(k_pull<8>, grid, dim3(kBlock), lds, s, pa); break;
     }
 }
 
@@ -283,6 +422,7 @@ struct StepArgs {
     float *I;
     uint64_t *zbits;
     uint64_t *refbits;
+    uint32_t *zmask;
     float *vsave;
     float *z_out, *v_out;
     int32_t *spike_count;
@@ -333,30 +473,12 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
         const int64_t bn = static_cast<int64_t>(b) * k.N + n;
         float Irl[kMaxBasis], Ib[kMaxBasis];
         for (int q = 0; q < nb; ++q) Ib[q] = 0.0f;
-        if (DET) {
-            float Ir[kMaxBasis], Il[kMaxBasis];
-            for (int q = 0; q < nb; ++q) Ir[q] = Il[q] = 0.0f;
-            for (int32_t j = a.rec_row[n], je = a.rec_row[n + 1]; j < je; ++j) {
-                const uint32_t q = a.rec_pd[j];
-                const int d = static_cast<int>(q >> 24) + 1;
-                if (!zbit(a.zbits, t - d + k.D, b, k.B, k.W, static_cast<int>(q & kLow24))) continue;
-                const float wv = a.rec_w[j];
-                const float *bs = basis_lds + a.rec_sid[j] * nb;
-                for (int r = 0; r < nb; ++r) Ir[r] = Ir[r] + wv * bs[r];
-            }
-            const uint8_t *xl = a.lgn_x + static_cast<int64_t>(b) * a.n_lgn;
-            for (int32_t j = a.lgn_row[n], je = a.lgn_row[n + 1]; j < je; ++j) {
-                if (xl[a.lgn_pd[j] & kLow24] == 0) continue;
-                const float wv = a.lgn_w[j];
-                const float *bs = basis_lds + a.lgn_sid[j] * nb;
-                for (int r = 0; r < nb; ++r) Il[r] = Il[r] + wv * bs[r];
-            }
-            for (int q = 0; q < nb; ++q) Irl[q] = Ir[q] + Il[q];
-        } else {
+        {
+            // the pushed (event) or pulled (deterministic) rec + LGN currents
             for (int q = 0; q < nb; ++q) {
                 float *Ip = a.I + q * BN + bn;
                 Irl[q] = *Ip;
-                *Ip = 0.0f;
+                if (!DET) *Ip = 0.0f;
             }
         }
         // background: every synapse of the row, weight times the Poisson count.  A zero
@@ -443,6 +565,7 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
         if (a.z_out) a.z_out[tbn] = spike ? 1.0f : 0.0f;
         if (a.v_out) a.v_out[tbn] = vn;
         if (a.spike_count && spike) a.spike_count[bn] += 1;
+        if (DET && spike) atomicOr(a.zmask + static_cast<int64_t>(t + k.D) * k.N + n, 1u << b);
     }
     const uint64_t zb = __ballot(spike), rb = __ballot(refr);
     const int64_t word = static_cast<int64_t>(b) * k.W + (n >> 6);
@@ -820,8 +943,9 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     // spike history of the initial state
     if ((rc = launch_fill_u32(w.rcount, 0u, c->D + 1, s))) return rc;
     const int64_t n_init = static_cast<int64_t>(c->D) * B * c->Np;
+    if (!event && (rc = launch_fill_u32(w.zmask, 0u, static_cast<size_t>(T + c->D) * c->N, s))) return rc;
     hipLaunchKernelGGL(k_init_history, dim3(ceil_div(n_init, kBlock)), dim3(kBlock), 0, s, st->z_buf, k,
-                       w.zbits, w.rlist, w.rcount, event ? 1 : 0);
+                       w.zbits, w.rlist, w.rcount, event ? 1 : 0, event ? nullptr : w.zmask);
     GLIF_HIP(hipGetLastError());
     if (event && (rc = launch_fill_u32(w.I, 0u, static_cast<size_t>(B) * c->N * c->nb, s))) return rc;
     const int64_t BNs = static_cast<int64_t>(B) * c->N;
@@ -845,6 +969,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     sa.I = w.I;
     sa.zbits = w.zbits;
     sa.refbits = w.refbits;
+    sa.zmask = w.zmask;
     sa.vsave = w.vsave;
     sa.z_out = z_out;
     sa.v_out = v_out;
@@ -894,6 +1019,34 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     const int push_grid = 2048;
     const dim3 step_grid(ceil_div(static_cast<int64_t>(B) * c->Np, kBlock));
 
+    PullArgs pl{};
+    if (!event) {
+        pl.N = c->N;
+        pl.B = B;
+        pl.D = c->D;
+        pl.nb = c->nb;
+        pl.n_types = c->n_types;
+        pl.n_lgn = static_cast<int32_t>(tl->n_cols);
+        pl.zmask = w.zmask;
+        pl.lmask = w.lmask;
+        pl.rec_row = tr->row_ptr;
+        pl.rec_pd = tr->pd;
+        pl.rec_sid = tr->sid_row;
+        pl.rec_w = tr->w_row;
+        pl.lgn_row = tl->row_ptr;
+        pl.lgn_pd = tl->pd;
+        pl.lgn_sid = tl->sid_row;
+        pl.lgn_w = tl->w_row;
+        pl.basis = tr->basis;
+        pl.I = w.I;
+        const int64_t n_lm = static_cast<int64_t>(T) * tl->n_cols;
+        if (n_lm > 0) {
+            hipLaunchKernelGGL(k_lgn_mask, dim3(ceil_div(n_lm, kBlock)), dim3(kBlock), 0, s, lgn, T, B,
+                               static_cast<int32_t>(tl->n_cols), w.lmask);
+            GLIF_HIP(hipGetLastError());
+        }
+    }
+
     for (int t = 0; t < T; ++t) {
         sa.t = t;
         sa.lgn_x = lgn + static_cast<int64_t>(t) * B * tl->n_cols;
@@ -907,6 +1060,11 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
             ProfScope p(kProfStep, s);
             launch_step<false>(sa, c->nb, step_grid, lds, s);
         } else {
+            pl.t = t;
+            {
+                ProfScope p(kProfPush, s);
+                launch_pull(pl, lds, s);
+            }
             ProfScope p(kProfStep, s);
             launch_step<true>(sa, c->nb, step_grid, lds, s);
         }
