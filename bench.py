@@ -34,7 +34,10 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", type=int, default=2, help="benchmark configuration (2: fwd+BPTT)")
+    ap.add_argument("--config", type=int, default=2,
+                    help="benchmark configuration: 2 fwd+BPTT (default), 1 or 3 forward, 4 the firing-rate "
+                         "sweep of the event push against the deterministic row pull (B=32)")
+    ap.add_argument("--rates", default="1,5,20,50", help="config 4: target mean rates in Hz")
     ap.add_argument("--mode", default="event", choices=["event", "deterministic"])
     ap.add_argument("--seq-len", type=int, default=None)
     ap.add_argument("--cpu-steps", type=int, default=10,
@@ -79,10 +82,128 @@ def load_traffic(name):
         return json.load(f)
 
 
+def sweep_rates(args):
+    """Config 4: forward throughput of the event push (K2) and the deterministic row pull
+    (K6) at several mean firing rates.  One global factor scales all three weight
+    populations; it is set per target rate by bisection in log space on short rollouts
+    (the achieved rate of the timed rollout is reported)."""
+    import numpy as np
+    import torch
+    from v1_glif_model_amd import _lib
+    from v1_glif_model_amd import synthetic as sy
+    from v1_glif_model_amd.models import V1Column
+
+    cfg = sy.config(4)
+    T = args.seq_len or cfg.seq_len
+    B = cfg.batch
+    net = sy.make_network(cfg, seed=0)
+    lgn_np, bkg_np = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
+    cell = V1Column(net, mode="event", gauss_std=0.5, dampening_factor=0.5, pseudo_gauss=True)
+    tb = cell.tables
+    N, S = tb.n_neurons, tb.rec.n_syn
+    dev = cell.device
+    lgn = torch.tensor(lgn_np, device=dev)
+    bkg = torch.tensor(bkg_np, device=dev)
+    ws_all = (cell.recurrent_weight_values, cell.input_weight_values, cell.bkg_input_weights)
+    base = [w.detach().clone() for w in ws_all]
+    sc = torch.zeros((B, N), dtype=torch.int32, device=dev)
+
+    def set_scale(f):
+        with torch.no_grad():
+            for w, b0 in zip(ws_all, base):
+                w.copy_(b0 * f)
+        cell.refresh_weights(force=True)
+
+    def rate_hz(f, Tp):
+        set_scale(f)
+        sc.zero_()
+        cell.rollout(lgn[:Tp], bkg[:Tp], record_z=False, record_v=False, spike_count=sc,
+                     mode="deterministic")
+        torch.cuda.synchronize()
+        return float(sc.sum().item()) / (B * N * Tp) * 1000.0
+
+    def find_scale(target, Tp=T):   # the whole rollout: the rate ramps up from rest
+        lo, hi = None, None
+        f = 1.0
+        r = rate_hz(f, Tp)
+        for _ in range(10):   # bracket
+            if r < target:
+                lo = (f, r)
+                if hi is not None:
+                    break
+                f *= 2.0
+            else:
+                hi = (f, r)
+                if lo is not None:
+                    break
+                f *= 0.5
+            r = rate_hz(f, Tp)
+        if lo is None or hi is None:
+            return f
+        for _ in range(7):   # bisect in log space
+            f = float(np.sqrt(lo[0] * hi[0]))
+            r = rate_hz(f, Tp)
+            if r < target:
+                lo = (f, r)
+            else:
+                hi = (f, r)
+        return float(np.sqrt(lo[0] * hi[0]))
+
+    def timed(mode, reps=2):
+        ws = cell.workspace(B, T)
+        out = []
+        for i in range(reps + 1):
+            st = cell.zero_state(B)
+            sc.zero_()
+            _lib.prof_enable(list(_lib.PROF_KINDS) if i == reps else [])
+            _lib.prof_collect()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            cell.rollout(lgn, bkg, state=st, record_z=False, record_v=False, spike_count=sc, mode=mode, ws=ws)
+            torch.cuda.synchronize()
+            if i > 0:
+                out.append((time.perf_counter() - t0) * 1000.0 / T)
+        prof = _lib.prof_collect()
+        _lib.prof_enable([])
+        rate = float(sc.sum().item()) / (B * N * T) * 1000.0
+        return min(out), rate, {k: round(v[0] / T * 1000.0, 2) for k, v in prof.items()}
+
+    rows = []
+    for target in [float(x) for x in args.rates.split(",") if x]:
+        f = find_scale(target)
+        set_scale(f)
+        ev_ms, ev_rate, ev_k = timed("event")
+        pl_ms, pl_rate, pl_k = timed("deterministic")
+        events = ev_rate / 1000.0 * B * S   # recurrent synaptic events per step
+        rows.append({"target_hz": target, "weight_factor": round(f, 4), "rate_hz": round(ev_rate, 3),
+                     "event_ms_per_step": round(ev_ms, 4), "pull_ms_per_step": round(pl_ms, 4),
+                     "event_kernel_us_per_step": ev_k, "pull_kernel_us_per_step": pl_k,
+                     "rec_events_per_step": round(events),
+                     # K2 bytes: 8-byte entry + one 4-byte atomic per event; K6: every
+                     # post-row entry (4 bytes) + the active entries' weight and type (5)
+                     "event_push_GBps": round(events * 12 / (ev_k.get("push", 1e9) * 1e-6) / 1e9, 1),
+                     "pull_GBps": round((S * 4 + events * 5) / (pl_k.get("push", 1e9) * 1e-6) / 1e9, 1)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    best5 = min((r for r in rows), key=lambda r: abs(r["target_hz"] - 5.0)) if rows else None
+    value = B * N / (min(best5["event_ms_per_step"], best5["pull_ms_per_step"]) / 1000.0) if best5 else 0.0
+    print(json.dumps({
+        "metric": "forward neuron-timesteps/s (66k neurons, B=32, T=500) at the ~5 Hz point; sweep over rates",
+        "value": round(value, 1), "unit": "neuron-timesteps/s", "n_gpus": 1, "steps": 2, "warmup": 1,
+        "ms_per_step": min(best5["event_ms_per_step"], best5["pull_ms_per_step"]) if best5 else None,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"config 4: {N} GLIF_3 neurons, {S} recurrent synapses, B={B}, T={T}, "
+                               "modulated LGN, forward; event push (K2) vs deterministic row pull (K6)",
+                   "neurons": N, "recurrent_synapses": S, "batch": B, "seq_len": T},
+        "sweep": rows}))
+
+
 def main():
     args = _args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.config == 4 and args.gpus == 1:
+        sweep_rates(args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU data parallelism "
@@ -95,6 +216,8 @@ def main():
     from v1_glif_model_amd.models import V1Column, rate_loss_grad
 
     cfg = sy.config(args.config)
+    if args.config in (0, 1, 3):
+        args.forward_only = True   # forward workloads
     T = args.seq_len or cfg.seq_len
     B = cfg.batch
     t_gen = time.time()
