@@ -611,17 +611,37 @@ struct AdjArgs {
 //   dy_{t-2} = (gR_{t-2} * p0) * lr_scale;  G[s][n][w*B + b] = sum_r dy_r basis[s][r]
 // dZ_s for s >= T-2 is zero (nothing downstream of I_{T-2}, I_{T-1} is observed).
 // The ticks of one window only read dZ of earlier (later-in-time) windows.
-template <int NB>
+// STAGE: a workgroup takes nr = kBlock / B neurons x all B batch entries (thread
+// b * nr + i -> (b, n0 + i): every [B][N] access is a few contiguous runs) and keeps
+// its G rows in LDS until the window's ticks are done, then writes whole rows.
+// Otherwise: thread per (n, b), batch fastest, G written in place.
+template <int NB, bool STAGE>
 __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
-    extern __shared__ float basis_lds[];
+    extern __shared__ float lds_f[];
+    float *basis_lds = lds_f;
     const CellConst &k = a.k;
     load_basis_lds(basis_lds, a.basis, k.n_types * k.nb);
-    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t BN = static_cast<int64_t>(k.B) * k.N;
-    if (gt >= BN) return;
-    // batch fastest: neighbouring lanes write neighbouring G entries
-    const int n = static_cast<int>(gt / k.B);
-    const int b = static_cast<int>(gt - static_cast<int64_t>(n) * k.B);
+    int n, b;
+    float *Gl = nullptr;
+    const int nr = kBlock / k.B;
+    const int32_t n0 = static_cast<int32_t>(blockIdx.x) * nr;
+    if (STAGE) {
+        Gl = lds_f + k.n_types * k.nb;
+        const int rows = k.n_types * nr * a.R;
+        for (int i = threadIdx.x; i < rows; i += blockDim.x) Gl[i] = 0.0f;
+        __syncthreads();
+        b = static_cast<int>(threadIdx.x) / nr;
+        n = n0 + static_cast<int>(threadIdx.x) - b * nr;
+    } else {
+        const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+        // batch fastest: neighbouring lanes write neighbouring G entries
+        n = static_cast<int>(gt / k.B);
+        b = static_cast<int>(gt - static_cast<int64_t>(n) * k.B);
+    }
+    const bool live = STAGE ? (b < k.B && n < k.N) : (static_cast<int64_t>(n) * k.B + b < BN);
+    if (!STAGE && !live) return;
+    if (live) {
     const int64_t bn = static_cast<int64_t>(b) * k.N + n;
     constexpr int nb = NB;
     const int64_t DN = static_cast<int64_t>(k.D) * k.N;
@@ -688,13 +708,27 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
             const float *bs = basis_lds + s * nb;
             float g = dy[0] * bs[0];
             for (int r = 1; r < nb; ++r) g = g + dy[r] * bs[r];
-            a.G[(static_cast<int64_t>(s) * k.N + n) * a.R + e] = g;
+            if (STAGE)
+                Gl[(s * nr + (n - n0)) * a.R + e] = g;
+            else
+                a.G[(static_cast<int64_t>(s) * k.N + n) * a.R + e] = g;
         }
     }
     a.gV[bn] = gVc;
     for (int q = 0; q < nb; ++q) {
         a.gP[static_cast<int64_t>(q) * BN + bn] = gP[q];
         a.gR[static_cast<int64_t>(q) * BN + bn] = gR[q];
+    }
+    }  // live
+    if (STAGE) {
+        __syncthreads();
+        // whole G rows of this workgroup's neurons (padding elements stay zero)
+        const int nn = min(nr, k.N - n0);
+        const int per_type = nn * a.R;
+        for (int i = threadIdx.x; i < k.n_types * per_type; i += blockDim.x) {
+            const int s = i / per_type, rem = i - s * per_type;
+            a.G[(static_cast<int64_t>(s) * k.N + n0) * a.R + rem] = Gl[s * nr * a.R + rem];
+        }
     }
 }
 
@@ -813,10 +847,26 @@ static void launch_step(const StepArgs &sa, int nb, dim3 grid, size_t lds, hipSt
     }
 }
 
-static void launch_adj(const AdjArgs &aa, int nb, dim3 grid, size_t lds, hipStream_t s) {
+constexpr size_t kAdjStageLds = 64 * 1024;  // LDS budget of the staged adjoint
+
+static size_t adj_stage_lds(const CellConst &k, int R) {
+    const int nr = kBlock / k.B;
+    return sizeof(float) * (static_cast<size_t>(k.n_types) * k.nb + static_cast<size_t>(k.n_types) * nr * R);
+}
+
+static void launch_adj(const AdjArgs &aa, int nb, size_t lds, hipStream_t s) {
+    const CellConst &k = aa.k;
+    const size_t slds = adj_stage_lds(k, aa.R);
+    const bool stage = slds <= kAdjStageLds;
+    const dim3 grid = stage ? dim3(ceil_div(k.N, kBlock / k.B))
+                            : dim3(ceil_div(static_cast<int64_t>(k.B) * k.N, kBlock));
+    const size_t use = stage ? slds : lds;
     switch (nb) {
-#define GLIF_ADJ(NB) \
-    case NB: hipLaunchKernelGGL((k_adj<NB>), grid, dim3(kBlock), lds, s, aa); break;
+#define GLIF_ADJ(NB)                                                                              \
+    case NB:                                                                                      \
+        if (stage) hipLaunchKernelGGL((k_adj<NB, true>), grid, dim3(kBlock), use, s, aa);         \
+        else hipLaunchKernelGGL((k_adj<NB, false>), grid, dim3(kBlock), use, s, aa);              \
+        break;
         GLIF_ADJ(1) GLIF_ADJ(2) GLIF_ADJ(3) GLIF_ADJ(4) GLIF_ADJ(5) GLIF_ADJ(6) GLIF_ADJ(7) GLIF_ADJ(8)
 #undef GLIF_ADJ
         default: break;
@@ -1156,7 +1206,6 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     const int64_t lgn_units = tl->n_cols * static_cast<int64_t>(la.chunks);
     const int64_t bkg_units = tb->n_cols * static_cast<int64_t>(ka.chunks);
 
-    const dim3 adj_grid(ceil_div(BN, kBlock));
     int j = 0;
     for (int t0 = T - 1; t0 >= 2; t0 -= Wwin, ++j) {
         const int nw = std::min(Wwin, t0 - 1);
@@ -1165,7 +1214,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         aa.nw = nw;
         {
             ProfScope p(kProfAdj, s);
-            launch_adj(aa, c->nb, adj_grid, lds, s);
+            launch_adj(aa, c->nb, lds, s);
         }
         ca.n_elem = nw * B;
         act.s0 = s0;
