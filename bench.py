@@ -3,8 +3,9 @@
 
 One step = one training pass of the config-2 workload: forward rollout of the
 66k-neuron network over T=500 ms at batch 5 (event-driven synaptic currents + fused
-GLIF_3 step), the firing-rate MSE loss, and BPTT through all 500 steps giving the
-recurrent and LGN weight gradients.  Inputs (LGN spikes, background Poisson counts)
+GLIF_3 step), the firing-rate MSE loss, BPTT through all 500 steps giving the
+recurrent and LGN weight gradients, and the ExponentiatedAdam update with the sign
+constraints of both weight vectors.  Inputs (LGN spikes, background Poisson counts)
 are resident in HBM before timing.  Prints one JSON line.
 
 The dominant kernel's roofline is measured live: its launches are bracketed by
@@ -214,6 +215,7 @@ def main():
     from v1_glif_model_amd import _lib
     from v1_glif_model_amd import synthetic as sy
     from v1_glif_model_amd.models import V1Column, rate_loss_grad
+    from v1_glif_model_amd.optim import ExponentiatedAdam, SignedConstraint
 
     cfg = sy.config(args.config)
     if args.config in (0, 1, 3):
@@ -239,6 +241,12 @@ def main():
     zero = cell.zero_state(B)
     state = [s.clone() for s in zero]
     want = ("rec", "lgn")
+    # the reference's optimizer and weight constraints (multi_training.py:1042, 1046;
+    # models.py:666, 729): ExponentiatedAdam, lr 0.005
+    opt = ExponentiatedAdam(learning_rate=0.005)
+    w_rec, w_lgn = cell.recurrent_weight_values, cell.input_weight_values
+    cons = {w_rec.data_ptr(): SignedConstraint(cell.recurrent_weight_positive),
+            w_lgn.data_ptr(): SignedConstraint(cell.input_weight_positive)}
     fwd_ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     timings = []
 
@@ -253,7 +261,8 @@ def main():
         fwd_ev[1].record()
         if not args.forward_only:
             _, gzn = rate_loss_grad(spike_count, targets, T)
-            cell.backward(gz_neuron=gzn, want=want)
+            g = cell.backward(gz_neuron=gzn, want=want)
+            opt.apply_gradients([(g["rec"], w_rec), (g["lgn"], w_lgn)], constraints=cons)
         fwd_ev[2].record()
         timings.append(fwd_ev)
 
@@ -349,7 +358,7 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"config {args.config}: {N} GLIF_3 neurons, {S} recurrent synapses, "
-                               f"B={B}, T={T}, {'forward' if args.forward_only else 'forward + BPTT (rec + LGN dW)'}",
+                               f"B={B}, T={T}, {'forward' if args.forward_only else 'forward + BPTT (rec + LGN dW) + ExponentiatedAdam update'}",
                    "neurons": N, "recurrent_synapses": S, "lgn_synapses": tb.lgn.n_syn,
                    "bkg_synapses": tb.bkg.n_syn, "batch": B, "seq_len": T, "mode": args.mode},
         "roofline": roofline,

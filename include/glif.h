@@ -161,6 +161,19 @@ int glif_cell_backward(glif_cell *c, int32_t B, int32_t T, const float *gz,
                        const float *gz_neuron, const float *gv, float *dw_rec, float *dw_lgn,
                        float *dw_bkg, void *ws, size_t ws_bytes, void *stream);
 
+/* ------------------------------------------------------------- optimizer ------
+ * Replaces ExponentiatedAdam.update_step, dense branch (v1_model_utils/optimizers.py:
+ * 354-376; alpha :273-283), followed by the variable's SignedConstraint (models.py:419-427, attached
+ * at :666, :729, :764), which Keras applies after the optimizer step.  One pass:
+ *   m += (g - m)(1 - beta_1);  v += (g^2 - v)(1 - beta_2);  AMSGrad: vhat = max(vhat, v)
+ *   w *= exp(-alpha * m / (sqrt(vhat or v) + epsilon) * sign(w)),  sign(0) = +1
+ *   positive != NULL: w = positive ? relu(w) : -relu(-w)
+ * alpha = learning_rate * sqrt(1 - beta_2^t) / (1 - beta_1^t) (t = iterations + 1) is
+ * the caller's fp32 scalar.  device: w, m, v [n] f32 in/out, vhat [n] (NULL: no
+ * AMSGrad), g [n] f32, positive [n] u8 (NULL: no constraint). */
+int glif_exp_adam(float *w, float *m, float *v, float *vhat, const float *g, const uint8_t *positive,
+                  int64_t n, float alpha, float beta_1, float beta_2, float epsilon, void *stream);
+
 /* ------------------------------------------------------------ profiling ------
  * No reference counterpart (the reference times whole steps with time(),
  * callbacks.py:1442-1449).  Kernel classes: 0 push, 1 step, 2 adj, 3 bwd_rec,
