@@ -174,6 +174,19 @@ int glif_cell_backward(glif_cell *c, int32_t B, int32_t T, const float *gz,
 int glif_exp_adam(float *w, float *m, float *v, float *vhat, const float *g, const uint8_t *positive,
                   int64_t n, float alpha, float beta_1, float beta_2, float epsilon, void *stream);
 
+/* ------------------------------------------------------------ input sampling -
+ * On-device replacements for the host input streams: LGN spikes (stim_dataset.py:182-197,
+ * Bernoulli with p = 1 - exp(-rate * dt / 1000)) and background counts (models.py:865-887,
+ * Poisson with lambda = rate * dt / 1000; TF's stateless stream cannot be reproduced).
+ * Generator: Philox4x32-10; element i of the stream (seed) is word i % 4 of the block for
+ * counter i / 4; `offset` continues a stream (element offset + i).  u = (word >> 8) * 2^-24.
+ * Bernoulli: out[i] = u < p[i].  Poisson: sequential inverse CDF in fp32 from
+ * exp_neg_lam = expf(-lam) (the caller's, so hosts and device agree bit for bit), counts
+ * capped at 255.  device: p [n] f32, out [n] u8. */
+int glif_sample_bernoulli(const float *p, int64_t n, uint64_t seed, uint64_t offset, uint8_t *out, void *stream);
+int glif_sample_poisson(float lam, float exp_neg_lam, int64_t n, uint64_t seed, uint64_t offset, uint8_t *out,
+                        void *stream);
+
 /* ------------------------------------------------------------ profiling ------
  * No reference counterpart (the reference times whole steps with time(),
  * callbacks.py:1442-1449).  Kernel classes: 0 push, 1 step, 2 adj, 3 bwd_rec,

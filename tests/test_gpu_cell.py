@@ -152,3 +152,24 @@ def test_wide_batch_forward_and_backward(B):
         scale = np.max(np.abs(e))
         assert scale > 0
         assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
+
+
+def test_call_steps_equal_rollout():
+    """The per-step Keras-cell API (models.py:1059-1135) over T calls equals one T-step
+    rollout (deterministic mode: bit for bit); without counts, call draws the background
+    from the device stream and advances the step counter."""
+    cfg = tiny_config(rs=2.0, ins=3.0)
+    tn = network(cfg, seed=2, dense_basis=True)
+    T, B = 20, 2
+    lgn, bkg = _inputs(cfg, T, B, seed=3)
+    cell = _cell(tn, "deterministic", **CELL_KW)
+    zr, vr, _ = cell.rollout(lgn, bkg)
+    state = cell.zero_state(B)
+    for t in range(T):
+        inp = torch.tensor(lgn[t], dtype=torch.float32, device="cuda")
+        (z, v), state = cell.call(inp, state, bkg_counts=torch.tensor(bkg[t], device="cuda"))
+        np.testing.assert_array_equal(z.cpu().numpy(), zr[t].cpu().numpy())
+        np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), vr[t].cpu().numpy().view(np.uint32))
+    assert int(state[6][0].item()) == T
+    (z, v), st2 = cell.call(torch.tensor(lgn[0], dtype=torch.float32, device="cuda"), state)
+    assert z.shape == (B, tn[1].n_neurons) and int(st2[6][0].item()) == T + 1

@@ -58,6 +58,8 @@ SIGNATURES = {
     "glif_cell_backward": (C.c_int, [vp, i32, i32, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
     "glif_exp_adam": (C.c_int, [vp, vp, vp, vp, vp, vp, i64, C.c_float, C.c_float, C.c_float, C.c_float,
                                 vp]),
+    "glif_sample_bernoulli": (C.c_int, [vp, i64, C.c_uint64, C.c_uint64, vp, vp]),
+    "glif_sample_poisson": (C.c_int, [C.c_float, C.c_float, i64, C.c_uint64, C.c_uint64, vp, vp]),
     "glif_prof_enable": (C.c_int, [C.c_uint32]),
     "glif_prof_collect": (C.c_int, [vp, vp, i32]),
     "glif_prof_name": (C.c_char_p, [i32]),

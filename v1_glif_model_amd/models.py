@@ -183,10 +183,12 @@ class V1Column:
         """One step (models.py:1059-1135): returns ((z, v), new_state)."""
         B = int(inputs.shape[0])
         if bkg_counts is None:
-            g = torch.Generator(device=self.device)
-            g.manual_seed(self.noise_seed * 1000003 + int(state[6][0].item()))
-            lam = torch.full((B, self.n_bkg), self.bkg_spike_prob, device=self.device)
-            bkg_counts = torch.poisson(lam, generator=g)
+            # the reference seeds its stateless Poisson per step with (noise_seed, step)
+            # (models.py:867-887); here the step picks the offset in the noise_seed stream
+            from .inputs import poisson
+            step = int(state[6][0].item())
+            bkg_counts = poisson(self.bkg_spike_prob, (B, self.n_bkg), self.noise_seed,
+                                 offset=step * B * self.n_bkg, device=self.device)
         lgn = inputs[:, :self.input_dim][None]
         z, v, st = self.rollout(lgn, bkg_counts[None], state=[s.clone() for s in state])
         return (z[0], v[0]), st
