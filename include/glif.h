@@ -161,6 +161,16 @@ int glif_cell_backward(glif_cell *c, int32_t B, int32_t T, const float *gz,
                        const float *gz_neuron, const float *gv, float *dw_rec, float *dw_lgn,
                        float *dw_bkg, void *ws, size_t ws_bytes, void *stream);
 
+/* Fused voltage regularization (VoltageRegularization, loss_functions.py:1047-1119):
+ * mode 0 off, 1 "range" (penalty relu(|v - 0.5| - 0.5)^2), 2 "threshold" ((v - 1)^2),
+ * loss = cost * mean over (T, B, N) of the penalty of the cell's output voltages.  While
+ * enabled, glif_cell_backward adds its gradient to dL/dv inside the adjoint (no dense dL/dv
+ * tensor), and glif_cell_voltage_loss reduces the loss of the last forward on `ws` into
+ * loss_out (device f32) in a fixed order. */
+int glif_cell_set_voltage_loss(glif_cell *c, int32_t mode, float cost);
+int glif_cell_voltage_loss(glif_cell *c, int32_t B, int32_t T, float *loss_out, void *ws, size_t ws_bytes,
+                           void *stream);
+
 /* ------------------------------------------------------------- optimizer ------
  * Replaces ExponentiatedAdam.update_step, dense branch (v1_model_utils/optimizers.py:
  * 354-376; alpha :273-283), followed by the variable's SignedConstraint (models.py:419-427, attached

@@ -173,3 +173,41 @@ def test_call_steps_equal_rollout():
     assert int(state[6][0].item()) == T
     (z, v), st2 = cell.call(torch.tensor(lgn[0], dtype=torch.float32, device="cuda"), state)
     assert z.shape == (B, tn[1].n_neurons) and int(st2[6][0].item()) == T + 1
+
+
+@pytest.mark.parametrize("mode", ["range", "threshold"])
+def test_fused_voltage_regularization(mode):
+    """VoltageRegularization (loss_functions.py:1047-1119) fused into the cell: the loss
+    reduced from the kept voltages equals the loss of the output voltages, and the BPTT
+    with the fused gradient equals the oracle's BPTT given dL/dv of that loss."""
+    from v1_glif_model_amd.losses import VoltageRegularization
+    cfg = tiny_config(rs=2.0, ins=3.0)
+    tn = network(cfg, seed=5, dense_basis=True)
+    T, B = 30, 3
+    lgn, bkg = _inputs(cfg, T, B, seed=6)
+    cell = _cell(tn, "deterministic", **CELL_KW)
+    cost = 0.5
+    reg = VoltageRegularization(cell, voltage_cost=cost, penalty_mode=mode)
+    z, v, _ = cell.rollout(lgn, bkg)
+    vn = v.cpu().numpy().astype(np.float64)
+    if mode == "range":
+        m = np.maximum(np.abs(vn - 0.5) - 0.5, 0.0)
+        pen, dpen = m * m, 2.0 * m * np.sign(vn - 0.5)
+    else:
+        pen, dpen = (vn - 1.0) ** 2, 2.0 * (vn - 1.0)
+    loss = float(reg())
+    assert abs(loss - cost * pen.mean()) <= 1e-6 * abs(cost * pen.mean()) + 1e-12
+    assert abs(float(reg(v)) - loss) <= 1e-6 * abs(loss) + 1e-12
+    oc = _oracle(tn[1], **ORC_KW)
+    oz, ov, oref, _ = oc.forward(lgn, bkg)
+    rng = np.random.default_rng(7)
+    gz = rng.normal(0, 1, oz.shape).astype(np.float32)
+    g = cell.backward(gz=torch.tensor(gz, device="cuda"))
+    gv = (cost * dpen / vn.size).astype(np.float32)
+    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz, gv_loss=gv)
+    reg.disable()
+    for k in ("rec", "lgn", "bkg"):
+        a, e = g[k].cpu().numpy(), og[k]
+        scale = np.max(np.abs(e))
+        assert scale > 0
+        assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k

@@ -56,6 +56,8 @@ SIGNATURES = {
     "glif_cell_forward": (C.c_int, [vp, i32, i32, i32, vp, vp, C.POINTER(State), vp, vp, vp, vp,
                                     sz, vp]),
     "glif_cell_backward": (C.c_int, [vp, i32, i32, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
+    "glif_cell_set_voltage_loss": (C.c_int, [vp, i32, C.c_float]),
+    "glif_cell_voltage_loss": (C.c_int, [vp, i32, i32, vp, vp, sz, vp]),
     "glif_exp_adam": (C.c_int, [vp, vp, vp, vp, vp, vp, i64, C.c_float, C.c_float, C.c_float, C.c_float,
                                 vp]),
     "glif_sample_bernoulli": (C.c_int, [vp, i64, C.c_uint64, C.c_uint64, vp, vp]),

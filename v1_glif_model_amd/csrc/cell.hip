@@ -28,6 +28,7 @@
 namespace glif {
 
 // ------------------------------------------------------------------ state ----
+constexpr int kVlossBlocks = 1024;  // blocks of the voltage-penalty reduction
 struct CellWs {
     float *I;           // [nb][B][N]   pushed rec + LGN currents (event mode)
     float *R, *P;       // [nb][B][N]   psc_rise, psc (receptor-major copies of the state)
@@ -54,6 +55,7 @@ struct CellWs {
     float *G;           // [n_types][N][R]
     float *gV;          // [B][N]
     float *gP, *gR;     // [nb][B][N]
+    float *vloss_part;  // [kVlossBlocks] partial sums of the voltage penalty
     float *dw_rec;      // type-phased order
     float *dw_lgn, *dw_bkg;  // column-grouped order
 };
@@ -96,6 +98,7 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.gV = cv.take<float>(BN);
     w.gP = cv.take<float>(BN * c->nb);
     w.gR = cv.take<float>(BN * c->nb);
+    w.vloss_part = cv.take<float>(kVlossBlocks);
     w.dw_rec = cv.take<float>(std::max<int64_t>(c->rec->n_syn, 1));
     w.dw_lgn = cv.take<float>(std::max<int64_t>(c->lgn->n_syn, 1));
     w.dw_bkg = cv.take<float>(std::max<int64_t>(c->bkg->n_syn, 1));
@@ -585,12 +588,68 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
     }
 }
 
+// ------------------------------------------------- voltage regularization ----
+// VoltageRegularization (loss_functions.py:1047-1119): penalty of the cell's output
+// voltage, range mode relu(|v - 0.5| - 0.5)^2 (zero inside [0, 1]), threshold mode
+// (v - 1)^2; the loss is cost * mean over (T, B, N).  Its gradient enters the adjoint
+// like dL/dv (relu' = 0 at the kink, as TF's).
+__device__ inline float vpenalty(int mode, float v) {
+    if (mode == 1) {
+        const float m = fabsf(v - 0.5f) - 0.5f;
+        return m > 0.0f ? m * m : 0.0f;
+    }
+    const float d = v - 1.0f;
+    return d * d;
+}
+
+__device__ inline float vpenalty_grad(int mode, float v) {
+    if (mode == 1) {
+        const float x = v - 0.5f;
+        const float m = fabsf(x) - 0.5f;
+        return m > 0.0f ? (2.0f * m) * (x > 0.0f ? 1.0f : -1.0f) : 0.0f;
+    }
+    return 2.0f * (v - 1.0f);
+}
+
+// Fixed-order reduction (run to run identical): block partials, then one block.
+__global__ void __launch_bounds__(kBlock)
+    k_vloss_partial(const float *__restrict__ v, int64_t n, int mode, float *__restrict__ part) {
+    __shared__ float red[kBlock];
+    float acc = 0.0f;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        acc += vpenalty(mode, v[i]);
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = kBlock / 2; o > 0; o >>= 1) {
+        if (static_cast<int>(threadIdx.x) < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+__global__ void __launch_bounds__(kBlock)
+    k_vloss_final(const float *__restrict__ part, int n_part, float scale, float *__restrict__ out) {
+    __shared__ float red[kBlock];
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < n_part; i += kBlock) acc += part[i];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = kBlock / 2; o > 0; o >>= 1) {
+        if (static_cast<int>(threadIdx.x) < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = red[0] * scale;
+}
+
 // --------------------------------------------------------------- adjoint ----
 constexpr int kDelayUnroll = 8;
 
 struct AdjArgs {
     CellConst k;
     int32_t t0, nw, T, ring, R;
+    int32_t vmode;   // fused voltage regularization (0 off, 1 range, 2 threshold)
+    float vscale;    // its cost / (T * B * N)
     const float *vsave;
     const uint64_t *refbits;
     const float *gz, *gz_neuron, *gv;
@@ -695,6 +754,7 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
         }
         float gV = gz * psi;
         if (a.gv) gV = gV + a.gv[tbn];
+        if (a.vmode) gV = gV + vpenalty_grad(a.vmode, a.vsave[tbn]) * a.vscale;
         gV = gV + (gVc * decay) * k.om;
         gVc = (k.hard_reset && refr) ? 0.0f : gV;
         float dy[kMaxBasis];
@@ -1163,6 +1223,10 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     aa.T = T;
     aa.ring = ring;
     aa.R = Rg;
+    aa.vmode = c->vloss_mode;
+    aa.vscale = c->vloss_mode ? c->vloss_cost / (static_cast<float>(T) * static_cast<float>(B) *
+                                                 static_cast<float>(c->N))
+                              : 0.0f;
     aa.vsave = w.vsave;
     aa.refbits = w.refbits;
     aa.gz = gz;
@@ -1239,6 +1303,33 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     if (dw_rec && (rc = launch_scatter_f32(dw_rec, w.dw_rec, tr->ph_order, tr->n_syn, s))) return rc;
     if (dw_lgn && (rc = launch_scatter_f32(dw_lgn, w.dw_lgn, tl->order, tl->n_syn, s))) return rc;
     if (dw_bkg && (rc = launch_scatter_f32(dw_bkg, w.dw_bkg, tb->order, tb->n_syn, s))) return rc;
+    return GLIF_OK;
+}
+
+int glif_cell_set_voltage_loss(glif_cell *cc, int32_t mode, float cost) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c) return fail(GLIF_EINVAL, "NULL cell");
+    if (mode < 0 || mode > 2) return fail(GLIF_EINVAL, "mode must be 0 (off), 1 (range) or 2 (threshold)");
+    c->vloss_mode = mode;
+    c->vloss_cost = cost;
+    return GLIF_OK;
+}
+
+int glif_cell_voltage_loss(glif_cell *cc, int32_t B, int32_t T, float *loss_out, void *ws, size_t ws_bytes,
+                           void *stream) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c || !loss_out) return fail(GLIF_EINVAL, "NULL argument");
+    if (c->vloss_mode == 0) return fail(GLIF_EINVAL, "voltage loss not enabled (glif_cell_set_voltage_loss)");
+    if (B <= 0 || B > kMaxBatch || T <= 0) return fail(GLIF_EINVAL, "bad B or T");
+    if (!ws || ws_bytes < glif_cell_workspace(cc, B, T)) return fail(GLIF_ENOMEM, "workspace too small");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    CellWs w = carve_cell(ws, c, B, T, nullptr);
+    const int64_t n = static_cast<int64_t>(T) * B * c->N;
+    hipLaunchKernelGGL(k_vloss_partial, dim3(kVlossBlocks), dim3(kBlock), 0, s, w.vsave, n, c->vloss_mode,
+                       w.vloss_part);
+    const float scale = c->vloss_cost / static_cast<float>(n);
+    hipLaunchKernelGGL(k_vloss_final, dim3(1), dim3(kBlock), 0, s, w.vloss_part, kVlossBlocks, scale, loss_out);
+    GLIF_HIP(hipGetLastError());
     return GLIF_OK;
 }
 

@@ -78,6 +78,8 @@ struct Cell {
     int32_t *tref = nullptr;                 // [N]
     float syn_decay[kMaxBasis]{}, psc_initial[kMaxBasis]{}, dtsd[kMaxBasis]{};
     Table *rec = nullptr, *lgn = nullptr, *bkg = nullptr;
+    int32_t vloss_mode = 0;    // fused voltage regularization: 0 off, 1 range, 2 threshold
+    float vloss_cost = 0.0f;
 };
 
 // Small per-cell constants passed by value to kernels.
