@@ -147,7 +147,8 @@ size_t glif_cell_workspace(const glif_cell *c, int32_t B, int32_t T);
  * device in: lgn [T][B][n_lgn] uint8 (spike where > 0), bkg [T][B][n_bkg] uint8
  * (Poisson counts; TF's stateless Poisson stream is not reproducible, so counts are
  * an input).  state: in/out.  out (each may be NULL): z [T][B][N] f32, v [T][B][N]
- * f32 (the cell outputs), spike_count [B][N] int32 (accumulated). */
+ * f32 (the cell outputs), spike_count [B][N] int32 (accumulated over the ticks of the
+ * trimming window, glif_cell_set_trim; all ticks by default). */
 int glif_cell_forward(glif_cell *c, int32_t B, int32_t T, int32_t mode, const uint8_t *lgn,
                       const uint8_t *bkg, glif_state *state, float *z_out, float *v_out,
                       int32_t *spike_count, void *ws, size_t ws_bytes, void *stream);
@@ -155,7 +156,7 @@ int glif_cell_forward(glif_cell *c, int32_t B, int32_t T, int32_t mode, const ui
 /* BPTT through the last glif_cell_forward on `ws` (zero initial state assumed for
  * the adjoint; gradients do not flow into the initial state).
  * device in (each may be NULL): gz [T][B][N] dL/dz, gz_neuron [N] dL/dz broadcast
- * over (t, b), gv [T][B][N] dL/dv.  out (each may be NULL): dw_rec, dw_lgn, dw_bkg,
+ * over b and the ticks of the trimming window, gv [T][B][N] dL/dv.  out (each may be NULL): dw_rec, dw_lgn, dw_bkg,
  * gradients of the three weight vectors in reference order (overwritten). */
 int glif_cell_backward(glif_cell *c, int32_t B, int32_t T, const float *gz,
                        const float *gz_neuron, const float *gv, float *dw_rec, float *dw_lgn,
@@ -170,6 +171,33 @@ int glif_cell_backward(glif_cell *c, int32_t B, int32_t T, const float *gz,
 int glif_cell_set_voltage_loss(glif_cell *c, int32_t mode, float cost);
 int glif_cell_voltage_loss(glif_cell *c, int32_t B, int32_t T, float *loss_out, void *ws, size_t ws_bytes,
                            void *stream);
+
+/* Spike trimming of the rate losses (spike_trimming, loss_functions.py:604-611, applied
+ * by SpikeRateDistributionTarget.__call__ :873-881): of a T-tick forward, only ticks
+ * [pre_delay, T - post_delay) add to spike_count, and glif_cell_backward broadcasts
+ * gz_neuron over those ticks only.  Default 0, 0 (every tick). */
+int glif_cell_set_trim(glif_cell *c, int32_t pre_delay, int32_t post_delay);
+
+/* ----------------------------------------------------------------- losses -----
+ * Rate-distribution loss (SpikeRateDistributionTarget.__call__, loss_functions.py:873-889
+ * -> compute_spike_rate_target_loss :634-664 -> compute_spike_rate_distribution_loss
+ * :666-681 -> huber_quantile_loss :626-632, kappa 0.002 at :680).
+ * rate[n] = (sum_r count[r][n]) / n_samples (count [count_rows][n_neurons] int32,
+ * device: the forward's spike_count, rows = B, n_samples = window ticks x B).
+ * Populations: ids [pop_ptr[n_pop]] int32 (device) holds the selected neuron ids of
+ * population k at [pop_ptr[k], pop_ptr[k+1]) (pop_ptr host, n_pop <= 64, ids distinct);
+ * targets (device f32, same layout) each population's ascending sampled target rates.
+ * Each population's rates are sorted ascending; ties are ordered by a Philox4x32-10 word
+ * (seed, offset + position) when shuffle != 0 (the reference's tf.random.shuffle), else
+ * by position in ids.  loss_out (device f32) = rate_cost * sum of the Huber-quantile
+ * terms / pop_ptr[n_pop] (NaN when an id is outside [0, n_neurons) or a count exceeds
+ * n_samples); gz_neuron [n_neurons] (device f32) += dL/drate / n_samples, the per-tick
+ * dL/dz for glif_cell_backward's gz_neuron.  Workspace: glif_rate_loss_workspace. */
+size_t glif_rate_loss_workspace(int64_t n_sel);
+int glif_rate_dist_loss(const int32_t *count, int32_t count_rows, int32_t n_neurons, int32_t n_samples,
+                        const int32_t *ids, const int32_t *pop_ptr, int32_t n_pop, const float *targets,
+                        float kappa, float rate_cost, int32_t shuffle, uint64_t seed, uint64_t offset,
+                        float *loss_out, float *gz_neuron, void *ws, size_t ws_bytes, void *stream);
 
 /* ------------------------------------------------------------- optimizer ------
  * Replaces ExponentiatedAdam.update_step, dense branch (v1_model_utils/optimizers.py:

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libglif.so")
 OBJ_DIR = os.path.join(HERE, "_build")
-SOURCES = ["table.hip", "compact.hip", "syn.hip", "cell.hip", "optim.hip", "sample.hip", "prof.hip"]
+SOURCES = ["table.hip", "compact.hip", "syn.hip", "cell.hip", "optim.hip", "sample.hip", "loss.hip", "prof.hip"]
 
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",

@@ -415,6 +415,7 @@ __global__ void __launch_bounds__(kBlock) k_push(PushArgs a) {
 struct StepArgs {
     CellConst k;
     int32_t t;
+    int32_t count_t0, count_t1;  // spike_count takes ticks [count_t0, count_t1)
     float *v;
     int16_t *r;
     float *A;   // [2][B][N]
@@ -567,7 +568,7 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
         a.vsave[tbn] = vn;
         if (a.z_out) a.z_out[tbn] = spike ? 1.0f : 0.0f;
         if (a.v_out) a.v_out[tbn] = vn;
-        if (a.spike_count && spike) a.spike_count[bn] += 1;
+        if (a.spike_count && spike && t >= a.count_t0 && t < a.count_t1) a.spike_count[bn] += 1;
         if (DET && spike) atomicOr(a.zmask + static_cast<int64_t>(t + k.D) * k.N + n, 1u << b);
     }
     const uint64_t zb = __ballot(spike), rb = __ballot(refr);
@@ -653,6 +654,7 @@ struct AdjArgs {
     const float *vsave;
     const uint64_t *refbits;
     const float *gz, *gz_neuron, *gv;
+    int32_t gzn_t0, gzn_t1;  // gz_neuron applies to ticks [gzn_t0, gzn_t1)
     const float *dZ;
     float *gV, *gP, *gR;
     const float *decay, *cf;
@@ -739,7 +741,7 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
         }
         const int64_t tbn = static_cast<int64_t>(t) * BN + bn;
         if (a.gz) gz = gz + a.gz[tbn];
-        if (a.gz_neuron) gz = gz + a.gz_neuron[n];
+        if (a.gz_neuron && t >= a.gzn_t0 && t < a.gzn_t1) gz = gz + a.gz_neuron[n];
         const bool refr = (a.refbits[(static_cast<int64_t>(t) * k.B + b) * k.W + (n >> 6)] >> (n & 63)) & 1ull;
         float psi = 0.0f;
         if (!refr) {
@@ -1084,6 +1086,8 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     sa.z_out = z_out;
     sa.v_out = v_out;
     sa.spike_count = spike_count;
+    sa.count_t0 = c->trim_pre;
+    sa.count_t1 = T - c->trim_post;
     sa.rlist = w.rlist;
     sa.rcount = w.rcount;
     sa.rec_row = tr->row_ptr;
@@ -1231,6 +1235,8 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     aa.refbits = w.refbits;
     aa.gz = gz;
     aa.gz_neuron = gz_neuron;
+    aa.gzn_t0 = c->trim_pre;
+    aa.gzn_t1 = T - c->trim_post;
     aa.gv = gv;
     aa.dZ = w.dZ;
     aa.gV = w.gV;
@@ -1312,6 +1318,15 @@ int glif_cell_set_voltage_loss(glif_cell *cc, int32_t mode, float cost) {
     if (mode < 0 || mode > 2) return fail(GLIF_EINVAL, "mode must be 0 (off), 1 (range) or 2 (threshold)");
     c->vloss_mode = mode;
     c->vloss_cost = cost;
+    return GLIF_OK;
+}
+
+int glif_cell_set_trim(glif_cell *cc, int32_t pre_delay, int32_t post_delay) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c) return fail(GLIF_EINVAL, "NULL cell");
+    if (pre_delay < 0 || post_delay < 0) return fail(GLIF_EINVAL, "pre_delay and post_delay must be >= 0");
+    c->trim_pre = pre_delay;
+    c->trim_post = post_delay;
     return GLIF_OK;
 }
 

@@ -80,6 +80,10 @@ struct Cell {
     Table *rec = nullptr, *lgn = nullptr, *bkg = nullptr;
     int32_t vloss_mode = 0;    // fused voltage regularization: 0 off, 1 range, 2 threshold
     float vloss_cost = 0.0f;
+    // spike-trimming window of the rate losses (loss_functions.py:604-611): the forward
+    // counts spikes of ticks [trim_pre, T - trim_post) and the backward broadcasts
+    // gz_neuron over the same ticks
+    int32_t trim_pre = 0, trim_post = 0;
 };
 
 // Small per-cell constants passed by value to kernels.

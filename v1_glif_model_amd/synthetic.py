@@ -39,7 +39,7 @@ from typing import Optional
 import numpy as np
 
 __all__ = ["SynthConfig", "CONFIGS", "make_network", "make_inputs", "make_rate_targets",
-           "config"]
+           "make_cell_types", "make_type_rates", "config"]
 
 
 @dataclasses.dataclass(frozen=True)
@@ -223,3 +223,36 @@ def make_rate_targets(n_neurons: int, seed: int = 2, mean_hz: float = 4.0, sigma
     rng = np.random.default_rng(seed)
     mu = math.log(mean_hz / 1000.0) - 0.5 * sigma ** 2
     return rng.lognormal(mu, sigma, n_neurons).astype(np.float32)
+
+
+# the 17 cell types of the rate losses (loss_functions.py:724-743) with the share of the
+# excitatory or inhibitory neurons each takes, and a mean recorded rate in Hz
+_EXC_TYPES = (("L2/3 Exc", 0.30, 2.0), ("L4 Exc", 0.25, 3.0), ("L5 Exc", 0.25, 4.0), ("L6 Exc", 0.20, 2.5))
+_INH_TYPES = (("L1 Htr3a", 0.04, 3.0), ("L2/3 PV", 0.10, 12.0), ("L2/3 SST", 0.07, 6.0),
+              ("L2/3 VIP", 0.08, 5.0), ("L4 PV", 0.12, 14.0), ("L4 SST", 0.07, 6.0), ("L4 VIP", 0.04, 5.0),
+              ("L5 PV", 0.14, 15.0), ("L5 SST", 0.10, 7.0), ("L5 VIP", 0.03, 5.0), ("L6 PV", 0.10, 12.0),
+              ("L6 SST", 0.08, 6.0), ("L6 VIP", 0.03, 4.0))
+
+
+def make_cell_types(n_neurons: int, n_exc: int, seed: int = 3):
+    """Per-neuron cell-type labels: the first n_exc neurons (the excitatory ones) over the
+    four Exc types, the rest over the 13 inhibitory types, in the shares above."""
+    rng = np.random.default_rng(seed)
+    out = np.empty(n_neurons, dtype=object)
+    for lo, hi, types in ((0, n_exc, _EXC_TYPES), (n_exc, n_neurons, _INH_TYPES)):
+        share = np.array([t[1] for t in types])
+        pick = rng.choice(len(types), size=hi - lo, p=share / share.sum())
+        out[lo:hi] = np.array([t[0] for t in types], dtype=object)[pick]
+    return out.astype(str)
+
+
+def make_type_rates(seed: int = 4, n_units: int = 200):
+    """Stand-in for the recorded per-type rates (the Neuropixels table is not part of the
+    workload): per type, n_units lognormal(sigma 1) rates in spikes/ms with the type's mean,
+    a 0 appended as loss_functions.py:854-857 does."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, _, mean_hz in _EXC_TYPES + _INH_TYPES:
+        r = rng.lognormal(math.log(mean_hz) - 0.5, 1.0, n_units) / 1000.0
+        out[name] = np.append(r, 0.0)
+    return out
