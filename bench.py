@@ -214,7 +214,9 @@ def main():
     import torch
     from v1_glif_model_amd import _lib
     from v1_glif_model_amd import synthetic as sy
-    from v1_glif_model_amd.models import V1Column, rate_loss_grad
+    from v1_glif_model_amd.losses import (SpikeRateDistributionTarget, VoltageRegularization,
+                                          population_neuron_ids)
+    from v1_glif_model_amd.models import V1Column
     from v1_glif_model_amd.optim import ExponentiatedAdam, SignedConstraint
 
     cfg = sy.config(args.config)
@@ -225,7 +227,6 @@ def main():
     t_gen = time.time()
     net = sy.make_network(cfg, seed=0)
     lgn_np, bkg_np = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
-    targets_np = sy.make_rate_targets(cfg.n_neurons, seed=2)
     cell = V1Column(net, mode=args.mode, gauss_std=0.5, dampening_factor=0.5,
                     recurrent_dampening_factor=0.5, voltage_gradient_dampening=0.5,
                     pseudo_gauss=True, train_input=True)
@@ -235,7 +236,6 @@ def main():
     N, S = tb.n_neurons, tb.rec.n_syn
     lgn = torch.tensor(lgn_np, device=dev)
     bkg = torch.tensor(bkg_np, device=dev)
-    targets = torch.tensor(targets_np, device=dev)
     ws = cell.workspace(B, T)
     spike_count = torch.zeros((B, N), dtype=torch.int32, device=dev)
     zero = cell.zero_state(B)
@@ -247,6 +247,14 @@ def main():
     w_rec, w_lgn = cell.recurrent_weight_values, cell.input_weight_values
     cons = {w_rec.data_ptr(): SignedConstraint(cell.recurrent_weight_positive),
             w_lgn.data_ptr(): SignedConstraint(cell.input_weight_positive)}
+    # the reference's training losses (multi_training.py:211-229, flags :1065-1078): the
+    # rate-distribution target over the cell types (rate_cost 1e4) and the voltage
+    # regularization ("threshold", voltage_cost 1), both fused with the cell
+    pops = population_neuron_ids(sy.make_cell_types(N, net["network"]["n_exc"]))
+    rate_loss = SpikeRateDistributionTarget(populations=pops, type_rates=sy.make_type_rates(),
+                                            rate_cost=10000.0, cell=cell, device=dev)
+    volt_loss = VoltageRegularization(cell, voltage_cost=1.0, penalty_mode="threshold")
+    gz_neuron = torch.zeros(N, dtype=torch.float32, device=dev)
     fwd_ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     timings = []
 
@@ -260,8 +268,10 @@ def main():
                      ws=ws)
         fwd_ev[1].record()
         if not args.forward_only:
-            _, gzn = rate_loss_grad(spike_count, targets, T)
-            g = cell.backward(gz_neuron=gzn, want=want)
+            gz_neuron.zero_()
+            rate_loss(spike_count=spike_count, T=T, gz_neuron=gz_neuron)
+            volt_loss()
+            g = cell.backward(gz_neuron=gz_neuron, want=want)
             opt.apply_gradients([(g["rec"], w_rec), (g["lgn"], w_lgn)], constraints=cons)
         fwd_ev[2].record()
         timings.append(fwd_ev)
@@ -341,9 +351,14 @@ def main():
         c0 = time.perf_counter()
         oz, ov, oref, _ = oc.forward(lgn_np[:Tc], bkg_np[:Tc])
         if not args.forward_only:
-            rbar = oz.reshape(Tc, B, N).mean((0, 1))
-            gzn = (2.0 / (N * B * Tc)) * (rbar - targets_np)
-            oc.backward(lgn_np[:Tc], bkg_np[:Tc], oz, oref, ov, gz_neuron=gzn.astype(np.float32),
+            from oracle.rate_loss_ref import rate_dist_loss
+            ids = np.concatenate([rate_loss.populations[k] for k in rate_loss.populations])
+            tgt = np.concatenate([rate_loss.target_rates[k]["sorted_target_rates"] for k in rate_loss.populations])
+            ptrs = np.concatenate([[0], np.cumsum([rate_loss.populations[k].size for k in rate_loss.populations])])
+            cnt = oz.reshape(Tc, B, N).sum((0, 1))
+            _, gzn = rate_dist_loss(cnt, Tc * B, ids, ptrs, tgt, rate_cost=10000.0, shuffle=True)
+            gv = (np.float32(2.0 / (Tc * B * N)) * (ov - np.float32(1.0))).astype(np.float32)
+            oc.backward(lgn_np[:Tc], bkg_np[:Tc], oz, oref, ov, gz_neuron=gzn, gv_loss=gv,
                         want=("rec", "lgn"))
         cpu_s = time.perf_counter() - c0
         cpu = {"value": round(B * N * Tc / cpu_s, 1), "unit": "neuron-timesteps/s", "cores": 1,
@@ -358,7 +373,7 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"config {args.config}: {N} GLIF_3 neurons, {S} recurrent synapses, "
-                               f"B={B}, T={T}, {'forward' if args.forward_only else 'forward + BPTT (rec + LGN dW) + ExponentiatedAdam update'}",
+                               f"B={B}, T={T}, {'forward' if args.forward_only else 'forward + rate-distribution and voltage losses + BPTT (rec + LGN dW) + ExponentiatedAdam update'}",
                    "neurons": N, "recurrent_synapses": S, "lgn_synapses": tb.lgn.n_syn,
                    "bkg_synapses": tb.bkg.n_syn, "batch": B, "seq_len": T, "mode": args.mode},
         "roofline": roofline,

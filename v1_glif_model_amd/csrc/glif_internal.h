@@ -16,6 +16,8 @@ constexpr int kBlock = 256;
 constexpr int kMaxBasis = 8;
 constexpr int kMaxBatch = 32;
 constexpr uint32_t kLow24 = 0x00FFFFFFu;
+constexpr int kChunkEntries = 512;
+constexpr int kChunkRows = 63;
 
 // ---- error plumbing -------------------------------------------------------
 void set_error(const std::string &msg);
@@ -51,6 +53,7 @@ struct Table {
     int32_t *row_ptr = nullptr;   // [n_post + 1]
     int32_t *perm = nullptr;      // [n_syn]       synapse id at position j
     uint32_t *pd = nullptr;       // [n_syn]       pre | (delay - 1) << 24
+    uint32_t *pidx = nullptr;     // [n_syn]       (n_slots - delay) * round64(n_pre) + pre, or null
     uint8_t *sid_row = nullptr;   // [n_syn]
     float *w_row = nullptr;       // [n_syn]
     // type-phased (backward): ordered by (syn_id, column, synapse id); the type-s
@@ -62,6 +65,11 @@ struct Table {
     int32_t ell_len = 0;
     uint2 *ell_pw = nullptr;      // [ell_len * n_post]
     int32_t *ell_src = nullptr;   // [ell_len * n_post] synapse id, -1 for padding
+    // row-aligned chunks of the post-grouped table for the deterministic pull: chunk k
+    // is {first row, rows, first entry, end entry}, at most kChunkRows rows and at most
+    // kChunkEntries entries unless it is a single longer row
+    int32_t n_chunks = 0;
+    int4 *chunk_desc = nullptr;   // [n_chunks]
     int32_t *ph_ptr = nullptr;    // [n_types * n_cols + 1]
     int32_t *ph_order = nullptr;  // [n_syn]       synapse id at position k
     uint2 *ph_pw = nullptr;       // [n_syn]       {post, weight bits}

@@ -110,7 +110,8 @@ static int upload(T **dst, const T *src, size_t n) {
 static void free_table(Table *t) {
     if (!t) return;
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
-                    t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src};
+                    t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
+                    t->chunk_desc, t->pidx};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete[] t->basis_host;
@@ -195,6 +196,11 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
     }
 
     std::vector<uint32_t> ps(n_syn), pd(n_syn);
+    // bit index of the entry's presynaptic spike in a stack of per-slot activity planes
+    // of round64(n_pre) bits, slot d at plane n_slots - d (the newest step last)
+    const int64_t pre_pad = (static_cast<int64_t>(n_pre) + 63) / 64 * 64;
+    const bool with_pidx = static_cast<int64_t>(n_delay_slots) * pre_pad < (int64_t(1) << 31);
+    std::vector<uint32_t> pidx(with_pidx ? n_syn : 0);
     std::vector<uint8_t> sid_row(n_syn);
     int32_t max_len = 0;
     for (int64_t c = 0; c < n_cols; ++c) max_len = std::max(max_len, col_ptr[c + 1] - col_ptr[c]);
@@ -207,6 +213,7 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         int64_t c = col[s];
         uint32_t d1 = static_cast<uint32_t>(c / n_pre), pre = static_cast<uint32_t>(c % n_pre);
         pd[j] = pre | (d1 << 24);
+        if (with_pidx) pidx[j] = static_cast<uint32_t>((n_delay_slots - 1 - d1) * pre_pad + pre);
         sid_row[j] = syn_id[s];
     }
 
@@ -241,6 +248,15 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
     t->n_basis = n_basis;
     t->max_col_len = max_len;
     t->ell_len = ell_len;
+    // row-aligned chunks, greedy in row order
+    std::vector<int4> chunk_desc;
+    for (int32_t n = 0; n < n_post;) {
+        int32_t m = n + 1;
+        while (m < n_post && m - n < kChunkRows && row_ptr[m + 1] - row_ptr[n] <= kChunkEntries) ++m;
+        chunk_desc.push_back(make_int4(n, m - n, row_ptr[n], row_ptr[m]));
+        n = m;
+    }
+    t->n_chunks = static_cast<int32_t>(chunk_desc.size());
     t->basis_host = new float[static_cast<size_t>(n_types) * n_basis];
     std::memcpy(t->basis_host, basis, sizeof(float) * n_types * n_basis);
     int rc = GLIF_OK;
@@ -249,8 +265,10 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         (rc = upload(&t->order, order.data(), order.size())) ||
         (rc = upload(&t->ps, ps.data(), ps.size())) ||
         (rc = upload(&t->row_ptr, row_ptr.data(), row_ptr.size())) ||
+        (rc = upload(&t->chunk_desc, chunk_desc.data(), chunk_desc.size())) ||
         (rc = upload(&t->perm, perm.data(), perm.size())) ||
         (rc = upload(&t->pd, pd.data(), pd.size())) ||
+        (with_pidx && (rc = upload(&t->pidx, pidx.data(), pidx.size()))) ||
         (rc = upload(&t->sid_row, sid_row.data(), sid_row.size())) ||
         (rc = upload(&t->ph_ptr, ph_ptr.data(), ph_ptr.size())) ||
         (rc = upload(&t->ph_order, ph_order.data(), ph_order.size())) ||
