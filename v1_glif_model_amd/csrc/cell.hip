@@ -330,6 +330,11 @@ constexpr int kPullBlock = 512;
 
 __device__ inline int rdlane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 
+// 4-byte load at a 32-bit byte offset (lets the compiler use the scalar-base form)
+__device__ inline uint32_t ld_off(const uint32_t *p, uint32_t byte_off) {
+    return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(p) + byte_off);
+}
+
 // The loads of one chunk given its descriptor d = {first row, rows, first entry, end
 // entry}: the row pointers of its rows (lane l: row l, l <= rows) and its first
 // kChunkEntries entries.
@@ -416,9 +421,9 @@ __device__ inline void pull_chunk(const PullArgs &a, const float *basis_lds, con
             sj[u] = 0;
             if (h) {
                 // zmask rows are Np wide, so slot t - d of pre is at t * Np + pidx
-                m[u] = REC ? a.zmask[static_cast<uint32_t>(a.t) * static_cast<uint32_t>(a.Np) + e[u]]
-                           : a.lmask[static_cast<uint32_t>(a.t) * static_cast<uint32_t>(a.n_lgn) + e[u]];
-                wj[u] = w[static_cast<uint32_t>(j)];
+                m[u] = REC ? ld_off(a.zmask, (static_cast<uint32_t>(a.t) * static_cast<uint32_t>(a.Np) + e[u]) * 4u)
+                           : ld_off(a.lmask, (static_cast<uint32_t>(a.t) * static_cast<uint32_t>(a.n_lgn) + e[u]) * 4u);
+                wj[u] = __uint_as_float(ld_off(reinterpret_cast<const uint32_t *>(w), static_cast<uint32_t>(j) * 4u));
                 sj[u] = sid[static_cast<uint32_t>(j)];
             }
             hm[u] = __ballot(h);
