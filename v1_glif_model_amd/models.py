@@ -26,7 +26,7 @@ from ._lib import check, lib, ptr, stream_ptr
 from .ops import MODES, SynapseTable
 from .tables import build_cell_tables
 
-__all__ = ["V1Column", "RSNNRollout", "rate_loss_grad"]
+__all__ = ["V1Column", "RSNNRollout"]
 
 
 class V1Column:
@@ -229,15 +229,3 @@ class RSNNRollout(torch.autograd.Function):
         g = ctx.cell.backward(gz=gz, gv=gv, want=ctx.want)
         return None, None, None, g["rec"], g["lgn"], g["bkg"]
 
-
-def rate_loss_grad(spike_count: torch.Tensor, targets: torch.Tensor, T: int):
-    """L = mean_n (rbar_n - r*_n)^2 with rbar_n = mean_{b,t} z[b, t, n].
-
-    spike_count [B, N] int32.  Returns (L, dL/dz [N]) -- dL/dz is the same for every (t, b)."""
-    B = spike_count.shape[0]
-    N = spike_count.shape[1]
-    rbar = spike_count.sum(0).float() / float(B * T)
-    diff = rbar - targets
-    loss = (diff * diff).mean()
-    gz = diff * (2.0 / (N * B * T))
-    return loss, gz
