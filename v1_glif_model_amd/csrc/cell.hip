@@ -41,8 +41,6 @@ struct CellWs {
     uint64_t *lbits;    // [T][Wl]           bit pre: x_t[b][pre] > 0 for some b
     float *I2;          // [nb][B][N]   LGN currents (deterministic chunk pull)
     float *vsave;       // [T][B][N]
-    int32_t *rlist;     // [(D + 1)][B * N]  active (b << 24 | n) of step s in slot (s + D) % (D + 1)
-    int32_t *rcount;    // [D + 1]
     int64_t *lgn_off;   // [T + 1]           per-step LGN (column, batch-mask) lists
     int32_t *lgn_pre;   // [T * n_lgn]
     uint32_t *lgn_mask;
@@ -85,8 +83,6 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.lbits = cv.take<uint64_t>(static_cast<size_t>(T) * ((nl + 63) / 64));
     w.I2 = cv.take<float>(BN * c->nb);
     w.vsave = cv.take<float>(static_cast<size_t>(T) * BN);
-    w.rlist = cv.take<int32_t>(static_cast<size_t>(c->D + 1) * BN);
-    w.rcount = cv.take<int32_t>(c->D + 1);
     w.lgn_off = cv.take<int64_t>(T + 1);
     w.lgn_pre = cv.take<int32_t>(static_cast<size_t>(T) * nl);
     w.lgn_mask = cv.take<uint32_t>(static_cast<size_t>(T) * nl);
@@ -142,18 +138,15 @@ static CellConst make_const(const Cell *c, int B) {
     return k;
 }
 
-__device__ inline int ring_slot(int s, int D) { return (s + D) % (D + 1); }
-
 __device__ inline bool zbit(const uint64_t *zbits, int slot, int b, int B, int W, int n) {
     return (zbits[(static_cast<int64_t>(slot) * B + b) * W + (n >> 6)] >> (n & 63)) & 1ull;
 }
 
 // ---------------------------------------------------------- history init ----
-// z_buf [B][D*N] (slot d-1 = z_{-d}) -> spike bits (slot D-d) and, in event mode,
-// the active lists of steps -1..-D.
+// z_buf [B][D*N] (slot d-1 = z_{-d}) -> spike bits (slot D-d) and, for the
+// deterministic pull, the batch masks and activity bitmaps of steps -1..-D.
 __global__ void __launch_bounds__(kBlock)
     k_init_history(const float *__restrict__ z_buf, CellConst k, uint64_t *__restrict__ zbits,
-                   int32_t *__restrict__ rlist, int32_t *__restrict__ rcount, int event,
                    uint32_t *__restrict__ zmask, uint64_t *__restrict__ abits) {
     const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t per_slot = static_cast<int64_t>(k.B) * k.Np;
@@ -166,15 +159,6 @@ __global__ void __launch_bounds__(kBlock)
     const uint64_t bits = __ballot(z);
     const int slot = k.D - d;
     if (lane == 0) zbits[(static_cast<int64_t>(slot) * k.B + b) * k.W + (n >> 6)] = bits;
-    if (event) {
-        int base = 0;
-        if (lane == 0 && bits) base = atomicAdd(&rcount[slot], __popcll(bits));
-        base = __shfl(base, 0, kWave);
-        if (z) {
-            const int rank = __popcll(bits & ((1ull << lane) - 1ull));
-            rlist[static_cast<int64_t>(slot) * k.B * k.N + base + rank] = (b << 24) | n;
-        }
-    }
     if (zmask && z) atomicOr(zmask + static_cast<int64_t>(slot) * k.Np + n, 1u << b);
     if (abits && lane == 0 && bits) atomicOr(abits + static_cast<int64_t>(slot) * k.W + (n >> 6), bits);
 }
@@ -664,9 +648,8 @@ __global__ void __launch_bounds__(kBlock)
 
 // ------------------------------------------------------------ event push ----
 struct PushArgs {
-    int32_t t, D, N, B, nb, n_types, chunks_rec, chunks_lgn;
-    const int32_t *rlist;
-    int32_t *rcount;
+    int32_t t, D, N, B, W, nb, n_types, chunks_lgn;
+    const uint64_t *zbits;  // [(T + D)][B][W] spike bits, slot s + D holds z_s
     const int32_t *rec_colptr;
     const uint32_t *rec_ps;
     const float *rec_w;
@@ -680,44 +663,44 @@ struct PushArgs {
     float *I;
 };
 
-// Work units: (item, chunk).  Items are the spikes of steps t-1..t-D (each one
-// column of the recurrent table) followed by the step's LGN columns.  A chunk is
-// L * kChunkIters synapses of the item's column, so long columns spread over
-// several sub-waves.
+// Work units, one wave each: the 64-bit spike words of steps t-1..t-D (D * B * W
+// words; each set bit is one spike, i.e. one column of the recurrent table, pushed
+// whole), then (column, chunk) units of the step's LGN columns (a chunk is
+// kWave * kChunkIters synapses, so long columns spread over several waves).  The
+// spike words come straight from the step kernel's ballots: no spike list, no
+// counter that every spiking wave would have to increment.
 constexpr int kChunkIters = 4;
 
-template <int L>
 __global__ void __launch_bounds__(kBlock) k_push(PushArgs a) {
+    constexpr int L = kWave;
     extern __shared__ float basis_lds[];
     load_basis_lds(basis_lds, a.basis, a.n_types * a.nb);
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.rcount[ring_slot(a.t, a.D)] = 0;
-    int64_t n_rec = 0;
-    for (int d = 1; d <= a.D; ++d) n_rec += a.rcount[ring_slot(a.t - d, a.D)];
+    const int64_t BW = static_cast<int64_t>(a.B) * a.W;
+    const int64_t n_words = static_cast<int64_t>(a.D) * BW;
     const int64_t l0 = a.lgn_off[a.t], n_lgn = a.lgn_off[a.t + 1] - l0;
-    const int64_t units = n_rec * a.chunks_rec + n_lgn * a.chunks_lgn;
+    const int64_t units = n_words + n_lgn * a.chunks_lgn;
     const int lane_s = threadIdx.x % L;
     const int64_t n_subs = static_cast<int64_t>(gridDim.x) * blockDim.x / L;
     const int64_t BN = static_cast<int64_t>(a.B) * a.N;
-    for (int64_t u = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / L; u < units;
-         u += n_subs) {
-        if (u < n_rec * a.chunks_rec) {
-            int64_t it = u / a.chunks_rec;
-            const int ch = static_cast<int>(u % a.chunks_rec);
-            int d = 1;
-            for (; d <= a.D; ++d) {
-                const int64_t c = a.rcount[ring_slot(a.t - d, a.D)];
-                if (it < c) break;
-                it -= c;
+    // the unit index is uniform across the wave: keep it (and the spike word) scalar
+    const int64_t u0 = static_cast<int64_t>(blockIdx.x) * (blockDim.x / L) +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / L));
+    for (int64_t u = u0; u < units; u += n_subs) {
+        if (u < n_words) {
+            const int d = static_cast<int>(u / BW) + 1;
+            const int64_t rem = u - static_cast<int64_t>(d - 1) * BW;
+            const int b = static_cast<int>(rem / a.W);
+            const int wi = static_cast<int>(rem - static_cast<int64_t>(b) * a.W);
+            uint64_t word = a.zbits[(static_cast<int64_t>(a.t - d + a.D) * a.B + b) * a.W + wi];
+            while (word) {
+                const int bit = __builtin_ctzll(word);
+                word &= word - 1ull;
+                const int32_t col = wi * 64 + bit + (d - 1) * a.N;
+                push_column<L>(lane_s, a.rec_colptr[col], a.rec_colptr[col + 1], 1u << b, MultOne{}, a.rec_ps,
+                               a.rec_w, basis_lds, a.nb, a.N, 1, BN, a.I);
             }
-            const int32_t e = a.rlist[static_cast<int64_t>(ring_slot(a.t - d, a.D)) * BN + it];
-            const int b = e >> 24;
-            const int32_t col = (e & static_cast<int32_t>(kLow24)) + (d - 1) * a.N;
-            const int32_t lo = a.rec_colptr[col] + ch * L * kChunkIters;
-            const int32_t hi = min(a.rec_colptr[col + 1], lo + L * kChunkIters);
-            push_column<L>(lane_s, lo, hi, 1u << b, MultOne{}, a.rec_ps, a.rec_w, basis_lds, a.nb, a.N, 1,
-                           BN, a.I);
         } else {
-            const int64_t v = u - n_rec * a.chunks_rec;
+            const int64_t v = u - n_words;
             const int64_t it = l0 + v / a.chunks_lgn;
             const int ch = static_cast<int>(v % a.chunks_lgn);
             const int32_t c = a.lgn_pre[it];
@@ -750,7 +733,6 @@ struct StepArgs {
     float *vsave;
     float *z_out, *v_out;
     int32_t *spike_count;
-    int32_t *rlist, *rcount;
     const int32_t *rec_row;
     const uint32_t *rec_pd;
     const uint8_t *rec_sid;
@@ -898,16 +880,6 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
         a.zbits[static_cast<int64_t>(t + k.D) * k.B * k.W + word] = zb;
         a.refbits[static_cast<int64_t>(t) * k.B * k.W + word] = rb;
         if (DET && zb) atomicOr(a.abits + static_cast<int64_t>(t + k.D) * k.W + (n >> 6), zb);
-    }
-    if (!DET) {
-        const int slot = ring_slot(t, k.D);
-        int base = 0;
-        if (lane == 0 && zb) base = atomicAdd(&a.rcount[slot], __popcll(zb));
-        base = __shfl(base, 0, kWave);
-        if (spike) {
-            const int rank = __popcll(zb & ((1ull << lane) - 1ull));
-            a.rlist[static_cast<int64_t>(slot) * k.B * k.N + base + rank] = (b << 24) | n;
-        }
     }
 }
 
@@ -1375,13 +1347,12 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     }
     GLIF_HIP(hipMemcpyAsync(w.bkg_cnt, bkg, static_cast<size_t>(T) * B * tb->n_cols, hipMemcpyDeviceToDevice, s));
     // spike history of the initial state
-    if ((rc = launch_fill_u32(w.rcount, 0u, c->D + 1, s))) return rc;
     const int64_t n_init = static_cast<int64_t>(c->D) * B * c->Np;
     if (!event && ((rc = launch_fill_u32(w.zmask, 0u, static_cast<size_t>(T + c->D) * c->Np, s)) ||
                    (rc = launch_fill_u32(w.abits, 0u, static_cast<size_t>(T + c->D) * c->W * 2, s))))
         return rc;
     hipLaunchKernelGGL(k_init_history, dim3(ceil_div(n_init, kBlock)), dim3(kBlock), 0, s, st->z_buf, k,
-                       w.zbits, w.rlist, w.rcount, event ? 1 : 0, event ? nullptr : w.zmask,
+                       w.zbits, event ? nullptr : w.zmask,
                        event ? nullptr : w.abits);
     GLIF_HIP(hipGetLastError());
     if (event && (rc = launch_fill_u32(w.I, 0u, static_cast<size_t>(B) * c->N * c->nb, s))) return rc;
@@ -1414,8 +1385,6 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     sa.spike_count = spike_count;
     sa.count_t0 = c->trim_pre;
     sa.count_t1 = T - c->trim_post;
-    sa.rlist = w.rlist;
-    sa.rcount = w.rcount;
     sa.rec_row = tr->row_ptr;
     sa.rec_pd = tr->pd;
     sa.rec_sid = tr->sid_row;
@@ -1440,11 +1409,9 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     pa.B = B;
     pa.nb = c->nb;
     pa.n_types = c->n_types;
-    const int Lp = 64;
-    pa.chunks_rec = chunks_for(tr, Lp);
-    pa.chunks_lgn = chunks_for(tl, Lp);
-    pa.rlist = w.rlist;
-    pa.rcount = w.rcount;
+    pa.chunks_lgn = chunks_for(tl, kWave);
+    pa.zbits = w.zbits;
+    pa.W = c->W;
     pa.rec_colptr = tr->col_ptr;
     pa.rec_ps = tr->ps;
     pa.rec_w = tr->w_col;
@@ -1510,7 +1477,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
             pa.t = t;
             {
                 ProfScope p(kProfPush, s);
-                hipLaunchKernelGGL((k_push<Lp>), dim3(push_grid), dim3(kBlock), lds, s, pa);
+                hipLaunchKernelGGL(k_push, dim3(push_grid), dim3(kBlock), lds, s, pa);
             }
             ProfScope p(kProfStep, s);
             launch_step<false>(sa, c->nb, step_grid, lds, s);
