@@ -40,6 +40,9 @@ def _args():
                          "sweep of the event push against the deterministic row pull (B=32)")
     ap.add_argument("--rates", default="1,5,20,50", help="config 4: target mean rates in Hz")
     ap.add_argument("--mode", default="event", choices=["event", "deterministic"])
+    ap.add_argument("--loss", default="mse", choices=["mse", "reference"],
+                    help="mse: the configuration's firing-rate MSE against lognormal(4 Hz) targets; "
+                         "reference: the reference's rate-distribution target + voltage regularization")
     ap.add_argument("--seq-len", type=int, default=None)
     ap.add_argument("--cpu-steps", type=int, default=10,
                     help="timesteps of the CPU baseline sample (0: skip)")
@@ -214,7 +217,7 @@ def main():
     import torch
     from v1_glif_model_amd import _lib
     from v1_glif_model_amd import synthetic as sy
-    from v1_glif_model_amd.losses import (SpikeRateDistributionTarget, VoltageRegularization,
+    from v1_glif_model_amd.losses import (RateMSE, SpikeRateDistributionTarget, VoltageRegularization,
                                           population_neuron_ids)
     from v1_glif_model_amd.models import V1Column
     from v1_glif_model_amd.optim import ExponentiatedAdam, SignedConstraint
@@ -247,13 +250,20 @@ def main():
     w_rec, w_lgn = cell.recurrent_weight_values, cell.input_weight_values
     cons = {w_rec.data_ptr(): SignedConstraint(cell.recurrent_weight_positive),
             w_lgn.data_ptr(): SignedConstraint(cell.input_weight_positive)}
-    # the reference's training losses (multi_training.py:211-229, flags :1065-1078): the
-    # rate-distribution target over the cell types (rate_cost 1e4) and the voltage
-    # regularization ("threshold", voltage_cost 1), both fused with the cell
-    pops = population_neuron_ids(sy.make_cell_types(N, net["network"]["n_exc"]))
-    rate_loss = SpikeRateDistributionTarget(populations=pops, type_rates=sy.make_type_rates(),
-                                            rate_cost=10000.0, cell=cell, device=dev)
-    volt_loss = VoltageRegularization(cell, voltage_cost=1.0, penalty_mode="threshold")
+    if args.loss == "mse":
+        # the configuration's loss: mean-squared firing-rate error against per-neuron
+        # lognormal(4 Hz) targets
+        targets_np = sy.make_rate_targets(cfg.n_neurons, seed=2)
+        rate_loss = RateMSE(targets_np, device=dev)
+        volt_loss = None
+    else:
+        # the reference's training losses (multi_training.py:211-229, flags :1065-1078): the
+        # rate-distribution target over the cell types (rate_cost 1e4) and the voltage
+        # regularization ("threshold", voltage_cost 1), both fused with the cell
+        pops = population_neuron_ids(sy.make_cell_types(N, net["network"]["n_exc"]))
+        rate_loss = SpikeRateDistributionTarget(populations=pops, type_rates=sy.make_type_rates(),
+                                                rate_cost=10000.0, cell=cell, device=dev)
+        volt_loss = VoltageRegularization(cell, voltage_cost=1.0, penalty_mode="threshold")
     gz_neuron = torch.zeros(N, dtype=torch.float32, device=dev)
     fwd_ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     timings = []
@@ -269,8 +279,11 @@ def main():
         fwd_ev[1].record()
         if not args.forward_only:
             gz_neuron.zero_()
-            rate_loss(spike_count=spike_count, T=T, gz_neuron=gz_neuron)
-            volt_loss()
+            if volt_loss is None:
+                rate_loss(spike_count, T, gz_neuron=gz_neuron)
+            else:
+                rate_loss(spike_count=spike_count, T=T, gz_neuron=gz_neuron)
+                volt_loss()
             g = cell.backward(gz_neuron=gz_neuron, want=want)
             opt.apply_gradients([(g["rec"], w_rec), (g["lgn"], w_lgn)], constraints=cons)
         fwd_ev[2].record()
@@ -351,13 +364,17 @@ def main():
         c0 = time.perf_counter()
         oz, ov, oref, _ = oc.forward(lgn_np[:Tc], bkg_np[:Tc])
         if not args.forward_only:
-            from oracle.rate_loss_ref import rate_dist_loss
-            ids = np.concatenate([rate_loss.populations[k] for k in rate_loss.populations])
-            tgt = np.concatenate([rate_loss.target_rates[k]["sorted_target_rates"] for k in rate_loss.populations])
-            ptrs = np.concatenate([[0], np.cumsum([rate_loss.populations[k].size for k in rate_loss.populations])])
+            from oracle.rate_loss_ref import rate_dist_loss, rate_mse
             cnt = oz.reshape(Tc, B, N).sum((0, 1))
-            _, gzn = rate_dist_loss(cnt, Tc * B, ids, ptrs, tgt, rate_cost=10000.0, shuffle=True)
-            gv = (np.float32(2.0 / (Tc * B * N)) * (ov - np.float32(1.0))).astype(np.float32)
+            gv = None
+            if args.loss == "mse":
+                _, gzn = rate_mse(cnt, Tc * B, targets_np)
+            else:
+                ids = np.concatenate([rate_loss.populations[k] for k in rate_loss.populations])
+                tgt = np.concatenate([rate_loss.target_rates[k]["sorted_target_rates"] for k in rate_loss.populations])
+                ptrs = np.concatenate([[0], np.cumsum([rate_loss.populations[k].size for k in rate_loss.populations])])
+                _, gzn = rate_dist_loss(cnt, Tc * B, ids, ptrs, tgt, rate_cost=10000.0, shuffle=True)
+                gv = (np.float32(2.0 / (Tc * B * N)) * (ov - np.float32(1.0))).astype(np.float32)
             oc.backward(lgn_np[:Tc], bkg_np[:Tc], oz, oref, ov, gz_neuron=gzn, gv_loss=gv,
                         want=("rec", "lgn"))
         cpu_s = time.perf_counter() - c0
@@ -373,9 +390,10 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"config {args.config}: {N} GLIF_3 neurons, {S} recurrent synapses, "
-                               f"B={B}, T={T}, {'forward' if args.forward_only else 'forward + rate-distribution and voltage losses + BPTT (rec + LGN dW) + ExponentiatedAdam update'}",
+                               f"B={B}, T={T}, {'forward' if args.forward_only else ('forward + firing-rate MSE' if args.loss == 'mse' else 'forward + rate-distribution and voltage losses') + ' + BPTT (rec + LGN dW) + ExponentiatedAdam update'}",
                    "neurons": N, "recurrent_synapses": S, "lgn_synapses": tb.lgn.n_syn,
-                   "bkg_synapses": tb.bkg.n_syn, "batch": B, "seq_len": T, "mode": args.mode},
+                   "bkg_synapses": tb.bkg.n_syn, "batch": B, "seq_len": T, "mode": args.mode,
+                   "loss": None if args.forward_only else args.loss},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(bwd_ms, 3),

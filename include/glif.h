@@ -193,6 +193,16 @@ int glif_cell_set_trim(glif_cell *c, int32_t pre_delay, int32_t post_delay);
  * terms / pop_ptr[n_pop] (NaN when an id is outside [0, n_neurons) or a count exceeds
  * n_samples); gz_neuron [n_neurons] (device f32) += dL/drate / n_samples, the per-tick
  * dL/dz for glif_cell_backward's gz_neuron.  Workspace: glif_rate_loss_workspace. */
+/* Mean-squared firing-rate error, the loss the benchmark's training configuration names (no
+ * counterpart in the reference's loss_functions.py; the per-neuron form of its rate losses):
+ * rbar[n] = (sum_r count[r][n]) / n_samples, loss_out = sum_n (rbar[n] - targets[n])^2 /
+ * n_neurons (fixed order), gz_neuron[n] += (rbar[n] - targets[n]) * 2 / (n_neurons *
+ * n_samples), the per-tick dL/dz.  Workspace: glif_rate_mse_workspace() bytes. */
+size_t glif_rate_mse_workspace(void);
+int glif_rate_mse_loss(const int32_t *count, int32_t count_rows, int32_t n_neurons, int32_t n_samples,
+                       const float *targets, float *loss_out, float *gz_neuron, void *ws, size_t ws_bytes,
+                       void *stream);
+
 size_t glif_rate_loss_workspace(int64_t n_sel);
 int glif_rate_dist_loss(const int32_t *count, int32_t count_rows, int32_t n_neurons, int32_t n_samples,
                         const int32_t *ids, const int32_t *pop_ptr, int32_t n_pop, const float *targets,

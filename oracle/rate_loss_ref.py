@@ -87,3 +87,15 @@ def rate_dist_loss(count, n_samples, ids, pop_ptr, targets, kappa=0.002, rate_co
     loss, grad = loss_from_rates(count.astype(f32) / S, ids, pop_ptr, targets, kappa, rate_cost, order)
     # added into a zero buffer, as the library adds into the caller's (-0 becomes +0)
     return loss, (np.zeros(count.shape, f32) + grad / S).astype(f32)
+
+
+def rate_mse(count, n_samples, targets):
+    """Mean-squared firing-rate error (the benchmark configuration's loss): count [N]
+    (summed over batch rows), rbar = count / S in float32; loss = mean (rbar - target)^2,
+    gz_neuron = 0 + (rbar - target) * float32(2 / (N * S)) per tick."""
+    count = np.asarray(count)
+    N = count.shape[-1]
+    diff = count.astype(f32) / f32(n_samples) - np.asarray(targets, f32)
+    loss = f32(np.sum(diff.astype(np.float64) ** 2) / N)
+    scale = f32(2.0 / (float(N) * float(n_samples)))
+    return loss, (np.zeros(N, f32) + diff * scale).astype(f32)

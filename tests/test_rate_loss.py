@@ -133,6 +133,26 @@ def test_tie_order_brute_force(shuffle):
     np.testing.assert_array_equal(order, expect)
 
 
+def test_rate_mse_oracle_closed_form_and_gradient():
+    rng = np.random.default_rng(11)
+    N, S = 400, 250
+    count = rng.integers(0, 6, N)
+    tg = rng.uniform(0, 0.02, N).astype(np.float32)
+    loss, gz = R.rate_mse(count, S, tg)
+    r = count / S
+    assert abs(loss - np.mean((r - tg.astype(np.float64)) ** 2)) <= 1e-6 * loss
+    # dL/dz of every tick: dL/drate / S, dL/drate = 2 (r - t) / N (finite differences in float64)
+    eps = 1e-7
+    for j in rng.choice(N, 10, replace=False):
+        rp, rm = r.copy(), r.copy()
+        rp[j] += eps
+        rm[j] -= eps
+        fd = (np.mean((rp - tg) ** 2) - np.mean((rm - tg) ** 2)) / (2 * eps)
+        assert abs(gz[j] * S - fd) <= 1e-4 * abs(fd) + 1e-9
+    l0, g0 = R.rate_mse(np.zeros(N, int), S, np.zeros(N, np.float32))
+    assert l0 == 0 and not np.any(g0)
+
+
 # ---------------------------------------------------------------- host side ----
 def test_sample_firing_rates_properties():
     from v1_glif_model_amd.losses import sample_firing_rates
@@ -279,3 +299,20 @@ def test_gpu_rate_target_fused_with_cell():
     gd = cell.backward(gz=dense)
     for k in gw:
         np.testing.assert_array_equal(gw[k].cpu().numpy(), gd[k].cpu().numpy())
+
+
+@pytest.mark.gpu
+def test_gpu_rate_mse_matches_oracle():
+    import torch
+    from v1_glif_model_amd.losses import RateMSE
+    rng = np.random.default_rng(12)
+    B, N, T = 5, 70000, 500
+    count = rng.poisson(2.5, (B, N)).astype(np.int32)
+    tg = rng.lognormal(np.log(0.004), 1.0, N).astype(np.float32)
+    f = RateMSE(tg)
+    gz0 = rng.normal(0, 1e-6, N).astype(np.float32)
+    g = torch.tensor(gz0, device="cuda")
+    loss = float(f(torch.tensor(count, device="cuda"), T, gz_neuron=g))
+    el, eg = R.rate_mse(count.sum(0), T * B, tg)
+    np.testing.assert_array_equal(g.cpu().numpy(), gz0 + eg)
+    assert abs(loss - el) <= 1e-6 * el

@@ -60,6 +60,8 @@ SIGNATURES = {
     "glif_cell_voltage_loss": (C.c_int, [vp, i32, i32, vp, vp, sz, vp]),
     "glif_cell_set_trim": (C.c_int, [vp, i32, i32]),
     "glif_rate_loss_workspace": (sz, [i64]),
+    "glif_rate_mse_workspace": (sz, []),
+    "glif_rate_mse_loss": (C.c_int, [vp, i32, i32, i32, vp, vp, vp, vp, sz, vp]),
     "glif_rate_dist_loss": (C.c_int, [vp, i32, i32, i32, vp, vp, i32, vp, C.c_float, C.c_float, i32,
                                       C.c_uint64, C.c_uint64, vp, vp, vp, sz, vp]),
     "glif_exp_adam": (C.c_int, [vp, vp, vp, vp, vp, vp, i64, C.c_float, C.c_float, C.c_float, C.c_float,

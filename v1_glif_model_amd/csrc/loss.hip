@@ -136,6 +136,44 @@ __global__ void __launch_bounds__(kBlock) k_rate_final(RateArgs a, int parts) {
     }
 }
 
+// Mean-squared firing-rate error (the benchmark's configuration-2 loss): per neuron
+// rbar = count / S, diff = rbar - target; loss = sum diff^2 / N in a fixed order,
+// gz_neuron += diff * scale with scale = 2 / (N * S) (the per-tick dL/dz).
+__global__ void __launch_bounds__(kBlock)
+    k_rate_mse(const int32_t *__restrict__ count, int32_t rows, int32_t N, float S, const float *__restrict__ tgt,
+               float scale, float *__restrict__ gz, float *__restrict__ partial) {
+    __shared__ float red[kBlock];
+    float acc = 0.0f;
+    for (int32_t n = blockIdx.x * blockDim.x + threadIdx.x; n < N; n += gridDim.x * blockDim.x) {
+        int32_t c = 0;
+        for (int32_t r = 0; r < rows; ++r) c += count[static_cast<int64_t>(r) * N + n];
+        const float diff = static_cast<float>(c) / S - tgt[n];
+        acc = acc + diff * diff;
+        gz[n] = gz[n] + diff * scale;
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = kBlock / 2; w > 0; w >>= 1) {
+        if (static_cast<int>(threadIdx.x) < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+__global__ void __launch_bounds__(kBlock) k_rate_mse_final(const float *__restrict__ partial, int parts, float N,
+                                                            float *__restrict__ loss) {
+    __shared__ float red[kBlock];
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < parts; i += kBlock) acc = acc + partial[i];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = kBlock / 2; w > 0; w >>= 1) {
+        if (static_cast<int>(threadIdx.x) < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) loss[0] = red[0] / N;
+}
+
 int bits_for(uint64_t v) {   // bits needed to hold values < v
     int b = 0;
     while (b < 64 && (uint64_t(1) << b) < v) ++b;
@@ -239,6 +277,27 @@ int glif_rate_dist_loss(const int32_t *count, int32_t count_rows, int32_t n_neur
     hipLaunchKernelGGL(k_rate_terms, dim3(parts), dim3(kBlock), 0, s, a);
     GLIF_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_rate_final, dim3(1), dim3(kBlock), 0, s, a, parts);
+    GLIF_HIP(hipGetLastError());
+    return GLIF_OK;
+}
+
+size_t glif_rate_mse_workspace(void) { return kLossParts * sizeof(float); }
+
+int glif_rate_mse_loss(const int32_t *count, int32_t count_rows, int32_t n_neurons, int32_t n_samples,
+                       const float *targets, float *loss_out, float *gz_neuron, void *ws, size_t ws_bytes,
+                       void *stream) {
+    if (!count || !targets || !loss_out || !gz_neuron) return fail(GLIF_EINVAL, "NULL argument");
+    if (count_rows <= 0 || n_neurons <= 0 || n_samples <= 0)
+        return fail(GLIF_EINVAL, "count_rows, n_neurons and n_samples must be > 0");
+    if (!ws || ws_bytes < glif_rate_mse_workspace()) return fail(GLIF_ENOMEM, "workspace too small");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int parts = std::min<int>(kLossParts, (n_neurons + kBlock - 1) / kBlock);
+    const float scale = static_cast<float>(2.0 / (static_cast<double>(n_neurons) * n_samples));
+    hipLaunchKernelGGL(k_rate_mse, dim3(parts), dim3(kBlock), 0, s, count, count_rows, n_neurons,
+                       static_cast<float>(n_samples), targets, scale, gz_neuron, static_cast<float *>(ws));
+    GLIF_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_rate_mse_final, dim3(1), dim3(kBlock), 0, s, static_cast<const float *>(ws), parts,
+                       static_cast<float>(n_neurons), loss_out);
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;
 }

@@ -22,7 +22,7 @@ import torch
 
 from ._lib import check, lib, ptr, stream_ptr
 
-__all__ = ["VoltageRegularization", "SpikeRateDistributionTarget", "CELL_TYPE_ORDER",
+__all__ = ["VoltageRegularization", "SpikeRateDistributionTarget", "RateMSE", "CELL_TYPE_ORDER",
            "population_neuron_ids", "sample_firing_rates", "load_neuropixels_type_rates",
            "neuropixels_cell_type_to_cell_type"]
 
@@ -252,5 +252,33 @@ class SpikeRateDistributionTarget:
                                         ptr(gz_neuron), ptr(self._ws), self._ws.numel(),
                                         stream_ptr(self.device)))
         self._offset += self._n_sel
+        self.gz_neuron = gz_neuron
+        return loss
+
+
+class RateMSE:
+    """Mean-squared firing-rate error against per-neuron targets (spikes per tick): the loss
+    the benchmark's training configuration names.  ``__call__(spike_count, T)`` takes the
+    forward's spike counts [B, N] over T ticks; dL/dz per tick is added into ``gz_neuron``."""
+
+    def __init__(self, targets, device="cuda"):
+        self.device = torch.device(device)
+        self.targets = torch.as_tensor(targets, dtype=torch.float32, device=self.device).contiguous()
+        self._ws = torch.empty(int(lib().glif_rate_mse_workspace()), dtype=torch.uint8, device=self.device)
+        self.gz_neuron = None
+
+    def __call__(self, spike_count, T, gz_neuron=None):
+        spike_count = spike_count.contiguous()
+        if spike_count.dtype != torch.int32:
+            raise TypeError("spike_count must be int32")
+        N = int(spike_count.shape[-1])
+        if N != self.targets.numel():
+            raise ValueError("one target per neuron")
+        rows = spike_count.numel() // N
+        if gz_neuron is None:
+            gz_neuron = torch.zeros(N, dtype=torch.float32, device=self.device)
+        loss = torch.empty((), dtype=torch.float32, device=self.device)
+        check(lib().glif_rate_mse_loss(ptr(spike_count), rows, N, int(T) * rows, ptr(self.targets), ptr(loss),
+                                       ptr(gz_neuron), ptr(self._ws), self._ws.numel(), stream_ptr(self.device)))
         self.gz_neuron = gz_neuron
         return loss
