@@ -939,6 +939,7 @@ __global__ void __launch_bounds__(kBlock)
 
 // --------------------------------------------------------------- adjoint ----
 constexpr int kDelayUnroll = 8;
+constexpr int kAdjMaxWin = 3;  // reverse ticks per window (3 when 3 * B <= 16, else 1)
 
 struct AdjArgs {
     CellConst k;
@@ -1007,39 +1008,12 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
         gR[q] = a.gR[static_cast<int64_t>(q) * BN + bn];
     }
     const float decay = a.decay[n], cfn = a.cf[n];
-    for (int w = 0; w < a.nw; ++w) {
-        const int t = a.t0 - w;
-        float gz = 0.0f;
-        if (k.D <= kDelayUnroll) {
-            // the D ring values are loaded together, then summed from d = D down to 1
-            float zv[kDelayUnroll];
-#pragma unroll
-            for (int d = 1; d <= kDelayUnroll; ++d) {
-                const int s = t + d;
-                zv[d - 1] = (d <= k.D && s <= a.T - 3)
-                                ? a.dZ[(static_cast<int64_t>(s % a.ring) * k.B + b) * DN +
-                                       static_cast<int64_t>(d - 1) * k.N + n]
-                                : 0.0f;
-            }
-#pragma unroll
-            for (int d = kDelayUnroll; d >= 1; --d)
-                if (d <= k.D && t + d <= a.T - 3) gz = gz + zv[d - 1] * k.rd_scale;
-        } else {
-            for (int d = k.D; d >= 1; --d) {
-                const int s = t + d;
-                if (s > a.T - 3) continue;
-                gz = gz + a.dZ[(static_cast<int64_t>(s % a.ring) * k.B + b) * DN +
-                               static_cast<int64_t>(d - 1) * k.N + n] *
-                              k.rd_scale;
-            }
-        }
-        const int64_t tbn = static_cast<int64_t>(t) * BN + bn;
-        if (a.gz) gz = gz + a.gz[tbn];
-        if (a.gz_neuron && t >= a.gzn_t0 && t < a.gzn_t1) gz = gz + a.gz_neuron[n];
-        const bool refr = (a.refbits[(static_cast<int64_t>(t) * k.B + b) * k.W + (n >> 6)] >> (n & 63)) & 1ull;
+    // one reverse tick given its loaded inputs: dL/dz (ring sum + loss terms), refractory
+    // bit, saved voltage, dL/dv
+    auto tick = [&](int w, float gz, bool refr, float vsv, float gvx) {
         float psi = 0.0f;
         if (!refr) {
-            const float vsc = a.vsave[tbn] - 1.0f;
+            const float vsc = vsv - 1.0f;
             if (k.pseudo_gauss) {
                 const float q = -(vsc * vsc) / (k.gauss_std * k.gauss_std);
                 psi = expf(q) * k.damp;
@@ -1049,8 +1023,8 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
             }
         }
         float gV = gz * psi;
-        if (a.gv) gV = gV + a.gv[tbn];
-        if (a.vmode) gV = gV + vpenalty_grad(a.vmode, a.vsave[tbn]) * a.vscale;
+        if (a.gv) gV = gV + gvx;
+        if (a.vmode) gV = gV + vpenalty_grad(a.vmode, vsv) * a.vscale;
         gV = gV + (gVc * decay) * k.om;
         gVc = (k.hard_reset && refr) ? 0.0f : gV;
         float dy[kMaxBasis];
@@ -1068,6 +1042,64 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
                 Gl[(s * nr + (n - n0)) * a.R + e] = g;
             else
                 a.G[(static_cast<int64_t>(s) * k.N + n) * a.R + e] = g;
+        }
+    };
+    auto refbit = [&](int t) {
+        return ((a.refbits[(static_cast<int64_t>(t) * k.B + b) * k.W + (n >> 6)] >> (n & 63)) & 1ull) != 0ull;
+    };
+    const float gzn = a.gz_neuron ? a.gz_neuron[n] : 0.0f;
+    if (k.D <= kDelayUnroll && a.nw <= kAdjMaxWin) {
+        // every input of the window's ticks is loaded up front (none of them is written
+        // by this window), then the ticks run in order
+        float zv[kAdjMaxWin][kDelayUnroll];
+        float lz[kAdjMaxWin], vs[kAdjMaxWin], gvw[kAdjMaxWin];
+        bool rf[kAdjMaxWin];
+#pragma unroll
+        for (int w = 0; w < kAdjMaxWin; ++w) {
+            const int t = a.t0 - w;
+            const bool on = w < a.nw;
+#pragma unroll
+            for (int d = 1; d <= kDelayUnroll; ++d) {
+                const int s = t + d;
+                zv[w][d - 1] = (on && d <= k.D && s <= a.T - 3)
+                                   ? a.dZ[(static_cast<int64_t>(s % a.ring) * k.B + b) * DN +
+                                          static_cast<int64_t>(d - 1) * k.N + n]
+                                   : 0.0f;
+            }
+            const int64_t tbn = static_cast<int64_t>(on ? t : a.t0) * BN + bn;
+            lz[w] = (on && a.gz) ? a.gz[tbn] : 0.0f;
+            rf[w] = on ? refbit(t) : false;
+            vs[w] = on ? a.vsave[tbn] : 0.0f;
+            gvw[w] = (on && a.gv) ? a.gv[tbn] : 0.0f;
+        }
+#pragma unroll
+        for (int w = 0; w < kAdjMaxWin; ++w) {
+            if (w >= a.nw) break;
+            const int t = a.t0 - w;
+            // the D ring values summed from d = D down to 1, then the loss terms
+            float gz = 0.0f;
+#pragma unroll
+            for (int d = kDelayUnroll; d >= 1; --d)
+                if (d <= k.D && t + d <= a.T - 3) gz = gz + zv[w][d - 1] * k.rd_scale;
+            if (a.gz) gz = gz + lz[w];
+            if (a.gz_neuron && t >= a.gzn_t0 && t < a.gzn_t1) gz = gz + gzn;
+            tick(w, gz, rf[w], vs[w], gvw[w]);
+        }
+    } else {
+        for (int w = 0; w < a.nw; ++w) {
+            const int t = a.t0 - w;
+            float gz = 0.0f;
+            for (int d = k.D; d >= 1; --d) {
+                const int s = t + d;
+                if (s > a.T - 3) continue;
+                gz = gz + a.dZ[(static_cast<int64_t>(s % a.ring) * k.B + b) * DN +
+                               static_cast<int64_t>(d - 1) * k.N + n] *
+                              k.rd_scale;
+            }
+            const int64_t tbn = static_cast<int64_t>(t) * BN + bn;
+            if (a.gz) gz = gz + a.gz[tbn];
+            if (a.gz_neuron && t >= a.gzn_t0 && t < a.gzn_t1) gz = gz + gzn;
+            tick(w, gz, refbit(t), a.vsave[tbn], a.gv ? a.gv[tbn] : 0.0f);
         }
     }
     a.gV[bn] = gVc;
