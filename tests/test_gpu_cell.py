@@ -211,3 +211,40 @@ def test_fused_voltage_regularization(mode):
         scale = np.max(np.abs(e))
         assert scale > 0
         assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
+
+
+def test_deterministic_fallback_pull_bit_exact():
+    """A network whose activity bitmaps exceed the LDS budget (D * N bits > 64 KB) takes the
+    global-memory row pull instead of the resident chunk kernel; still bit-exact."""
+    cfg = tiny_config(n=120_000, fanin=6, delays=5, n_lgn=200, lgn_fanin=4, n_bkg=10, bkg_fanin=2,
+                      rs=4.0, ins=20.0, lgn_p=0.2)
+    tn = network(cfg, seed=4)
+    T, B = 20, 2
+    lgn, bkg = _inputs(cfg, T, B, seed=5)
+    cell = _cell(tn, "deterministic", **CELL_KW)
+    z, v, _ = cell.rollout(lgn, bkg)
+    oz, ov, _, _ = _oracle(tn[1], **ORC_KW).forward(lgn, bkg)
+    assert oz.sum() > 0
+    np.testing.assert_array_equal(z.cpu().numpy().astype(np.uint8), oz)
+    np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), ov.view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 7])
+def test_short_sequences_forward_and_backward(T):
+    """Sequences shorter than / around one backward window (no window for T < 3)."""
+    cfg = tiny_config(rs=2.0, ins=3.0, delays=1)
+    tn = network(cfg, seed=6, dense_basis=True)
+    B = 2
+    lgn, bkg = _inputs(cfg, T, B, seed=7)
+    cell = _cell(tn, "deterministic", **CELL_KW)
+    z, v, _ = cell.rollout(lgn, bkg)
+    oc = _oracle(tn[1], **ORC_KW)
+    oz, ov, oref, _ = oc.forward(lgn, bkg)
+    np.testing.assert_array_equal(z.cpu().numpy().astype(np.uint8), oz)
+    np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), ov.view(np.uint32))
+    gz = np.random.default_rng(T).normal(0, 1, oz.shape).astype(np.float32)
+    g = cell.backward(gz=torch.tensor(gz, device="cuda"))
+    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz)
+    for k in ("rec", "lgn", "bkg"):
+        a, e = g[k].cpu().numpy(), og[k]
+        assert np.max(np.abs(a - e)) <= 1e-5 * max(np.max(np.abs(e)), 1e-30) + 1e-6, k
