@@ -47,6 +47,10 @@ def _args():
     ap.add_argument("--cpu-steps", type=int, default=10,
                     help="timesteps of the CPU baseline sample (0: skip)")
     ap.add_argument("--forward-only", action="store_true")
+    ap.add_argument("--op", action="store_true",
+                    help="time the op-level entry points instead (calculate_synaptic_currents forward in "
+                         "both modes and its custom gradient) on the config-2 recurrent table, B=5, "
+                         "z_buf spikes at 5 Hz")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (5 times): the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -201,8 +205,60 @@ def sweep_rates(args):
         "sweep": rows}))
 
 
+def bench_op(args):
+    """Op-level timing (glif_syn_fwd / glif_syn_bwd, models.py:103-263) on the config-2
+    recurrent table: z_buf [5][D*N] Bernoulli(0.005) spikes, dy [5*N][nb] normal."""
+    import numpy as np
+    import torch
+    from v1_glif_model_amd import synthetic as sy
+    from v1_glif_model_amd.ops import SynapseTable
+    from v1_glif_model_amd.tables import build_cell_tables
+    cfg = sy.config(2)
+    tb = build_cell_tables(sy.make_network(cfg, seed=0))
+    N, D, B, nb = tb.n_neurons, tb.max_delay, 5, tb.n_basis
+    t = SynapseTable(np.stack([tb.rec.post, tb.rec.col], -1), tb.rec.syn_id, (N, tb.rec.n_cols), tb.basis,
+                     n_delay_slots=D)
+    t.set_weights(torch.tensor(tb.rec.weight, device="cuda"))
+    rng = np.random.default_rng(3)
+    z = torch.tensor((rng.uniform(size=(B, D * N)) < 0.005).astype(np.float32), device="cuda")
+    dy = torch.tensor(rng.normal(0, 1, (B * N, nb)).astype(np.float32), device="cuda")
+    zc = z.cpu().numpy()
+    events = int(sum(np.count_nonzero(zc[b][tb.rec.col]) for b in range(B)))
+    out = {}
+    for name, fn in (("fwd_event", lambda: t.forward(z, mode="event")),
+                     ("fwd_deterministic", lambda: t.forward(z, mode="deterministic")),
+                     ("bwd", lambda: t.backward(z, dy))):
+        for _ in range(max(args.warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1000.0 / args.steps
+    S = tb.rec.n_syn
+    print(json.dumps({
+        "metric": "op-level synaptic-current forward / custom gradient, us per call",
+        "value": round(out["fwd_event"] + out["bwd"], 2), "unit": "us per fwd+bwd call", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "higher_is_better": False, "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"config-2 recurrent table: {N} posts, {D} delay slots, {S} synapses, B={B}, "
+                               f"z_buf density 0.005 ({events} synapse events per call)",
+                   "neurons": N, "synapses": S, "batch": B},
+        "us_per_call": {k: round(v, 2) for k, v in out.items()},
+        "synaptic_events_per_s": {"fwd_event": round(events / (out["fwd_event"] * 1e-6), 1),
+                                  "fwd_deterministic": round(events / (out["fwd_deterministic"] * 1e-6), 1)},
+        # the gradient touches every synapse for every batch entry: dz needs all of them
+        "bwd_synapse_batch_products_per_s": round(S * B / (out["bwd"] * 1e-6), 1)}))
+
+
 def main():
     args = _args()
+    if args.op and args.gpus == 1:
+        bench_op(args)
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return

@@ -73,6 +73,8 @@ struct Table {
     int32_t *ph_ptr = nullptr;    // [n_types * n_cols + 1]
     int32_t *ph_order = nullptr;  // [n_syn]       synapse id at position k
     uint2 *ph_pw = nullptr;       // [n_syn]       {post, weight bits}
+    int32_t *order_inv = nullptr; // [n_syn]       position of synapse s in the column-grouped order
+    int32_t *ph_inv = nullptr;    // [n_syn]       position of synapse s in the type-phased order
     float *basis_host = nullptr;  // host copy [n_types][n_basis]
 };
 
@@ -121,7 +123,6 @@ struct Carver {
 // ---- launch helpers (defined in the .hip files) ----------------------------
 int launch_fill_u32(void *p, uint32_t value, size_t n, hipStream_t s);
 int launch_gather_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s);
-int launch_scatter_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s);
 
 inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
 

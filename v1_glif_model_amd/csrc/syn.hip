@@ -5,6 +5,7 @@
 #include "compact.h"
 #include "glif_internal.h"
 #include "prof.h"
+#include "pull_kernels.h"
 #include "syn_kernels.h"
 
 namespace glif {
@@ -83,6 +84,28 @@ __global__ void __launch_bounds__(kBlock)
     write_G(G, n, b, Bp, d, basis_lds, n_types, nb, n_post);
 }
 
+// Batch masks and "active in some batch entry" bitmaps of a dense z [B][n_cols] in the
+// row pull's layout: slot plane n_slots - d holds column pre + n_pre * (d - 1) at bit
+// pre (planes of pre_pad = round64(n_pre) bits); one thread per (plane, pre), one wave per
+// 64-bit word.
+__global__ void __launch_bounds__(kBlock)
+    k_op_colmask(const float *__restrict__ z, int32_t B, int64_t n_cols, int32_t n_pre, int32_t n_slots,
+                 int32_t pre_pad, uint32_t *__restrict__ cm, uint64_t *__restrict__ bits) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(n_slots) * pre_pad) return;  // whole waves (pre_pad % 64 == 0)
+    const int32_t plane = static_cast<int32_t>(i / pre_pad);
+    const int32_t pre = static_cast<int32_t>(i - static_cast<int64_t>(plane) * pre_pad);
+    uint32_t m = 0u;
+    if (pre < n_pre) {
+        const int64_t c = pre + static_cast<int64_t>(n_pre) * (n_slots - 1 - plane);
+        for (int b = 0; b < B; ++b)
+            if (z[static_cast<int64_t>(b) * n_cols + c] > 0.0f) m |= 1u << b;
+    }
+    cm[i] = m;
+    const uint64_t bal = __ballot(m != 0u);
+    if ((threadIdx.x & (kWave - 1)) == 0) bits[i >> 6] = bal;
+}
+
 template <int LG>
 __global__ void __launch_bounds__(kBlock) k_syn_bwd_cols(ColArgs a, ActDense act) {
     bwd_cols<LG, 2>(a, act);
@@ -102,22 +125,25 @@ int grid_subwaves(int64_t items, int L) {
 int batch_pad(int B) { return B <= 4 ? 4 : (B <= 8 ? 8 : (B <= 16 ? 16 : 32)); }
 
 struct SynWs {
+    uint32_t *cm;      // [n_slots * pre_pad] batch masks (deterministic forward)
+    uint64_t *cbits;   // [n_slots * pre_pad / 64] activity bitmaps
     int64_t *row_off;
     int32_t *cols;
     uint32_t *masks;
     float *G;
-    float *dw_col;
     void *scratch;
 };
 
 static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes) {
     Carver cv(ws, SIZE_MAX);
     SynWs w{};
+    const int64_t pre_pad = (static_cast<int64_t>(t->n_pre) + 63) / 64 * 64;
+    w.cm = cv.take<uint32_t>(static_cast<size_t>(t->n_slots) * pre_pad);
+    w.cbits = cv.take<uint64_t>(static_cast<size_t>(t->n_slots) * pre_pad / 64);
     w.row_off = cv.take<int64_t>(2);
     w.cols = cv.take<int32_t>(t->n_cols);
     w.masks = cv.take<uint32_t>(t->n_cols);
     w.G = cv.take<float>(static_cast<size_t>(t->n_post) * t->n_types * batch_pad(B));
-    w.dw_col = cv.take<float>(std::max<int64_t>(t->n_syn, 1));
     w.scratch = cv.take<char>(compact_scratch_bytes(1, t->n_cols));
     if (bytes) *bytes = cv.off;
     return w;
@@ -146,6 +172,46 @@ int glif_syn_fwd(const glif_table *tt, const float *z, int32_t B, int32_t counts
     const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     const int64_t nI = static_cast<int64_t>(B) * t->n_post;
     if (mode == GLIF_MODE_DETERMINISTIC) {
+        if (!counts && t->pidx && t->chunk_desc) {
+            // the resident chunk pull over activity bitmaps built from z (one step, t = 0)
+            if (!ws || ws_bytes < glif_syn_workspace(tt, B)) return fail(GLIF_ENOMEM, "workspace too small");
+            SynWs w = carve_syn(ws, t, B, nullptr);
+            const int32_t pre_pad = static_cast<int32_t>((static_cast<int64_t>(t->n_pre) + 63) / 64 * 64);
+            PullArgs pa{};
+            pa.t = 0;
+            pa.T = 1;
+            pa.N = t->n_post;
+            pa.Np = pre_pad;
+            pa.B = B;
+            pa.D = t->n_slots;
+            pa.nb = t->n_basis;
+            pa.n_types = t->n_types;
+            pa.os_r = 1;
+            pa.os_b = static_cast<int64_t>(t->n_post) * t->n_basis;
+            pa.os_n = t->n_basis;
+            pa.W = pre_pad / 64;
+            pa.Wl = 0;
+            pa.rec_chunks = t->n_chunks;
+            pa.rec_cdesc = t->chunk_desc;
+            pa.rec_row = t->row_ptr;
+            pa.rec_pidx = t->pidx;
+            pa.rec_sid = t->sid_row;
+            pa.rec_w = t->w_row;
+            pa.zmask = w.cm;
+            pa.abits = w.cbits;
+            pa.lbits = w.cbits;
+            pa.basis = t->basis;
+            pa.I = I;
+            if (pull_chunked(pa)) {
+                const int64_t n_mask = static_cast<int64_t>(t->n_slots) * pre_pad;
+                hipLaunchKernelGGL(k_op_colmask, dim3(ceil_div(n_mask, kBlock)), dim3(kBlock), 0, s, z, B, t->n_cols,
+                                   t->n_pre, t->n_slots, pre_pad, w.cm, w.cbits);
+                GLIF_HIP(hipGetLastError());
+                launch_pull_chunks(pa, s);
+                GLIF_HIP(hipGetLastError());
+                return GLIF_OK;
+            }
+        }
         dim3 grid(ceil_div(nI, kBlock));
         if (counts)
             hipLaunchKernelGGL((k_syn_pull_dense<true>), grid, dim3(kBlock), lds, s, z, B, t->n_cols,
@@ -202,8 +268,9 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     hipLaunchKernelGGL(k_make_G, dim3(ceil_div(nI, kBlock)), dim3(kBlock), lds, s, dy, B, t->n_post, Bp,
                        t->basis, t->n_types, t->n_basis, w.G);
     GLIF_HIP(hipGetLastError());
-    if (dw && (rc = launch_fill_u32(w.dw_col, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
-    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, t->ph_pw, w.G, dz ? 1 : 0, dw ? w.dw_col : nullptr};
+    // one pass writes every active synapse's dW once, in reference order; the rest stay 0
+    if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
+    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, t->ph_pw, w.G, dz ? 1 : 0, dw, t->ph_order};
     ActDense act{z, dz, t->n_cols, counts};
     const dim3 grid(ceil_div(t->n_cols * (Bp / 4), kBlock));
     switch (Bp / 4) {
@@ -213,7 +280,6 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
         default: hipLaunchKernelGGL(k_syn_bwd_cols<8>, grid, dim3(kBlock), 0, s, ca, act); break;
     }
     GLIF_HIP(hipGetLastError());
-    if (dw) return launch_scatter_f32(dw, w.dw_col, t->ph_order, t->n_syn, s);
     return GLIF_OK;
 }
 

@@ -170,6 +170,9 @@ struct ColArgs {
     const float *G;          // [n_types][n_post][R], < 4 GiB
     int32_t want_dz;
     float *dw;               // [n_syn] type-phased order, accumulated; or nullptr
+    // when set, each synapse's dW is written once, straight to dw[dw_ref[k]] (reference
+    // order, the caller zero-fills dw) instead of accumulated at position k
+    const int32_t *dw_ref;
 };
 
 // Op-level activity: z [B][n_cols] dense, element e = b.
@@ -228,7 +231,12 @@ __device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
             // an active column's dW values travel with the entries (no extra round trip)
             float old[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) old[u] = (any && q == 0 && k0 + u < hi) ? a.dw[k0 + u] : 0.0f;
+            for (int u = 0; u < U; ++u)
+                old[u] = (any && q == 0 && k0 + u < hi) ? (a.dw_ref ? 0.0f : a.dw[k0 + u]) : 0.0f;
+            int32_t dst[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                dst[u] = (any && q == 0 && k0 + u < hi) ? (a.dw_ref ? a.dw_ref[k0 + u] : k0 + u) : 0;
             float4 g[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) g[u] = *reinterpret_cast<const float4 *>(Gs + e[u].x * (R * 4u));
@@ -261,7 +269,7 @@ __device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
                 if (q == 0) {
 #pragma unroll
                     for (int u = 0; u < U; ++u)
-                        if (k0 + u < hi) a.dw[k0 + u] = old[u] + pp[u];
+                        if (k0 + u < hi) a.dw[dst[u]] = old[u] + pp[u];
                 }
             }
         }

@@ -51,13 +51,6 @@ __global__ void k_gather_ell_w(uint2 *__restrict__ dst, const float *__restrict_
     for (; i < n; i += stride) dst[i].y = idx[i] >= 0 ? __float_as_uint(src[idx[i]]) : 0u;
 }
 
-__global__ void k_scatter_f32(float *__restrict__ dst, const float *__restrict__ src,
-                              const int32_t *__restrict__ idx, int64_t n) {
-    int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (; i < n; i += stride) dst[idx[i]] = src[i];
-}
-
 static int grid_for(int64_t n) {
     int64_t g = (n + kBlock - 1) / kBlock;
     return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(g, 8192)));
@@ -74,13 +67,6 @@ int launch_fill_u32(void *p, uint32_t value, size_t n, hipStream_t s) {
 int launch_gather_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s) {
     if (n == 0) return GLIF_OK;
     hipLaunchKernelGGL(k_gather_f32, dim3(grid_for(n)), dim3(kBlock), 0, s, dst, src, idx, n);
-    GLIF_HIP(hipGetLastError());
-    return GLIF_OK;
-}
-
-int launch_scatter_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s) {
-    if (n == 0) return GLIF_OK;
-    hipLaunchKernelGGL(k_scatter_f32, dim3(grid_for(n)), dim3(kBlock), 0, s, dst, src, idx, n);
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;
 }
@@ -111,7 +97,7 @@ static void free_table(Table *t) {
     if (!t) return;
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
                     t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
-                    t->chunk_desc, t->pidx};
+                    t->chunk_desc, t->pidx, t->order_inv, t->ph_inv};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete[] t->basis_host;
@@ -195,6 +181,13 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         ph_pw[k].y = 0u;  // the weight, written by glif_table_set_weights
     }
 
+    // inverse permutations: position of synapse s in the column-grouped and type-phased
+    // orders (gradients go back to reference order with coalesced writes)
+    std::vector<int32_t> order_inv(n_syn), ph_inv(n_syn);
+    for (int64_t k = 0; k < n_syn; ++k) {
+        order_inv[order[k]] = static_cast<int32_t>(k);
+        ph_inv[ph_order[k]] = static_cast<int32_t>(k);
+    }
     std::vector<uint32_t> ps(n_syn), pd(n_syn);
     // bit index of the entry's presynaptic spike in a stack of per-slot activity planes
     // of round64(n_pre) bits, slot d at plane n_slots - d (the newest step last)
@@ -272,6 +265,8 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         (rc = upload(&t->sid_row, sid_row.data(), sid_row.size())) ||
         (rc = upload(&t->ph_ptr, ph_ptr.data(), ph_ptr.size())) ||
         (rc = upload(&t->ph_order, ph_order.data(), ph_order.size())) ||
+        (rc = upload(&t->order_inv, order_inv.data(), order_inv.size())) ||
+        (rc = upload(&t->ph_inv, ph_inv.data(), ph_inv.size())) ||
         (rc = upload(&t->ph_pw, ph_pw.data(), ph_pw.size())) ||
         (ell_len && (rc = upload(&t->ell_pw, ell_pw.data(), ell_pw.size()))) ||
         (ell_len && (rc = upload(&t->ell_src, ell_src.data(), ell_src.size())))) {
