@@ -213,10 +213,12 @@ def test_fused_voltage_regularization(mode):
         assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
 
 
-def test_deterministic_fallback_pull_bit_exact():
-    """A network whose activity bitmaps exceed the LDS budget (D * N bits > 64 KB) takes the
-    global-memory row pull instead of the resident chunk kernel; still bit-exact."""
-    cfg = tiny_config(n=120_000, fanin=6, delays=5, n_lgn=200, lgn_fanin=4, n_bkg=10, bkg_fanin=2,
+@pytest.mark.parametrize("n", [120_000, 270_000])
+def test_deterministic_large_bitmaps_bit_exact(n):
+    """Large activity bitmaps: at 120k neurons (75 KB) the chunk kernel runs one 1024-lane
+    workgroup per CU; at 270k (169 KB, beyond the 160 KB of LDS) the global-memory row pull
+    runs instead.  Both bit-exact."""
+    cfg = tiny_config(n=n, fanin=6, delays=5, n_lgn=200, lgn_fanin=4, n_bkg=10, bkg_fanin=2,
                       rs=4.0, ins=20.0, lgn_p=0.2)
     tn = network(cfg, seed=4)
     T, B = 20, 2

@@ -289,8 +289,8 @@ __device__ inline void copy_to_lds(uint64_t *dst, const uint64_t *src, int n) {
     }
 }
 
-template <int G>
-__global__ void __launch_bounds__(kPullBlock) k_pull_chunks(PullArgs a) {
+template <int G, int BLOCK>
+__global__ void __launch_bounds__(BLOCK) k_pull_chunks(PullArgs a) {
     extern __shared__ float lds_f[];
     float *basis_lds = lds_f;
     const int nbasis = a.n_types * a.nb;
@@ -389,43 +389,56 @@ static bool pull_chunked(const PullArgs &pa) {
     // 32-bit offsets of the batch-mask gathers
     const bool fits = static_cast<int64_t>(pa.T + pa.D) * pa.Np < (int64_t(1) << 32) &&
                       static_cast<int64_t>(pa.T) * pa.n_lgn < (int64_t(1) << 32);
-    return fits && pa.rec_pidx && (pa.lgn_chunks == 0 || pa.lgn_pidx) && lb <= ds.lds_per_block && lb <= 65536 &&
+    return fits && pa.rec_pidx && (pa.lgn_chunks == 0 || pa.lgn_pidx) && lb <= ds.lds_per_block &&
            pa.B * pa.nb <= 4 * kWave;
 }
 
-// The resident chunk kernel, when pull_chunked(pa); false (nothing launched) otherwise.
-static bool launch_pull_chunks(const PullArgs &pa, hipStream_t s) {
-    if (pull_chunked(pa)) {
-        const DevShape &ds = dev_shape();
-        const size_t lb = chunk_lds_bytes(pa);
-        const int G = (pa.B * pa.nb + kWave - 1) / kWave;
-        const void *fn = G == 1 ? reinterpret_cast<const void *>(&k_pull_chunks<1>)
-                         : G == 2 ? reinterpret_cast<const void *>(&k_pull_chunks<2>)
-                                  : reinterpret_cast<const void *>(&k_pull_chunks<4>);
-        // as many workgroups as stay resident (registers and LDS permitting), per device,
-        // G and LDS size
-        static int cache_pc[64][3];
-        static size_t cache_lb[64][3];
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-        const int gi = G == 1 ? 0 : G == 2 ? 1 : 2;
-        int per_cu = cache_pc[dev][gi];
-        if (per_cu < 1 || cache_lb[dev][gi] != lb) {
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPullBlock, lb) != hipSuccess ||
-                per_cu < 1)
-                per_cu = 1;
-            cache_pc[dev][gi] = per_cu;
-            cache_lb[dev][gi] = lb;
-        }
-        const dim3 grid(ds.n_cu * per_cu);
-        switch (G) {
-            case 1: hipLaunchKernelGGL(k_pull_chunks<1>, grid, dim3(kPullBlock), lb, s, pa); break;
-            case 2: hipLaunchKernelGGL(k_pull_chunks<2>, grid, dim3(kPullBlock), lb, s, pa); break;
-            default: hipLaunchKernelGGL(k_pull_chunks<4>, grid, dim3(kPullBlock), lb, s, pa); break;
-        }
-        return true;
+template <int BLOCK>
+static const void *chunk_kernel(int G) {
+    return G == 1 ? reinterpret_cast<const void *>(&k_pull_chunks<1, BLOCK>)
+           : G == 2 ? reinterpret_cast<const void *>(&k_pull_chunks<2, BLOCK>)
+                    : reinterpret_cast<const void *>(&k_pull_chunks<4, BLOCK>);
+}
+
+template <int BLOCK>
+static void launch_chunks(int G, dim3 grid, size_t lb, hipStream_t s, const PullArgs &pa) {
+    switch (G) {
+        case 1: hipLaunchKernelGGL((k_pull_chunks<1, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
+        case 2: hipLaunchKernelGGL((k_pull_chunks<2, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
+        default: hipLaunchKernelGGL((k_pull_chunks<4, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
     }
-    return false;
+}
+
+// The resident chunk kernel, when pull_chunked(pa); false (nothing launched) otherwise.
+// Workgroups of kPullBlock lanes, as many as stay resident; when the bitmaps leave room
+// for only one workgroup per CU, workgroups of 2 * kPullBlock lanes instead.
+static bool launch_pull_chunks(const PullArgs &pa, hipStream_t s) {
+    if (!pull_chunked(pa)) return false;
+    const DevShape &ds = dev_shape();
+    const size_t lb = chunk_lds_bytes(pa);
+    const int G = (pa.B * pa.nb + kWave - 1) / kWave;
+    const bool wide = ds.lds_per_cu / lb < 2;
+    const void *fn = wide ? chunk_kernel<2 * kPullBlock>(G) : chunk_kernel<kPullBlock>(G);
+    // resident workgroups per CU, per device, kernel and LDS size
+    static int cache_pc[64][6];
+    static size_t cache_lb[64][6];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    const int gi = (G == 1 ? 0 : G == 2 ? 1 : 2) + (wide ? 3 : 0);
+    int per_cu = cache_pc[dev][gi];
+    if (per_cu < 1 || cache_lb[dev][gi] != lb) {
+        if (lb > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lb));
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wide ? 2 * kPullBlock : kPullBlock, lb) !=
+                hipSuccess ||
+            per_cu < 1)
+            per_cu = 1;
+        cache_pc[dev][gi] = per_cu;
+        cache_lb[dev][gi] = lb;
+    }
+    const dim3 grid(ds.n_cu * per_cu);
+    if (wide) launch_chunks<2 * kPullBlock>(G, grid, lb, s, pa);
+    else launch_chunks<kPullBlock>(G, grid, lb, s, pa);
+    return true;
 }
 
 static void launch_pull(const PullArgs &pa, size_t lds, hipStream_t s) {
