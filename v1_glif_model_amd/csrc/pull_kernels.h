@@ -389,8 +389,10 @@ static bool pull_chunked(const PullArgs &pa) {
     // 32-bit offsets of the batch-mask gathers
     const bool fits = static_cast<int64_t>(pa.T + pa.D) * pa.Np < (int64_t(1) << 32) &&
                       static_cast<int64_t>(pa.T) * pa.n_lgn < (int64_t(1) << 32);
+    // one accumulator slot per lane (B * nb <= 64): with more, every hit costs several slot
+    // passes and the half-wave row pull (two rows per wave) was measured faster
     return fits && pa.rec_pidx && (pa.lgn_chunks == 0 || pa.lgn_pidx) && lb <= ds.lds_per_block &&
-           pa.B * pa.nb <= 4 * kWave;
+           pa.B * pa.nb <= kWave;
 }
 
 template <int BLOCK>
