@@ -91,8 +91,8 @@ def load_traffic(name):
 
 
 def sweep_rates(args):
-    """Config 4: forward throughput of the event push (K2) and the deterministic row pull
-    (K6) at several mean firing rates.  One global factor scales all three weight
+    """Config 4: forward throughput of the event push and the deterministic row pull
+    at several mean firing rates.  One global factor scales all three weight
     populations; it is set per target rate by bisection in log space on short rollouts
     (the achieved rate of the timed rollout is reported)."""
     import numpy as np
@@ -187,7 +187,7 @@ def sweep_rates(args):
                      "event_ms_per_step": round(ev_ms, 4), "pull_ms_per_step": round(pl_ms, 4),
                      "event_kernel_us_per_step": ev_k, "pull_kernel_us_per_step": pl_k,
                      "rec_events_per_step": round(events),
-                     # K2 bytes: 8-byte entry + one 4-byte atomic per event; K6: every
+                     # push bytes: 8-byte entry + one 4-byte atomic per event; pull: every
                      # post-row entry (4 bytes) + the active entries' weight and type (5)
                      "event_push_GBps": round(events * 12 / (ev_k.get("push", 1e9) * 1e-6) / 1e9, 1),
                      "pull_GBps": round((S * 4 + events * 5) / (pl_k.get("push", 1e9) * 1e-6) / 1e9, 1)})
@@ -200,7 +200,7 @@ def sweep_rates(args):
         "ms_per_step": min(best5["event_ms_per_step"], best5["pull_ms_per_step"]) if best5 else None,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"config 4: {N} GLIF_3 neurons, {S} recurrent synapses, B={B}, T={T}, "
-                               "modulated LGN, forward; event push (K2) vs deterministic row pull (K6)",
+                               "modulated LGN, forward; event push vs deterministic row pull",
                    "neurons": N, "recurrent_synapses": S, "batch": B, "seq_len": T},
         "sweep": rows}))
 

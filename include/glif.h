@@ -47,7 +47,7 @@ typedef struct glif_cell glif_cell;    /* GLIF_3 parameters + rec/LGN/bkg tables
 const char *glif_last_error(void);
 int glif_version(void);
 
-/* ---------------------------------------------------------------- A1 ---------
+/* ----------------------------------------------- CSR (pre_ind_table) --------
  * make_pre_ind_table (models.py:343-373 with _validate_inputs :299-315 and
  * _build_csr_order_numba :317-341): stable counting sort of synapse ids by
  * presynaptic column.  host in: cols [n_syn] int64 (column 1 of `indices`);
@@ -57,7 +57,7 @@ int glif_version(void);
 int glif_make_pre_ind_table(const int64_t *cols, int64_t n_syn, int64_t n_source,
                             int32_t *order, int32_t *row_splits, int64_t *bad_index);
 
-/* ---------------------------------------------------------------- A3 ---------
+/* -------------------------------------------------- spike compaction --------
  * tf.where(z > 0) (models.py:128, 823-826, 890): row-major list of (row, col)
  * pairs of a [rows][cols] float32 device array.  device out: pairs [<= rows*cols][2]
  * int64 and count [1] int64.  Workspace: glif_where_workspace(). */
@@ -65,7 +65,7 @@ size_t glif_where_workspace(int64_t rows, int64_t cols);
 int glif_where_gt0(const float *z, int64_t rows, int64_t cols, int64_t *pairs, int64_t *count,
                    void *ws, size_t ws_bytes, void *stream);
 
-/* ---------------------------------------------------------------- A2 ---------
+/* ----------------------------------------------------- synapse tables -------
  * Synapse table of one population, built from the arrays V1Column.__init__ keeps
  * (models.py:625-773).  host in, reference order (sorted by (post, pre)):
  *   post [n_syn] int64, col [n_syn] int64 (pre + n_post*(delay-1) for the recurrent
@@ -77,7 +77,7 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
                       const float *basis, int32_t n_types, int32_t n_basis, glif_table **out);
 void glif_table_destroy(glif_table *t);
 int64_t glif_table_n_syn(const glif_table *t);
-/* Device pointers owned by the table: the bit-exact A1 result (order int32 [n_syn],
+/* Device pointers owned by the table: the bit-exact pre_ind_table (order int32 [n_syn],
  * row_splits int32 [n_cols + 1]). */
 int glif_table_pre_ind(const glif_table *t, const int32_t **order, const int32_t **row_splits);
 /* refresh_recurrent_weight_shadow (models.py:966-976): copy the trainable weight
@@ -85,7 +85,7 @@ int glif_table_pre_ind(const glif_table *t, const int32_t **order, const int32_t
  * row-grouped copies.  Must be called before use and after every weight update. */
 int glif_table_set_weights(glif_table *t, const float *w, void *stream);
 
-/* ------------------------------------------------------------ A4-A8 ----------
+/* --------------------------------------- synaptic-current op (fwd, grad) ----
  * calculate_synaptic_currents (models.py:103-263).
  * Forward: z [B][n_cols] float32 device (event where z > 0; with counts != 0 the
  * value scales the weight as the background current does, models.py:917-931);
@@ -100,7 +100,7 @@ int glif_syn_fwd(const glif_table *t, const float *z, int32_t B, int32_t counts,
 int glif_syn_bwd(const glif_table *t, const float *z, const float *dy, int32_t B, int32_t counts,
                  float *dz, float *dw, void *ws, size_t ws_bytes, void *stream);
 
-/* ------------------------------------------------------------ A11-A17 --------
+/* --------------------------------------------------- GLIF_3 cell, BPTT -------
  * V1Column (models.py:450-1135) run over T steps on one stream. */
 typedef struct {
     int32_t n_neurons;

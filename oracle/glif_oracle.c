@@ -38,7 +38,7 @@
 #define ORC_ERANGE (-34)
 #define ORC_ENOMEM (-12)
 
-/* ------------------------------------------------------------------ A1 ---- */
+/* -------------------------------------------- CSR (pre_ind_table) build ---- */
 /* Returns 0, or ORC_EINVAL (n_cols <= 0), or ORC_ERANGE with *bad_index set to the
  * first offending synapse (models.py:308-314 raises ValueError there). */
 int orc_csr_build(const int64_t *cols, int64_t S, int64_t n_cols, int64_t *order,
@@ -62,7 +62,7 @@ int orc_csr_build(const int64_t *cols, int64_t S, int64_t n_cols, int64_t *order
     return 0;
 }
 
-/* ------------------------------------------------------------------ A3 ---- */
+/* ---------------------------------------------------- spike compaction ---- */
 int64_t orc_where_gt0(const float *z, int64_t rows, int64_t cols, int64_t *out)
 {
     int64_t n = 0;
@@ -75,7 +75,7 @@ int64_t orc_where_gt0(const float *z, int64_t rows, int64_t cols, int64_t *out)
     return n;
 }
 
-/* ------------------------------------------------------------- A4-A6 ---- */
+/* ------------------------------------------ synaptic currents (forward) ---- */
 /* act: [B][n_cols] values, an event where act > 0.  use_count: scale the weight by
  * the value (background Poisson counts, models.py:917-931); otherwise value 1.
  * I: [B*n_post][nb], accumulated into (the caller zeroes it). */
@@ -98,7 +98,7 @@ void orc_syn_fwd(int B, int64_t n_post, int64_t n_cols, int nb, const float *act
         }
 }
 
-/* ---------------------------------------------------------------- A7-A8 ---- */
+/* ------------------------------------------- custom gradient (dz and dW) ---- */
 /* dy: [B*n_post][nb].  dz: [B][n_cols] (written, may be NULL).  dW: [S] accumulated
  * (may be NULL).  act/use_count as in orc_syn_fwd (events for dW only).
  * scratch: [B][n_cols] floats when dz != NULL. */

@@ -90,7 +90,7 @@ def main():
     gz = rng.normal(0, 1, z.shape).astype(np.float32)
     gv = rng.normal(0, 0.1, z.shape).astype(np.float32)
     dW = oc.backward(lgn, bkg, z, ref, v, gz_loss=gz, gv_loss=gv)
-    # op level (A5, A7, A8) on the recurrent table: a random binary z and dy
+    # op level (currents, dz, dW) on the recurrent table: a random binary z and dy
     zop = (rng.random((B, tb.rec.n_cols)) < 0.05).astype(np.float32)
     dy = rng.normal(0, 1, (B * tb.n_neurons, tb.n_basis)).astype(np.float32)
     I_op = syn_fwd(tb.rec, zop, tb.basis)

@@ -1,4 +1,4 @@
-"""GPU parity of the T-step GLIF_3 cell (A11-A17) and its BPTT against the CPU oracle.
+"""GPU parity of the T-step GLIF_3 cell and its BPTT against the CPU oracle.
 
 Bars: deterministic mode reproduces the oracle's spike trains, voltages and final
 state bit for bit; event (atomic) mode keeps >= 99.9% per-neuron spike-count

@@ -1,4 +1,4 @@
-"""GPU parity of the synaptic-current operator (A1, A3-A8) against the CPU oracle.
+"""GPU parity of the synaptic-current operator (CSR build, spike compaction, currents, dz, dW) against the CPU oracle.
 
 Bars: compaction and CSR/CSC bit-exact; deterministic forward bit-exact with the
 oracle's reference-order fp32 sum; event (atomic) forward and the backward within

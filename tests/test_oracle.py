@@ -27,7 +27,7 @@ from tests.helpers import network, tiny_config
 from v1_glif_model_amd import synthetic as sy
 
 
-# ---------------------------------------------------------------- A1 -------
+# ------------------------------------------- CSR (pre_ind_table) build -------
 @settings(max_examples=60, deadline=None)
 @given(st.integers(1, 50), st.lists(st.integers(0, 49), max_size=300))
 def test_csr_build_matches_reference_numpy_fallback(n_cols, cols):
@@ -52,7 +52,7 @@ def test_csr_build_edge_cases():
         orc.csr_build(np.array([0]), 0)
 
 
-# ---------------------------------------------------------------- A3 -------
+# --------------------------------------------------- spike compaction -------
 @pytest.mark.parametrize("shape,p", [((1, 1), 1.0), ((3, 100), 0.1), ((5, 1000), 0.01), ((2, 0), 0.5)])
 def test_where_matches_argwhere(shape, p):
     rng = np.random.default_rng(shape[1])
@@ -60,7 +60,7 @@ def test_where_matches_argwhere(shape, p):
     np.testing.assert_array_equal(orc.where_gt0(z), np.argwhere(z > 0))
 
 
-# ------------------------------------------------------------- A4-A6 -------
+# ----------------------------------------- synaptic currents (forward) -------
 def _op_case(seed=0, B=3, p=0.05, dense_basis=True):
     cfg = tiny_config()
     _, tb = network(cfg, seed=seed, dense_basis=dense_basis)
@@ -113,7 +113,7 @@ def test_syn_fwd_invariants():
     np.testing.assert_array_equal(orc.syn_fwd(w2, z, tb.basis), 2 * orc.syn_fwd(tb.rec, z, tb.basis))
 
 
-# ------------------------------------------------------------- A7-A8 -------
+# ------------------------------------------ custom gradient (dz and dW) -------
 @pytest.mark.parametrize("seed", [0, 1])
 def test_syn_bwd_matches_float64_bruteforce(seed):
     tb, z, rng = _op_case(seed)

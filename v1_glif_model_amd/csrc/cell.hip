@@ -1,14 +1,15 @@
 // The GLIF_3 cell over T steps (V1Column.call, models.py:1059-1135) and its BPTT.
 //
 // Forward, per step t (one stream, no host round trip):
-//   event mode:   k_push(t)   rec spikes of steps t-1..t-D (ring of active lists)
-//                             and the step's LGN (column, batch-mask) list are
-//                             streamed through the column-grouped tables and added
-//                             into I with fp32 atomics;
-//                 k_step(t)   background pull, GLIF_3 update, spike bits, the
-//                             step's active list; I is re-zeroed after reading.
-//   deterministic: k_step(t)  pulls rec, LGN and background per post row in the
-//                             reference's accumulation order, then the same update.
+//   event mode:   k_push(t)   the spike words of steps t-1..t-D (set bits = columns of
+//                             the recurrent table) and the step's LGN (column,
+//                             batch-mask) list are streamed through the column-grouped
+//                             tables and added into I with fp32 atomics;
+//                 k_step(t)   background pull, GLIF_3 update, spike bits (wave
+//                             ballots); I is re-zeroed after reading.
+//   deterministic: the row pull (pull_kernels.h) sums rec and LGN per post row in
+//                 the reference's accumulation order, then k_step(t) adds the
+//                 background and does the same update.
 // Backward, in windows of Wwin reverse ticks t0, t0-1, .. (lagged adjoint, k_adj):
 //   k_adj         per tick t: gz_t -> gV_t -> gP_{t-1} -> gR_{t-2} -> G_{t-2}
 //   k_bwd_rec     dz of the window's steps t0-2, t0-3, .. over every recurrent
@@ -745,7 +746,7 @@ struct BwdInArgs {
     float *dw;           // column-grouped order, accumulated
 };
 
-// dW of one window's input events (A8 for LGN, models.py:814-863 autodiff, and the
+// dW of one window's input events (the LGN weight gradient, models.py:814-863 autodiff, and the
 // background source): item (column, mask over w*B + b) -> every synapse k of the
 // column adds G[sid][post][e] * mult for the set elements e in ascending order
 // (reverse time, then batch), the order in which the reference's per-step

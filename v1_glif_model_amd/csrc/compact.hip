@@ -1,4 +1,4 @@
-// Ordered stream compaction (A3: tf.where(z > 0), models.py:128).
+// Ordered stream compaction (tf.where(z > 0), models.py:128).
 //
 // A [rows][cols] predicate is cut into tiles of kTile consecutive elements that
 // never cross a row.  Pass 1 counts the active elements of every tile, pass 2

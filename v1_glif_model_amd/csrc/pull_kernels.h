@@ -12,7 +12,7 @@
 namespace glif {
 
 // ------------------------------------------------------ deterministic pull ----
-// The currents of step t in the reference's order (A6, models.py:141-169 and
+// The currents of step t in the reference's order (models.py:141-169 and
 // 841-857 summed as TF's CPU UnsortedSegmentSum meets the events): per (b, post, r)
 // from +0, the recurrent events in ascending (column, synapse id) of the post row,
 // the LGN events likewise, then I = rec + lgn (the background is added by the step

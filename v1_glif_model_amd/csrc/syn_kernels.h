@@ -84,7 +84,7 @@ __device__ inline void push_column(int lane_s, int32_t lo, int32_t hi, uint32_t 
     }
 }
 
-// ---- fused backward of one column (A7 + A8) --------------------------------------
+// ---- fused backward of one column (dz and dW) -------------------------------------
 // dz[b] = sum_k w[k] * G[post_k][sid_k][b]   (returned reduced over the sub-wave)
 // dw_col[k] += sum_{b in bmask, ascending} G[post_k][sid_k][b] * mult_b
 template <int L, int BQ, bool WANT_DZ, class Mult>
@@ -143,7 +143,7 @@ __device__ inline void write_G(float *__restrict__ G, int64_t post, int b, int B
     }
 }
 
-// ---- column backward (A7 + A8): dz of every column, dW of its active events -----
+// ---- column backward: dz of every column, dW of its active events ---------------
 // G rows hold R floats: n_elem used elements (for the cell, W consecutive reverse
 // timesteps x B batch entries, e = w*B + b), zero padding after.  A group of
 // LG = R/4 lanes owns one column and walks its synapses type by type in the

@@ -1,5 +1,5 @@
 // Synapse tables: the one-time host build of the column- and post-grouped
-// orders (A1/A2), their upload, the weight-shadow refresh, and shared helpers.
+// orders (pre_ind_table and the preprocessed copies), their upload, the weight-shadow refresh, and shared helpers.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -159,7 +159,7 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
             return fail(GLIF_ERANGE, "syn_id " + std::to_string(syn_id[i]) + " >= n_types");
     }
 
-    // column-grouped order (A1, bit-exact with models.py:317-341)
+    // column-grouped order (bit-exact with models.py:317-341)
     std::vector<int32_t> col_ptr(n_cols + 1), order(n_syn);
     counting_sort(col, nullptr, n_syn, n_cols, col_ptr.data(), order.data());
     // post-grouped order with each row in ascending (col, id): a stable sort of the

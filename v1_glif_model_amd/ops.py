@@ -123,7 +123,7 @@ class SynapseTable:
             self.handle = None
 
     def pre_ind_device(self):
-        """(order, row_splits) device pointers of the bit-exact A1 result."""
+        """(order, row_splits) device pointers of the bit-exact pre_ind_table."""
         o, r = C.c_void_p(), C.c_void_p()
         check(lib().glif_table_pre_ind(self.handle, C.byref(o), C.byref(r)))
         return o.value, r.value
