@@ -172,6 +172,12 @@ int glif_cell_set_voltage_loss(glif_cell *c, int32_t mode, float cost);
 int glif_cell_voltage_loss(glif_cell *c, int32_t B, int32_t T, float *loss_out, void *ws, size_t ws_bytes,
                            void *stream);
 
+/* The core mask of the voltage regularization (VoltageRegularization's core_mask,
+ * loss_functions.py:1105-1109: the penalty's mean runs over the selected neurons only):
+ * mask device uint8 [n_neurons] (nonzero = selected; the caller keeps it alive while the
+ * loss is enabled) and the number it selects, or NULL for every neuron. */
+int glif_cell_set_voltage_mask(glif_cell *c, const uint8_t *mask, int32_t n_selected);
+
 /* Spike trimming of the rate losses (spike_trimming, loss_functions.py:604-611, applied
  * by SpikeRateDistributionTarget.__call__ :873-881): of a T-tick forward, only ticks
  * [pre_delay, T - post_delay) add to spike_count, and glif_cell_backward broadcasts

@@ -175,8 +175,8 @@ def test_call_steps_equal_rollout():
     assert z.shape == (B, tn[1].n_neurons) and int(st2[6][0].item()) == T + 1
 
 
-@pytest.mark.parametrize("mode", ["range", "threshold"])
-def test_fused_voltage_regularization(mode):
+@pytest.mark.parametrize("mode,core", [("range", False), ("threshold", False), ("range", True)])
+def test_fused_voltage_regularization(mode, core):
     """VoltageRegularization (loss_functions.py:1047-1119) fused into the cell: the loss
     reduced from the kept voltages equals the loss of the output voltages, and the BPTT
     with the fused gradient equals the oracle's BPTT given dL/dv of that loss."""
@@ -187,7 +187,9 @@ def test_fused_voltage_regularization(mode):
     lgn, bkg = _inputs(cfg, T, B, seed=6)
     cell = _cell(tn, "deterministic", **CELL_KW)
     cost = 0.5
-    reg = VoltageRegularization(cell, voltage_cost=cost, penalty_mode=mode)
+    N = tn[1].n_neurons
+    mask = (np.arange(N) % 3 == 0) if core else None
+    reg = VoltageRegularization(cell, voltage_cost=cost, penalty_mode=mode, core_mask=mask)
     z, v, _ = cell.rollout(lgn, bkg)
     vn = v.cpu().numpy().astype(np.float64)
     if mode == "range":
@@ -195,15 +197,17 @@ def test_fused_voltage_regularization(mode):
         pen, dpen = m * m, 2.0 * m * np.sign(vn - 0.5)
     else:
         pen, dpen = (vn - 1.0) ** 2, 2.0 * (vn - 1.0)
+    sel = np.ones(N, bool) if mask is None else mask
+    expect = cost * pen[:, :, sel].mean()
     loss = float(reg())
-    assert abs(loss - cost * pen.mean()) <= 1e-6 * abs(cost * pen.mean()) + 1e-12
+    assert abs(loss - expect) <= 1e-6 * abs(expect) + 1e-12
     assert abs(float(reg(v)) - loss) <= 1e-6 * abs(loss) + 1e-12
     oc = _oracle(tn[1], **ORC_KW)
     oz, ov, oref, _ = oc.forward(lgn, bkg)
     rng = np.random.default_rng(7)
     gz = rng.normal(0, 1, oz.shape).astype(np.float32)
     g = cell.backward(gz=torch.tensor(gz, device="cuda"))
-    gv = (cost * dpen / vn.size).astype(np.float32)
+    gv = (cost * dpen / (vn.shape[0] * vn.shape[1] * sel.sum()) * sel).astype(np.float32)
     og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz, gv_loss=gv)
     reg.disable()
     for k in ("rec", "lgn", "bkg"):

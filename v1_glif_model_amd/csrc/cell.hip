@@ -487,12 +487,13 @@ __device__ inline float vpenalty_grad(int mode, float v) {
 
 // Fixed-order reduction (run to run identical): block partials, then one block.
 __global__ void __launch_bounds__(kBlock)
-    k_vloss_partial(const float *__restrict__ v, int64_t n, int mode, float *__restrict__ part) {
+    k_vloss_partial(const float *__restrict__ v, int64_t n, int mode, const uint8_t *__restrict__ mask, int32_t N,
+                    float *__restrict__ part) {
     __shared__ float red[kBlock];
     float acc = 0.0f;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
-        acc += vpenalty(mode, v[i]);
+        if (!mask || mask[i % N]) acc += vpenalty(mode, v[i]);
     red[threadIdx.x] = acc;
     __syncthreads();
     for (int o = kBlock / 2; o > 0; o >>= 1) {
@@ -524,7 +525,8 @@ struct AdjArgs {
     CellConst k;
     int32_t t0, nw, T, ring, R;
     int32_t vmode;   // fused voltage regularization (0 off, 1 range, 2 threshold)
-    float vscale;    // its cost / (T * B * N)
+    float vscale;    // its cost / (T * B * selected neurons)
+    const uint8_t *vmask;  // [N] the selected neurons (core mask), or nullptr: all
     const float *vsave;
     const uint64_t *refbits;
     const float *gz, *gz_neuron, *gv;
@@ -603,7 +605,7 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
         }
         float gV = gz * psi;
         if (a.gv) gV = gV + gvx;
-        if (a.vmode) gV = gV + vpenalty_grad(a.vmode, vsv) * a.vscale;
+        if (a.vmode && (!a.vmask || a.vmask[n])) gV = gV + vpenalty_grad(a.vmode, vsv) * a.vscale;
         gV = gV + (gVc * decay) * k.om;
         gVc = (k.hard_reset && refr) ? 0.0f : gV;
         float dy[kMaxBasis];
@@ -1150,8 +1152,9 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     aa.ring = ring;
     aa.R = Rg;
     aa.vmode = c->vloss_mode;
+    aa.vmask = c->vloss_mask;
     aa.vscale = c->vloss_mode ? c->vloss_cost / (static_cast<float>(T) * static_cast<float>(B) *
-                                                 static_cast<float>(c->N))
+                                                 static_cast<float>(c->vloss_mask ? c->vloss_n : c->N))
                               : 0.0f;
     aa.vsave = w.vsave;
     aa.refbits = w.refbits;
@@ -1243,6 +1246,16 @@ int glif_cell_set_voltage_loss(glif_cell *cc, int32_t mode, float cost) {
     return GLIF_OK;
 }
 
+int glif_cell_set_voltage_mask(glif_cell *cc, const uint8_t *mask, int32_t n_selected) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c) return fail(GLIF_EINVAL, "NULL cell");
+    if (mask && (n_selected <= 0 || n_selected > c->N))
+        return fail(GLIF_EINVAL, "n_selected must be in [1, n_neurons] with a mask");
+    c->vloss_mask = mask;
+    c->vloss_n = mask ? n_selected : c->N;
+    return GLIF_OK;
+}
+
 int glif_cell_set_trim(glif_cell *cc, int32_t pre_delay, int32_t post_delay) {
     Cell *c = reinterpret_cast<Cell *>(cc);
     if (!c) return fail(GLIF_EINVAL, "NULL cell");
@@ -1263,8 +1276,9 @@ int glif_cell_voltage_loss(glif_cell *cc, int32_t B, int32_t T, float *loss_out,
     CellWs w = carve_cell(ws, c, B, T, nullptr);
     const int64_t n = static_cast<int64_t>(T) * B * c->N;
     hipLaunchKernelGGL(k_vloss_partial, dim3(kVlossBlocks), dim3(kBlock), 0, s, w.vsave, n, c->vloss_mode,
-                       w.vloss_part);
-    const float scale = c->vloss_cost / static_cast<float>(n);
+                       c->vloss_mask, c->N, w.vloss_part);
+    const float scale =
+        c->vloss_cost / static_cast<float>(c->vloss_mask ? static_cast<int64_t>(T) * B * c->vloss_n : n);
     hipLaunchKernelGGL(k_vloss_final, dim3(1), dim3(kBlock), 0, s, w.vloss_part, kVlossBlocks, scale, loss_out);
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;

@@ -90,6 +90,8 @@ struct Cell {
     Table *rec = nullptr, *lgn = nullptr, *bkg = nullptr;
     int32_t vloss_mode = 0;    // fused voltage regularization: 0 off, 1 range, 2 threshold
     float vloss_cost = 0.0f;
+    const uint8_t *vloss_mask = nullptr;  // device [N] core mask of the voltage loss (caller-owned), or null
+    int32_t vloss_n = 0;                  // neurons it selects
     // spike-trimming window of the rate losses (loss_functions.py:604-611): the forward
     // counts spikes of ticks [trim_pre, T - trim_post) and the backward broadcasts
     // gz_neuron over the same ticks

@@ -8,7 +8,7 @@ the (trimmed) ticks, so no [T, B, N] spike gradient has to exist.
 
 ``VoltageRegularization`` (loss_functions.py:1047-1119): the penalty of the cell's output
 voltages, "range" relu(|v - 0.5| - 0.5)^2 or "threshold" (v - 1)^2, cost * mean over
-(B, T, N).  Constructing it enables the fused form on the cell: the loss of the last
+(B, T, N) -- over the core-mask neurons only when a ``core_mask`` is given.  Constructing it enables the fused form on the cell: the loss of the last
 rollout is reduced from the voltages the cell keeps for BPTT, and ``V1Column.backward``
 adds the gradient inside the adjoint, so no [T, B, N] voltage tensor has to exist.
 """
@@ -38,15 +38,24 @@ class VoltageRegularization:
     def __init__(self, cell, voltage_cost=1e-5, dtype=torch.float32, core_mask=None, penalty_mode="range"):
         if penalty_mode not in _MODES:
             raise ValueError("penalty_mode must be 'range' or 'threshold'")
-        if core_mask is not None:
-            raise NotImplementedError("core_mask is not supported by the fused form")
         self._cell = cell
         self._voltage_cost = float(voltage_cost)
         self._penalty_mode = penalty_mode
+        self._core_mask = None
+        if core_mask is not None:
+            m = torch.as_tensor(core_mask, device=cell.device).to(torch.bool).reshape(-1)
+            if m.numel() != cell._n_neurons or not bool(m.any()):
+                raise ValueError("core_mask must select at least one of the cell's neurons")
+            self._core_mask = m
+            self._mask_u8 = m.to(torch.uint8).contiguous()   # kept alive while enabled
+            check(lib().glif_cell_set_voltage_mask(cell.handle, ptr(self._mask_u8), int(m.sum().item())))
+        else:
+            check(lib().glif_cell_set_voltage_mask(cell.handle, None, 0))
         check(lib().glif_cell_set_voltage_loss(cell.handle, _MODES[penalty_mode], self._voltage_cost))
 
     def disable(self):
         check(lib().glif_cell_set_voltage_loss(self._cell.handle, 0, 0.0))
+        check(lib().glif_cell_set_voltage_mask(self._cell.handle, None, 0))
 
     @staticmethod
     def penalty(v, mode="range"):
@@ -58,6 +67,8 @@ class VoltageRegularization:
     def __call__(self, voltages=None):
         """Loss of ``voltages`` [T, B, N] if given, else (fused) of the cell's last rollout."""
         if voltages is not None:
+            if self._core_mask is not None:
+                voltages = voltages[:, :, self._core_mask]   # tf.boolean_mask(..., axis=2)
             return self.penalty(voltages, self._penalty_mode).mean() * self._voltage_cost
         cell = self._cell
         if getattr(cell, "_last", None) is None:
@@ -155,7 +166,13 @@ class SpikeRateDistributionTarget:
                  post_delay=None, data_dir=None, core_mask=None, rates_dampening=1.0, seed=42,
                  dtype=torch.float32, neuropixels_df=None, populations: Optional[Dict] = None,
                  type_rates: Optional[Dict] = None, cell=None, kappa=0.002, shuffle_seed=0,
-                 device="cuda"):
+                 device="cuda", **kwargs):
+        # deprecated flags of the reference map to a stimulus type (loss_functions.py:796-801)
+        if kwargs.get("spontaneous_fr"):
+            stimulus_type = "spontaneous"
+        elif kwargs.get("natural_images"):
+            stimulus_type = "natural_stimuli"
+        _rate_feature(stimulus_type)  # validates it
         if dtype != torch.float32:
             raise NotImplementedError("the rate loss computes in float32")
         self._rate_cost = float(rate_cost)
