@@ -202,9 +202,7 @@ def test_population_ids_and_cell_type_names(tmp_path):
     np.testing.assert_allclose(L.load_neuropixels_type_rates(str(g), "gray")["L4 PV"], [0.003, 0.0])
     with pytest.raises(ValueError, match="Unknown stimulus_type"):
         L.load_neuropixels_type_rates(str(g), "movies")
-    # the reference's deprecated flags pick the stimulus type (and hence the rate column)
-    pops = {"L6 Exc": np.array([0, 1], np.int32)}
-    t_sp = L.SpikeRateDistributionTarget.__new__(L.SpikeRateDistributionTarget)
+    # stimulus types name the rate column (loss_functions.py:796-810)
     with pytest.raises(ValueError, match="Unknown stimulus_type"):
         L._rate_feature("movies")
     assert L._rate_feature("gray") == "firing_rate_sp" and L._rate_feature("natural_images") == "firing_rate_ns"
