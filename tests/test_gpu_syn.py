@@ -54,7 +54,7 @@ def test_where_matches_argwhere(rows, cols, p):
 
 
 @pytest.mark.parametrize("seed", [0, 1])
-@pytest.mark.parametrize("B", [1, 3, 8])
+@pytest.mark.parametrize("B", [1, 3, 8, 20])
 def test_syn_fwd_deterministic_is_bit_exact(seed, B):
     tb, t, _ = _setup(seed=seed)
     rng = np.random.default_rng(100 + seed)
@@ -62,6 +62,21 @@ def test_syn_fwd_deterministic_is_bit_exact(seed, B):
     got = t.forward(torch.tensor(z, device="cuda"), mode="deterministic").cpu().numpy()
     ref = orc.syn_fwd(tb.rec, z, tb.basis)
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_syn_fwd_deterministic_input_table_bit_exact():
+    """The op on an input population's table (one delay slot, n_pre != n_post)."""
+    from v1_glif_model_amd.ops import SynapseTable
+    cfg = tiny_config(n_lgn=333, lgn_fanin=12)
+    net, tb = network(cfg, seed=5, dense_basis=True)
+    t = SynapseTable(tb.lgn.indices, tb.lgn.syn_id, (tb.n_neurons, tb.lgn.n_cols), tb.basis)
+    t.set_weights(torch.tensor(tb.lgn.weight, device="cuda"))
+    rng = np.random.default_rng(12)
+    for B in (2, 9):
+        z = _spikes(rng, B, tb.lgn.n_cols, 0.1)
+        got = t.forward(torch.tensor(z, device="cuda"), mode="deterministic").cpu().numpy()
+        ref = orc.syn_fwd(tb.lgn, z, tb.basis)
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("B", [1, 5, 17])
