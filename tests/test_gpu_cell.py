@@ -110,6 +110,33 @@ def test_backward_matches_oracle(pseudo_gauss, hard_reset):
         assert err <= 1e-5 * scale + 1e-6
 
 
+@pytest.mark.parametrize("B,n,T", [(3, 300, 40), (4, 301, 40), (5, 299, 40), (9, 302, 30), (16, 300, 20)])
+def test_backward_grouped_walk_matches_oracle(B, n, T):
+    """16-float G rows (B = 3-5 with three-tick windows, B = 9-16 with one-tick windows)
+    take the grouped row-sliced recurrent backward: four columns per lane group (n * D
+    not a multiple of four leaves a partial last group), a last window of two ticks
+    (T = 40: 38 = 12 * 3 + 2); dz and dW of active columns within the bar."""
+    cfg = tiny_config(n=n, rs=2.0, ins=3.0)
+    tn = network(cfg, seed=n + B, dense_basis=True)
+    lgn, bkg = _inputs(cfg, T, B, seed=B)
+    cell = _cell(tn, "deterministic", **CELL_KW)
+    z, v, _ = cell.rollout(lgn, bkg)
+    oc = _oracle(tn[1], **ORC_KW)
+    oz, ov, oref, _ = oc.forward(lgn, bkg)
+    assert oz.sum() > 0
+    np.testing.assert_array_equal(z.cpu().numpy().astype(np.uint8), oz)
+    rng = np.random.default_rng(B * 100 + T)
+    gz = rng.normal(0, 1, oz.shape).astype(np.float32)
+    gv = rng.normal(0, 0.1, oz.shape).astype(np.float32)
+    g = cell.backward(gz=torch.tensor(gz, device="cuda"), gv=torch.tensor(gv, device="cuda"))
+    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz, gv_loss=gv)
+    for k in ("rec", "lgn", "bkg"):
+        a, e = g[k].cpu().numpy(), og[k]
+        scale = np.max(np.abs(e))
+        assert scale > 0, k
+        assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
+
+
 def test_backward_rate_loss_per_neuron_grad():
     """gz broadcast per neuron (the rate-loss form) equals the dense form."""
     cfg = tiny_config(rs=2.0, ins=1.0)
@@ -235,12 +262,13 @@ def test_deterministic_large_bitmaps_bit_exact(n):
     np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), ov.view(np.uint32))
 
 
+@pytest.mark.parametrize("B", [2, 5])
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 7])
-def test_short_sequences_forward_and_backward(T):
-    """Sequences shorter than / around one backward window (no window for T < 3)."""
+def test_short_sequences_forward_and_backward(T, B):
+    """Sequences shorter than / around one backward window (no window for T < 3); B = 5
+    takes the grouped row-sliced recurrent backward."""
     cfg = tiny_config(rs=2.0, ins=3.0, delays=1)
     tn = network(cfg, seed=6, dense_basis=True)
-    B = 2
     lgn, bkg = _inputs(cfg, T, B, seed=7)
     cell = _cell(tn, "deterministic", **CELL_KW)
     z, v, _ = cell.rollout(lgn, bkg)

@@ -12,8 +12,10 @@
 //                 background and does the same update.
 // Backward, in windows of Wwin reverse ticks t0, t0-1, .. (lagged adjoint, k_adj):
 //   k_adj         per tick t: gz_t -> gV_t -> gP_{t-1} -> gR_{t-2} -> G_{t-2}
-//   k_bwd_rec     dz of the window's steps t0-2, t0-3, .. over every recurrent
-//                 column (+ dW of active columns), one table pass per window
+//   k_bwd_rec_gs  dz of the window's steps t0-2, t0-3, .. over every recurrent
+//                 column, one pass over the grouped row-sliced table per window (16-float
+//                 G rows), then k_bwd_rec_dw: dW of the window's active columns;
+//                 other row lengths: k_bwd_rec, dz and dW in one type-phased pass
 //   k_bwd_in      dW of the LGN / background events of the window's steps
 // A window is legal because dz_s depends only on dz_{>= s+3}: a spike reaches the
 // rise current one step later, the PSC the next, the voltage the one after.
@@ -59,7 +61,7 @@ struct CellWs {
     float *gV;          // [B][N]
     float *gP, *gR;     // [nb][B][N]
     float *vloss_part;  // [kVlossBlocks] partial sums of the voltage penalty
-    float *dw_rec;      // type-phased order
+    float *dw_rec;      // column-grouped order with the grouped walk, else type-phased
     float *dw_lgn, *dw_bkg;  // column-grouped order
 };
 
@@ -723,6 +725,13 @@ struct ActWin {
         const int w = e / B, b = e - w * B;
         return zbit(zbits, ci.slot0 - w, b, B, W, ci.pre);
     }
+    // the spike word of element e and its bit (on() in two steps, so that a group of
+    // lookups can be issued before any of them is tested)
+    __device__ uint64_t word(const Col &ci, int e) const {
+        const int w = e / B, b = e - w * B;
+        return zbits[(static_cast<int64_t>(ci.slot0 - w) * B + b) * W + (ci.pre >> 6)];
+    }
+    __device__ bool bit(const Col &ci, uint64_t wd) const { return ((wd >> (ci.pre & 63)) & 1ull) != 0ull; }
     __device__ float mult(int64_t, int) const { return 1.0f; }
     __device__ float *out(const Col &ci, int e) const {
         const int w = e / B, b = e - w * B;
@@ -733,6 +742,66 @@ struct ActWin {
 template <int LG>
 __global__ void __launch_bounds__(kBlock) k_bwd_rec(ColArgs a, ActWin act) {
     bwd_cols<LG, 2>(a, act);
+}
+
+__global__ void __launch_bounds__(kBlock) k_bwd_rec_gs(GsArgs a, ActWin act) { bwd_groups(a, act); }
+
+// dW of one window's active recurrent columns next to the grouped walk (which computes
+// dz only): a wave per 64 consecutive columns; lane l finds the activity of column c0 + l
+// over the window's elements (the spikes z_{s0-w-d}[b][pre] of ActWin), then the wave
+// walks the column-grouped synapses of each active column, a lane per synapse, adding
+// G[sid][post][e] for the set elements e in ascending order (reverse time, then batch).
+struct RecDwArgs {
+    int64_t n_cols;
+    int32_t n_elem, n_post, R;
+    const int32_t *col_ptr;
+    const uint32_t *ps;
+    const float *G;
+    float *dw;  // column-grouped order, accumulated
+};
+
+__global__ void __launch_bounds__(kBlock) k_bwd_rec_dw(RecDwArgs a, ActWin act) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t c0 =
+        static_cast<int64_t>(blockIdx.x) * blockDim.x + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave;
+    if (c0 >= a.n_cols) return;  // the whole wave leaves together
+    const int64_t c = c0 + lane;
+    uint32_t m = 0;
+    int32_t lo = 0, hi = 0;
+    {
+        // the element lookups are issued at clamped, in-range positions before any is tested
+        const ActWin::Col ci = act.col(min(c, a.n_cols - 1));
+        uint64_t wd[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) wd[e] = act.word(ci, min(e, a.n_elem - 1));
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            if (e < a.n_elem && act.bit(ci, wd[e])) m |= 1u << e;
+        if (c >= a.n_cols) m = 0;
+        if (m) {
+            lo = a.col_ptr[c];
+            hi = a.col_ptr[c + 1];
+        }
+    }
+    uint64_t live = __ballot(m != 0u);
+    while (live) {
+        const int l = __ffsll(static_cast<unsigned long long>(live)) - 1;
+        live &= live - 1;
+        const uint32_t mm = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), l));
+        const int32_t clo = __builtin_amdgcn_readlane(lo, l), chi = __builtin_amdgcn_readlane(hi, l);
+        for (int32_t k = clo + lane; k < chi; k += kWave) {
+            const uint32_t p = a.ps[k];
+            const float *g = a.G + (static_cast<int64_t>(p >> 24) * a.n_post + (p & kLow24)) * a.R;
+            float d = a.dw[k];
+            uint32_t mb = mm;
+            while (mb) {
+                const int e = __ffs(mb) - 1;
+                mb &= mb - 1;
+                d += g[e];
+            }
+            a.dw[k] = d;
+        }
+    }
 }
 
 struct BwdInArgs {
@@ -1138,6 +1207,8 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     // padding elements of each G row stay zero
     if ((rc = launch_fill_u32(w.G, 0u, static_cast<size_t>(c->N) * c->n_types * g_row(win_width(B), B), s)))
         return rc;
+    // the grouped row-sliced walk serves 16-float G rows
+    const bool gs = tr->n_gs > 0 && g_row(win_width(B), B) == 16;
     if (dw_rec && (rc = launch_fill_u32(w.dw_rec, 0u, tr->n_syn, s))) return rc;
     if (dw_lgn && (rc = launch_fill_u32(w.dw_lgn, 0u, tl->n_syn, s))) return rc;
     if (dw_bkg && (rc = launch_fill_u32(w.dw_bkg, 0u, tb->n_syn, s))) return rc;
@@ -1173,6 +1244,8 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     aa.basis = tr->basis;
 
     ColArgs ca{tr->n_cols, c->N, c->n_types, 0, tr->ph_ptr, tr->ph_pw, w.G, 1, dw_rec ? w.dw_rec : nullptr};
+    GsArgs ga{tr->n_cols, tr->n_groups, 0, tr->gs_seg, tr->gs_pw, w.G};
+    RecDwArgs da{tr->n_cols, 0, c->N, Rg, tr->col_ptr, tr->ps, w.G, w.dw_rec};
     ActWin act{w.zbits, w.dZ, tr->n_cols, 0, B, c->D, c->W, c->N, ring};
 
     BwdInArgs la{}, ka{};
@@ -1211,11 +1284,17 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
             ProfScope p(kProfAdj, s);
             launch_adj(aa, c->nb, lds, s);
         }
-        ca.n_elem = nw * B;
+        ca.n_elem = ga.n_elem = da.n_elem = nw * B;
         act.s0 = s0;
         {
             ProfScope p(kProfBwdRec, s);
-            launch_bwd_rec(ca, Rg, act, s);
+            if (gs) {
+                hipLaunchKernelGGL(k_bwd_rec_gs, dim3(ceil_div(ga.n_groups * 4, kBlock)), dim3(kBlock), 0, s, ga, act);
+                if (dw_rec)
+                    hipLaunchKernelGGL(k_bwd_rec_dw, dim3(ceil_div(tr->n_cols, kBlock)), dim3(kBlock), 0, s, da, act);
+            } else {
+                launch_bwd_rec(ca, Rg, act, s);
+            }
         }
         if (dw_lgn) {
             la.j = j;
@@ -1231,7 +1310,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         }
     }
     GLIF_HIP(hipGetLastError());
-    if (dw_rec && (rc = launch_gather_f32(dw_rec, w.dw_rec, tr->ph_inv, tr->n_syn, s))) return rc;
+    if (dw_rec && (rc = launch_gather_f32(dw_rec, w.dw_rec, gs ? tr->order_inv : tr->ph_inv, tr->n_syn, s))) return rc;
     if (dw_lgn && (rc = launch_gather_f32(dw_lgn, w.dw_lgn, tl->order_inv, tl->n_syn, s))) return rc;
     if (dw_bkg && (rc = launch_gather_f32(dw_bkg, w.dw_bkg, tb->order_inv, tb->n_syn, s))) return rc;
     return GLIF_OK;

@@ -18,6 +18,13 @@ constexpr int kMaxBatch = 32;
 constexpr uint32_t kLow24 = 0x00FFFFFFu;
 constexpr int kChunkEntries = 512;
 constexpr int kChunkRows = 63;
+// grouped row-sliced backward order (recurrent tables): kGsCols columns per lane group,
+// kGsSlices equal ranges of G rows, segments padded to kGsPad entries
+constexpr int kGsCols = 4;
+constexpr int kGsSlices = 4;
+constexpr int kGsPad = 8;
+constexpr int kGsRowBits = 29;
+constexpr uint32_t kGsRowMask = (1u << kGsRowBits) - 1u;
 
 // ---- error plumbing -------------------------------------------------------
 void set_error(const std::string &msg);
@@ -75,6 +82,17 @@ struct Table {
     uint2 *ph_pw = nullptr;       // [n_syn]       {post, weight bits}
     int32_t *order_inv = nullptr; // [n_syn]       position of synapse s in the column-grouped order
     int32_t *ph_inv = nullptr;    // [n_syn]       position of synapse s in the type-phased order
+    // grouped row-sliced order (recurrent backward over 16-float G rows): lane group g owns
+    // columns kGsCols*g ..; its entries in G-row slice p (rows syn_id * n_post + post, slice p
+    // = rows [n_rows * p / kGsSlices, n_rows * (p + 1) / kGsSlices)) are positions
+    // [gs_seg[g * (kGsSlices + 1) + p], gs_seg[g * (kGsSlices + 1) + p + 1]), ordered by
+    // (row, column, synapse id) and padded to a multiple of kGsPad with entries
+    // {the segment's last row | 7 << kGsRowBits, +0.0f}.  n_gs = 0: not built.
+    int64_t n_gs = 0;             // positions, padding included
+    int64_t n_groups = 0;
+    int32_t *gs_seg = nullptr;    // [n_groups * (kGsSlices + 1)]
+    uint2 *gs_pw = nullptr;       // [n_gs]        {row | column-in-group << kGsRowBits, weight bits}
+    int32_t *gs_src = nullptr;    // [n_gs]        synapse id, -1 for padding
     float *basis_host = nullptr;  // host copy [n_types][n_basis]
 };
 

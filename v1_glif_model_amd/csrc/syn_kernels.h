@@ -283,6 +283,94 @@ __device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
     }
 }
 
+// ---- grouped row-sliced backward (16-float G rows) ------------------------------
+// dz of every column over the grouped row-sliced order: lane group g (4 lanes, lane q
+// holding floats 4q..4q+3 of a row) owns columns kGsCols*g ..; it walks its entries of
+// one G-row slice at a time, 8 per step (one 64-byte load, lane q holding entries 2q and
+// 2q+1, shared in the group by DPP), and adds w * G[row] into the column's accumulator.
+// Every wave finishes a slice before starting the next, so the waves in flight gather
+// from one quarter of G at a time, and a group owns its columns, so dz needs no atomics.
+// Each column sums its entries in G-row order (syn_id, then post), the order of
+// bwd_cols.  The dW of active columns is a separate pass (k_bwd_rec_dw in cell.hip):
+// holding it here costs a third more registers and a second walk per group.
+//
+// Measured on MI355X with a config-2-sized table (16.5M synapses, 330k columns, G 21 MB):
+// 146 us per pass against 195 us for the type-phased walk.  The type-phased walk makes
+// 27.7M L2 requests (its 8-byte entry loads are re-requested), a row-sorted walk without
+// slices 18.5M but misses L2 on 42% of them; the slices bring the misses down while the
+// 8-entry loads keep the requests near one per synapse.
+struct GsArgs {
+    int64_t n_cols, n_groups;
+    int32_t n_elem;
+    const int32_t *seg;   // [n_groups * (kGsSlices + 1)]
+    const uint2 *pw;      // {row | column-in-group << kGsRowBits, weight bits}
+    const float *G;       // [rows][16], < 4 GiB
+};
+
+// value of lane `src` of this lane's quad (DPP quad_perm broadcast)
+__device__ inline uint32_t quad_bcast(uint32_t v, int src) {
+    switch (src) {
+        case 0: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x00, 0xF, 0xF, false));
+        case 1: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x55, 0xF, 0xF, false));
+        case 2: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xAA, 0xF, 0xF, false));
+        default: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xFF, 0xF, 0xF, false));
+    }
+}
+
+template <class Act>
+__device__ inline void bwd_groups(const GsArgs &a, const Act &act) {
+    const int q = threadIdx.x % 4;
+    const int64_t g = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / 4;
+    if (g >= a.n_groups) return;  // the whole lane group leaves together
+    const char *Gb = reinterpret_cast<const char *>(a.G) + static_cast<uint32_t>(q) * 16u;
+    float acc[kGsCols][4];
+#pragma unroll
+    for (int j = 0; j < kGsCols; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[j][i] = 0.0f;
+    const int32_t *sg = a.seg + g * (kGsSlices + 1);
+    int32_t lo = sg[0];
+    for (int p = 0; p < kGsSlices; ++p) {
+        const int32_t hi = sg[p + 1];
+        for (int32_t k0 = lo; k0 < hi; k0 += 8) {
+            const uint4 ch = *reinterpret_cast<const uint4 *>(a.pw + k0 + 2 * q);
+            float4 gv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t r = quad_bcast((u & 1) ? ch.z : ch.x, u >> 1);
+                gv[u] = *reinterpret_cast<const float4 *>(Gb + (r & kGsRowMask) * 64u);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t col = quad_bcast((u & 1) ? ch.z : ch.x, u >> 1) >> kGsRowBits;
+                const float wu = __uint_as_float(quad_bcast((u & 1) ? ch.w : ch.y, u >> 1));
+                const float t0 = wu * gv[u].x, t1 = wu * gv[u].y, t2 = wu * gv[u].z, t3 = wu * gv[u].w;
+#pragma unroll
+                for (int j = 0; j < kGsCols; ++j) {
+                    const bool m = col == static_cast<uint32_t>(j);
+                    acc[j][0] += m ? t0 : 0.0f;
+                    acc[j][1] += m ? t1 : 0.0f;
+                    acc[j][2] += m ? t2 : 0.0f;
+                    acc[j][3] += m ? t3 : 0.0f;
+                }
+            }
+        }
+        lo = hi;
+    }
+#pragma unroll
+    for (int j = 0; j < kGsCols; ++j) {
+        const int64_t c = g * kGsCols + j;
+        if (c < a.n_cols) {
+            const typename Act::Col ci = act.col(c);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = 4 * q + i;
+                if (e < a.n_elem) *act.out(ci, e) = acc[j][i];
+            }
+        }
+    }
+}
+
 // Row length (floats) of G for B batch entries over W timesteps: a power of two >= 4.
 __host__ __device__ inline int g_row(int W, int B) {
     int r = 4;

@@ -44,6 +44,7 @@ __global__ void k_gather_pair_w(uint2 *__restrict__ dst, const float *__restrict
     for (; i < n; i += stride) dst[i].y = __float_as_uint(src[idx[i]]);
 }
 
+// dst[i].y = weight of synapse idx[i], +0.0f where idx[i] < 0 (padding)
 __global__ void k_gather_ell_w(uint2 *__restrict__ dst, const float *__restrict__ src,
                                const int32_t *__restrict__ idx, int64_t n) {
     int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -97,7 +98,7 @@ static void free_table(Table *t) {
     if (!t) return;
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
                     t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
-                    t->chunk_desc, t->pidx, t->order_inv, t->ph_inv};
+                    t->chunk_desc, t->pidx, t->order_inv, t->ph_inv, t->gs_seg, t->gs_pw, t->gs_src};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete[] t->basis_host;
@@ -188,6 +189,56 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         order_inv[order[k]] = static_cast<int32_t>(k);
         ph_inv[ph_order[k]] = static_cast<int32_t>(k);
     }
+    // grouped row-sliced order (recurrent tables): a stable counting sort by (G row,
+    // column in group), then by (group, row slice); each (group, slice) segment is padded to
+    // a multiple of kGsPad with copies of its last row marked as column 7 (weight +0.0f)
+    const int64_t n_rows = static_cast<int64_t>(n_types) * n_post;
+    std::vector<int32_t> gs_seg, gs_src;
+    std::vector<uint2> gs_pw;
+    int64_t n_groups = 0, n_gs = 0;
+    if (n_delay_slots > 1 && n_syn > 0 && n_rows <= static_cast<int64_t>(kGsRowMask) + 1) {
+        n_groups = (n_cols + kGsCols - 1) / kGsCols;
+        std::vector<int64_t> key(n_syn);
+        for (int64_t i = 0; i < n_syn; ++i)
+            key[i] = (static_cast<int64_t>(syn_id[i]) * n_post + post[i]) * kGsCols + col[i] % kGsCols;
+        std::vector<int32_t> ptr1(n_rows * kGsCols + 1), ord1(n_syn);
+        counting_sort(key.data(), nullptr, n_syn, n_rows * kGsCols, ptr1.data(), ord1.data());
+        for (int64_t i = 0; i < n_syn; ++i) {
+            const int64_t row = static_cast<int64_t>(syn_id[i]) * n_post + post[i];
+            key[i] = (col[i] / kGsCols) * kGsSlices + row * kGsSlices / n_rows;
+        }
+        const int64_t n_seg = n_groups * kGsSlices;
+        std::vector<int32_t> ptr2(n_seg + 1), ord2(n_syn);
+        counting_sort(key.data(), ord1.data(), n_syn, n_seg, ptr2.data(), ord2.data());
+        for (int64_t b = 0; b < n_seg; ++b) n_gs += (ptr2[b + 1] - ptr2[b] + kGsPad - 1) / kGsPad * kGsPad;
+        if (n_gs < INT32_MAX) {
+            gs_seg.resize(n_groups * (kGsSlices + 1));
+            gs_pw.resize(n_gs);
+            gs_src.resize(n_gs);
+            int64_t pos = 0;
+            for (int64_t g = 0; g < n_groups; ++g) {
+                for (int p = 0; p < kGsSlices; ++p) {
+                    const int64_t b = g * kGsSlices + p;
+                    gs_seg[g * (kGsSlices + 1) + p] = static_cast<int32_t>(pos);
+                    uint32_t last = 0;
+                    for (int32_t r = ptr2[b]; r < ptr2[b + 1]; ++r, ++pos) {
+                        const int32_t sidx = ord2[r];
+                        last = static_cast<uint32_t>(static_cast<int64_t>(syn_id[sidx]) * n_post + post[sidx]);
+                        gs_pw[pos] = make_uint2(last | static_cast<uint32_t>(col[sidx] % kGsCols) << kGsRowBits, 0u);
+                        gs_src[pos] = sidx;
+                    }
+                    for (; pos % kGsPad; ++pos) {
+                        gs_pw[pos] = make_uint2(last | 7u << kGsRowBits, 0u);
+                        gs_src[pos] = -1;
+                    }
+                }
+                gs_seg[g * (kGsSlices + 1) + kGsSlices] = static_cast<int32_t>(pos);
+            }
+        } else {
+            n_groups = n_gs = 0;
+        }
+    }
+
     std::vector<uint32_t> ps(n_syn), pd(n_syn);
     // bit index of the entry's presynaptic spike in a stack of per-slot activity planes
     // of round64(n_pre) bits, slot d at plane n_slots - d (the newest step last)
@@ -241,6 +292,8 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
     t->n_basis = n_basis;
     t->max_col_len = max_len;
     t->ell_len = ell_len;
+    t->n_gs = n_gs;
+    t->n_groups = n_groups;
     // row-aligned chunks, greedy in row order
     std::vector<int4> chunk_desc;
     for (int32_t n = 0; n < n_post;) {
@@ -269,7 +322,10 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         (rc = upload(&t->ph_inv, ph_inv.data(), ph_inv.size())) ||
         (rc = upload(&t->ph_pw, ph_pw.data(), ph_pw.size())) ||
         (ell_len && (rc = upload(&t->ell_pw, ell_pw.data(), ell_pw.size()))) ||
-        (ell_len && (rc = upload(&t->ell_src, ell_src.data(), ell_src.size())))) {
+        (ell_len && (rc = upload(&t->ell_src, ell_src.data(), ell_src.size()))) ||
+        (n_gs && (rc = upload(&t->gs_seg, gs_seg.data(), gs_seg.size()))) ||
+        (n_gs && (rc = upload(&t->gs_pw, gs_pw.data(), gs_pw.size()))) ||
+        (n_gs && (rc = upload(&t->gs_src, gs_src.data(), gs_src.size())))) {
         free_table(t);
         return rc;
     }
@@ -308,6 +364,11 @@ int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
     if (t->n_syn) {
         hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(t->n_syn)), dim3(kBlock), 0, s, t->ph_pw, w,
                            t->ph_order, t->n_syn);
+        GLIF_HIP(hipGetLastError());
+    }
+    if (t->n_gs) {
+        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(t->n_gs)), dim3(kBlock), 0, s, t->gs_pw, w, t->gs_src,
+                           t->n_gs);
         GLIF_HIP(hipGetLastError());
     }
     if (t->ell_len) {
