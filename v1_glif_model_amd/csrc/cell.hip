@@ -744,13 +744,17 @@ __global__ void __launch_bounds__(kBlock) k_bwd_rec(ColArgs a, ActWin act) {
     bwd_cols<LG, 2>(a, act);
 }
 
-__global__ void __launch_bounds__(kBlock) k_bwd_rec_gs(GsArgs a, ActWin act) { bwd_groups(a, act); }
+__global__ void __launch_bounds__(kBlock) k_bwd_rec_gs(GsArgs a, ActWin act) {
+    __shared__ float stage[kBlock / kWave * kGsStage];
+    bwd_groups(a, act, stage);
+}
 
 // dW of one window's active recurrent columns next to the grouped walk (which computes
 // dz only): a wave per 64 consecutive columns; lane l finds the activity of column c0 + l
-// over the window's elements (the spikes z_{s0-w-d}[b][pre] of ActWin), then the wave
-// walks the column-grouped synapses of each active column, a lane per synapse, adding
-// G[sid][post][e] for the set elements e in ascending order (reverse time, then batch).
+// over the window's elements (the spikes z_{s0-w-d}[b][pre] of ActWin), then 16-lane
+// sub-groups walk the column-grouped synapses of the active columns, a lane per synapse,
+// adding G[sid][post][e] for the set elements e in ascending order (reverse time, then
+// batch).
 struct RecDwArgs {
     int64_t n_cols;
     int32_t n_elem, n_post, R;
@@ -783,23 +787,48 @@ __global__ void __launch_bounds__(kBlock) k_bwd_rec_dw(RecDwArgs a, ActWin act) 
             hi = a.col_ptr[c + 1];
         }
     }
+    // four 16-lane sub-groups take the next four active columns, four synapses per lane
+    // in flight
+    const int sub = lane / 16, sl = lane % 16;
     uint64_t live = __ballot(m != 0u);
     while (live) {
-        const int l = __ffsll(static_cast<unsigned long long>(live)) - 1;
-        live &= live - 1;
-        const uint32_t mm = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), l));
-        const int32_t clo = __builtin_amdgcn_readlane(lo, l), chi = __builtin_amdgcn_readlane(hi, l);
-        for (int32_t k = clo + lane; k < chi; k += kWave) {
-            const uint32_t p = a.ps[k];
-            const float *g = a.G + (static_cast<int64_t>(p >> 24) * a.n_post + (p & kLow24)) * a.R;
-            float d = a.dw[k];
+        uint64_t lv = live;
+        int src = -1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = lv ? __ffsll(static_cast<unsigned long long>(lv)) - 1 : -1;
+            if (i == sub) src = f;
+            lv &= lv - 1;
+        }
+        live = lv;
+        // every lane takes part in the shuffles (a lane left out would read back wrong to
+        // the lanes that use it as their source); idle sub-groups are masked afterwards
+        const int sl_src = src >= 0 ? src : 0;
+        const uint32_t msrc = static_cast<uint32_t>(__shfl(static_cast<int>(m), sl_src, kWave));
+        const int32_t clo = __shfl(lo, sl_src, kWave);
+        const int32_t hsrc = __shfl(hi, sl_src, kWave);
+        const uint32_t mm = src >= 0 ? msrc : 0u;
+        const int32_t chi = src >= 0 ? hsrc : clo;
+        for (int32_t k0 = clo; k0 < chi; k0 += 64) {
+            float d[4];
+            const float *gp[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int32_t k = min(k0 + 16 * u + sl, chi - 1);
+                const uint32_t p = a.ps[k];
+                gp[u] = a.G + (static_cast<int64_t>(p >> 24) * a.n_post + (p & kLow24)) * a.R;
+                d[u] = a.dw[k];
+            }
             uint32_t mb = mm;
             while (mb) {
                 const int e = __ffs(mb) - 1;
                 mb &= mb - 1;
-                d += g[e];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) d[u] += gp[u][e];
             }
-            a.dw[k] = d;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (k0 + 16 * u + sl < chi) a.dw[k0 + 16 * u + sl] = d[u];
         }
     }
 }

@@ -317,8 +317,12 @@ __device__ inline uint32_t quad_bcast(uint32_t v, int src) {
     }
 }
 
+// LDS floats per wave for the dz staging of bwd_groups: [16 elements][64 columns + 1]
+constexpr int kGsStage = 16 * (kWave + 1);
+
+// stage: kGsStage floats of LDS per wave of the block
 template <class Act>
-__device__ inline void bwd_groups(const GsArgs &a, const Act &act) {
+__device__ inline void bwd_groups(const GsArgs &a, const Act &act, float *stage) {
     const int q = threadIdx.x % 4;
     const int64_t g = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / 4;
     if (g >= a.n_groups) return;  // the whole lane group leaves together
@@ -357,17 +361,23 @@ __device__ inline void bwd_groups(const GsArgs &a, const Act &act) {
         }
         lo = hi;
     }
+    // dz through LDS: the wave's 16 groups own 64 consecutive columns, so each element's
+    // 64 values leave as one coalesced store (lane l writes column 64 * wave + l, which
+    // belongs to its own group)
+    const int lane = threadIdx.x % kWave;
+    float *st = stage + (threadIdx.x / kWave) * kGsStage;
+    const int gl = lane / 4;
 #pragma unroll
-    for (int j = 0; j < kGsCols; ++j) {
-        const int64_t c = g * kGsCols + j;
-        if (c < a.n_cols) {
-            const typename Act::Col ci = act.col(c);
+    for (int j = 0; j < kGsCols; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = 4 * q + i;
-                if (e < a.n_elem) *act.out(ci, e) = acc[j][i];
-            }
-        }
+        for (int i = 0; i < 4; ++i) st[(4 * q + i) * (kWave + 1) + 4 * gl + j] = acc[j][i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int64_t c = (g - gl) * kGsCols + lane;
+    if (c < a.n_cols) {
+        const typename Act::Col ci = act.col(c);
+        for (int e = 0; e < a.n_elem; ++e) *act.out(ci, e) = st[e * (kWave + 1) + lane];
     }
 }
 
