@@ -387,10 +387,11 @@ def main():
     tot_ms, launches = prof.get(dominant, (0.0, 0))
     if dominant == "bwd_rec":
         # per launch = one backward window of Wwin timesteps (the last window may be
-        # shorter; launches = ceil((T-2)/Wwin)): the type-phased table (post + weight,
-        # 8 B/synapse) and its (type, column) pointers once, the dz rows of the
-        # window's steps, the G projection read once, spike words, and the dW
-        # read-modify-write of the window's active events
+        # shorter; launches = ceil((T-2)/Wwin)): one 8-byte table entry per synapse
+        # (G row + weight) and per-column pointers once, the dz rows of the window's
+        # steps, the G projection read once, spike words, and the dW read-modify-write
+        # of the window's active events (the algorithm's bytes, whichever table layout
+        # the library walks)
         steps_per_launch = (T - 2) / max(launches / args.steps, 1)
         active = e_rec / max(T, 1) * steps_per_launch
         alg_bytes = (S * 8 + (nt * D * N + 1) * 4 + steps_per_launch * B * D * N * 4 + N * nt * Rg * 4

@@ -12,6 +12,9 @@
 //     synapse id); the type-s synapses of column c are
 //     k in [ph_ptr[s * n_cols + c], ph_ptr[s * n_cols + c + 1]);
 //     ph_pw[k] = {post, weight bits}.
+//   grouped row-sliced table (Table::gs_seg/gs_pw, recurrent tables): lane group g's
+//     columns 4g..4g+3, by G-row slice, then G row (syn_id * n_post + post); entries
+//     {row | column-in-group << 29, weight bits}, each segment padded to 8 entries.
 //   I  [B][n_post][nb]  (the reference's i_rec_flat [B*N, nb]).
 //   G  [n_types][n_post][R]: G[s][post][e] = sum_r dy[b][post][r] * basis[s][r] for
 //     element e (batch b, possibly of several timesteps), the per-synapse-type
