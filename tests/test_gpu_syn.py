@@ -122,6 +122,49 @@ def test_syn_bwd_matches_oracle(B):
         assert np.max(np.abs(got - ex) - 1e-5 * sc) <= 1e-6, what
 
 
+@pytest.mark.parametrize("B", [5, 12])
+def test_syn_bwd_counts_and_partial_requests(B):
+    """Poisson-count inputs (dW scaled by the count, models.py:917-931) through the grouped
+    row-sliced dz walk (8- and 16-float G rows) and the active-column dW pass; dz-only and
+    dW-only calls give the same values as the full call."""
+    tb, t, _ = _setup(seed=7, n=301)
+    rng = np.random.default_rng(B)
+    z = (rng.random((B, tb.rec.n_cols)) < 0.08).astype(np.float32) * rng.integers(1, 4, (B, tb.rec.n_cols))
+    z = z.astype(np.float32)
+    dy = rng.normal(0, 1, (B * tb.n_neurons, tb.n_basis)).astype(np.float32)
+    zt, dyt = torch.tensor(z, device="cuda"), torch.tensor(dy, device="cuda")
+    dz, dw = t.backward(zt, dyt, counts=True)
+    dz, dw = dz.cpu().numpy(), dw.cpu().numpy()
+    rdz, rdw = orc.syn_bwd(tb.rec, z, tb.basis, dy, use_count=True)
+    _, _, dz_abs, dw_abs = dense.syn_bwd_f64(tb.rec, z, tb.basis, dy, use_count=True)
+    assert np.max(np.abs(dz - rdz) - 1e-5 * dz_abs) <= 1e-6
+    assert np.max(np.abs(dw - rdw) - 1e-5 * dw_abs) <= 1e-6
+    assert np.count_nonzero(dw) > 0
+    dz_only, none_w = t.backward(zt, dyt, counts=True, want_dw=False)
+    none_z, dw_only = t.backward(zt, dyt, counts=True, want_dz=False)
+    assert none_w is None and none_z is None
+    np.testing.assert_array_equal(dz_only.cpu().numpy(), dz)
+    np.testing.assert_array_equal(dw_only.cpu().numpy(), dw)
+
+
+@pytest.mark.parametrize("B", [5, 9])
+def test_syn_bwd_input_table(B):
+    """The backward on an input population's table (one delay slot, n_pre != n_post)."""
+    from v1_glif_model_amd.ops import SynapseTable
+    cfg = tiny_config(n_lgn=333, lgn_fanin=12)
+    net, tb = network(cfg, seed=5, dense_basis=True)
+    t = SynapseTable(tb.lgn.indices, tb.lgn.syn_id, (tb.n_neurons, tb.lgn.n_cols), tb.basis)
+    t.set_weights(torch.tensor(tb.lgn.weight, device="cuda"))
+    rng = np.random.default_rng(B + 40)
+    z = _spikes(rng, B, tb.lgn.n_cols, 0.1)
+    dy = rng.normal(0, 1, (B * tb.n_neurons, tb.n_basis)).astype(np.float32)
+    dz, dw = t.backward(torch.tensor(z, device="cuda"), torch.tensor(dy, device="cuda"))
+    rdz, rdw = orc.syn_bwd(tb.lgn, z, tb.basis, dy)
+    _, _, dz_abs, dw_abs = dense.syn_bwd_f64(tb.lgn, z, tb.basis, dy)
+    assert np.max(np.abs(dz.cpu().numpy() - rdz) - 1e-5 * dz_abs) <= 1e-6
+    assert np.max(np.abs(dw.cpu().numpy() - rdw) - 1e-5 * dw_abs) <= 1e-6
+
+
 def test_calculate_synaptic_currents_autograd():
     from v1_glif_model_amd.ops import calculate_synaptic_currents, make_pre_ind_table
     cfg = tiny_config()

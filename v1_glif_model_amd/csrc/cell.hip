@@ -746,7 +746,7 @@ __global__ void __launch_bounds__(kBlock) k_bwd_rec(ColArgs a, ActWin act) {
 
 __global__ void __launch_bounds__(kBlock) k_bwd_rec_gs(GsArgs a, ActWin act) {
     __shared__ float stage[kBlock / kWave * kGsStage];
-    bwd_groups(a, act, stage);
+    bwd_groups<4>(a, act, stage);
 }
 
 // dW of one window's active recurrent columns next to the grouped walk (which computes

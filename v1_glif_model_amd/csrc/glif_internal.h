@@ -18,7 +18,7 @@ constexpr int kMaxBatch = 32;
 constexpr uint32_t kLow24 = 0x00FFFFFFu;
 constexpr int kChunkEntries = 512;
 constexpr int kChunkRows = 63;
-// grouped row-sliced backward order (recurrent tables): kGsCols columns per lane group,
+// grouped row-sliced backward order: kGsCols columns per lane group,
 // kGsSlices equal ranges of G rows, segments padded to kGsPad entries
 constexpr int kGsCols = 4;
 constexpr int kGsSlices = 4;
@@ -82,7 +82,7 @@ struct Table {
     uint2 *ph_pw = nullptr;       // [n_syn]       {post, weight bits}
     int32_t *order_inv = nullptr; // [n_syn]       position of synapse s in the column-grouped order
     int32_t *ph_inv = nullptr;    // [n_syn]       position of synapse s in the type-phased order
-    // grouped row-sliced order (recurrent backward over 16-float G rows): lane group g owns
+    // grouped row-sliced order (backward dz walks over 8- and 16-float G rows): lane group g owns
     // columns kGsCols*g ..; its entries in G-row slice p (rows syn_id * n_post + post, slice p
     // = rows [n_rows * p / kGsSlices, n_rows * (p + 1) / kGsSlices)) are positions
     // [gs_seg[g * (kGsSlices + 1) + p], gs_seg[g * (kGsSlices + 1) + p + 1]), ordered by

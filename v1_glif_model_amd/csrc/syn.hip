@@ -111,6 +111,88 @@ __global__ void __launch_bounds__(kBlock) k_syn_bwd_cols(ColArgs a, ActDense act
     bwd_cols<LG, 2>(a, act);
 }
 
+template <int LG>
+__global__ void __launch_bounds__(kBlock) k_syn_bwd_gs(GsArgs a, ActDense act) {
+    __shared__ float stage[kBlock / kWave * kGsStage];
+    bwd_groups<LG>(a, act, stage);
+}
+
+// dW of the active columns (z[b][c] > 0) next to the grouped dz walk: a wave per 64
+// consecutive columns finds each column's batch mask, then 16-lane sub-groups walk the
+// column-grouped synapses of four active columns at a time and write each synapse's dW
+// once, straight to reference order: the sum over the set batch entries b, ascending, of
+// G[sid][post][b] times the input value (counts) or 1 (spikes).
+struct SynDwArgs {
+    int64_t n_cols;
+    int32_t B, n_post, R, counts;
+    const float *z;  // [B][n_cols]
+    const int32_t *col_ptr;
+    const uint32_t *ps;
+    const int32_t *order;
+    const float *G;
+    float *dw;  // reference order, zero-filled by the caller
+};
+
+__global__ void __launch_bounds__(kBlock) k_syn_bwd_dw(SynDwArgs a) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t c0 =
+        static_cast<int64_t>(blockIdx.x) * blockDim.x + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave;
+    if (c0 >= a.n_cols) return;  // the whole wave leaves together
+    const int64_t c = c0 + lane;
+    const int64_t cl = min(c, a.n_cols - 1);
+    uint32_t m = 0;
+    for (int b = 0; b < a.B; ++b) m |= (a.z[b * a.n_cols + cl] > 0.0f ? 1u : 0u) << b;
+    if (c >= a.n_cols) m = 0;
+    int32_t lo = 0, hi = 0;
+    if (m) {
+        lo = a.col_ptr[c];
+        hi = a.col_ptr[c + 1];
+    }
+    const int sub = lane / 16, sl = lane % 16;
+    uint64_t live = __ballot(m != 0u);
+    while (live) {
+        uint64_t lv = live;
+        int src = -1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = lv ? __ffsll(static_cast<unsigned long long>(lv)) - 1 : -1;
+            if (i == sub) src = f;
+            lv &= lv - 1;
+        }
+        live = lv;
+        // every lane takes part in the shuffles; idle sub-groups are masked afterwards
+        const int sl_src = src >= 0 ? src : 0;
+        const uint32_t msrc = static_cast<uint32_t>(__shfl(static_cast<int>(m), sl_src, kWave));
+        const int32_t clo = __shfl(lo, sl_src, kWave);
+        const int32_t hsrc = __shfl(hi, sl_src, kWave);
+        const uint32_t mm = src >= 0 ? msrc : 0u;
+        const int32_t chi = src >= 0 ? hsrc : clo;
+        const int64_t cc = c0 + sl_src;
+        for (int32_t k0 = clo; k0 < chi; k0 += 64) {
+            float d[4];
+            const float *gp[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int32_t k = min(k0 + 16 * u + sl, chi - 1);
+                const uint32_t p = a.ps[k];
+                gp[u] = a.G + (static_cast<int64_t>(p >> 24) * a.n_post + (p & kLow24)) * a.R;
+                d[u] = 0.0f;
+            }
+            uint32_t mb = mm;
+            while (mb) {
+                const int b = __ffs(mb) - 1;
+                mb &= mb - 1;
+                const float mult = a.counts ? a.z[b * a.n_cols + cc] : 1.0f;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) d[u] += a.counts ? gp[u][b] * mult : gp[u][b];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (k0 + 16 * u + sl < chi) a.dw[a.order[k0 + 16 * u + sl]] = d[u];
+        }
+    }
+}
+
 int sub_wave_for(const Table *t) {  // lanes per column: ~ the mean column length
     double avg = t->n_cols ? static_cast<double>(t->n_syn) / t->n_cols : 0.0;
     return avg <= 24.0 ? 16 : (avg <= 48.0 ? 32 : 64);
@@ -270,6 +352,24 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     GLIF_HIP(hipGetLastError());
     // one pass writes every active synapse's dW once, in reference order; the rest stay 0
     if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
+    if (t->n_gs && (Bp == 8 || Bp == 16)) {
+        // the grouped row-sliced walk for dz, then the active columns' dW
+        ActDense act{z, dz, t->n_cols, counts};
+        if (dz) {
+            GsArgs ga{t->n_cols, t->n_groups, B, t->gs_seg, t->gs_pw, w.G};
+            const int LG = Bp / 4;
+            const dim3 grid(ceil_div(t->n_groups * LG, kBlock));
+            if (LG == 2) hipLaunchKernelGGL(k_syn_bwd_gs<2>, grid, dim3(kBlock), 0, s, ga, act);
+            else hipLaunchKernelGGL(k_syn_bwd_gs<4>, grid, dim3(kBlock), 0, s, ga, act);
+            GLIF_HIP(hipGetLastError());
+        }
+        if (dw) {
+            SynDwArgs da{t->n_cols, B, t->n_post, Bp, counts, z, t->col_ptr, t->ps, t->order, w.G, dw};
+            hipLaunchKernelGGL(k_syn_bwd_dw, dim3(ceil_div(t->n_cols, kBlock)), dim3(kBlock), 0, s, da);
+            GLIF_HIP(hipGetLastError());
+        }
+        return GLIF_OK;
+    }
     ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, t->ph_pw, w.G, dz ? 1 : 0, dw, t->ph_order};
     ActDense act{z, dz, t->n_cols, counts};
     const dim3 grid(ceil_div(t->n_cols * (Bp / 4), kBlock));

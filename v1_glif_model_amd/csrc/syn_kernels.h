@@ -307,7 +307,7 @@ struct GsArgs {
     int32_t n_elem;
     const int32_t *seg;   // [n_groups * (kGsSlices + 1)]
     const uint2 *pw;      // {row | column-in-group << kGsRowBits, weight bits}
-    const float *G;       // [rows][16], < 4 GiB
+    const float *G;       // [rows][4 LG], < 4 GiB
 };
 
 // value of lane `src` of this lane's quad (DPP quad_perm broadcast)
@@ -320,37 +320,58 @@ __device__ inline uint32_t quad_bcast(uint32_t v, int src) {
     }
 }
 
-// LDS floats per wave for the dz staging of bwd_groups: [16 elements][64 columns + 1]
+// value of lane `src` of this lane's group of LG lanes (LG = 2: the lane pairs of a quad,
+// quad_perm [src, src, 2 + src, 2 + src]; LG = 4: the quad)
+template <int LG>
+__device__ inline uint32_t group_bcast(uint32_t v, int src) {
+    static_assert(LG == 2 || LG == 4, "lane groups of 2 or 4");
+    if (LG == 4) return quad_bcast(v, src);
+    return src == 0 ? static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xA0, 0xF, 0xF, false))
+                    : static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xF5, 0xF, 0xF, false));
+}
+
+// LDS floats per wave for the dz staging of bwd_groups: [R][columns per wave + 1], at most
+// 16 x 65 (LG = 4) or 8 x 129 (LG = 2)
 constexpr int kGsStage = 16 * (kWave + 1);
 
-// stage: kGsStage floats of LDS per wave of the block
-template <class Act>
+// LG lanes per G row (R = 4 LG floats, LG = 2 or 4), lane q holding floats 4q..4q+3; a chunk
+// of 8 entries is 8 / LG entries per lane (one or two 16-byte loads).  stage: kGsStage floats
+// of LDS per wave of the block.
+template <int LG, class Act>
 __device__ inline void bwd_groups(const GsArgs &a, const Act &act, float *stage) {
-    const int q = threadIdx.x % 4;
-    const int64_t g = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / 4;
-    if (g >= a.n_groups) return;  // the whole lane group leaves together
+    constexpr int R = 4 * LG, EPL = 8 / LG, CW = (kWave / LG) * kGsCols;
+    const int q = threadIdx.x % LG;
+    const int64_t g = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / LG;
+    // a group past the end walks nothing but still takes part in the staging below
+    const bool own = g < a.n_groups;
     const char *Gb = reinterpret_cast<const char *>(a.G) + static_cast<uint32_t>(q) * 16u;
     float acc[kGsCols][4];
 #pragma unroll
     for (int j = 0; j < kGsCols; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[j][i] = 0.0f;
-    const int32_t *sg = a.seg + g * (kGsSlices + 1);
-    int32_t lo = sg[0];
+    const int32_t *sg = a.seg + (own ? g : 0) * (kGsSlices + 1);
+    int32_t lo = own ? sg[0] : 0;
     for (int p = 0; p < kGsSlices; ++p) {
-        const int32_t hi = sg[p + 1];
+        const int32_t hi = own ? sg[p + 1] : 0;
         for (int32_t k0 = lo; k0 < hi; k0 += 8) {
-            const uint4 ch = *reinterpret_cast<const uint4 *>(a.pw + k0 + 2 * q);
+            uint2 my[EPL];
+#pragma unroll
+            for (int h = 0; h < EPL; h += 2) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(a.pw + k0 + EPL * q + h);
+                my[h] = make_uint2(v.x, v.y);
+                my[h + 1] = make_uint2(v.z, v.w);
+            }
             float4 gv[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const uint32_t r = quad_bcast((u & 1) ? ch.z : ch.x, u >> 1);
-                gv[u] = *reinterpret_cast<const float4 *>(Gb + (r & kGsRowMask) * 64u);
+                const uint32_t r = group_bcast<LG>(my[u % EPL].x, u / EPL);
+                gv[u] = *reinterpret_cast<const float4 *>(Gb + (r & kGsRowMask) * (R * 4u));
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const uint32_t col = quad_bcast((u & 1) ? ch.z : ch.x, u >> 1) >> kGsRowBits;
-                const float wu = __uint_as_float(quad_bcast((u & 1) ? ch.w : ch.y, u >> 1));
+                const uint32_t col = group_bcast<LG>(my[u % EPL].x, u / EPL) >> kGsRowBits;
+                const float wu = __uint_as_float(group_bcast<LG>(my[u % EPL].y, u / EPL));
                 const float t0 = wu * gv[u].x, t1 = wu * gv[u].y, t2 = wu * gv[u].z, t3 = wu * gv[u].w;
 #pragma unroll
                 for (int j = 0; j < kGsCols; ++j) {
@@ -364,23 +385,26 @@ __device__ inline void bwd_groups(const GsArgs &a, const Act &act, float *stage)
         }
         lo = hi;
     }
-    // dz through LDS: the wave's 16 groups own 64 consecutive columns, so each element's
-    // 64 values leave as one coalesced store (lane l writes column 64 * wave + l, which
-    // belongs to its own group)
+    // dz through LDS: the wave's groups own CW consecutive columns, so each element's
+    // values leave as coalesced stores
     const int lane = threadIdx.x % kWave;
     float *st = stage + (threadIdx.x / kWave) * kGsStage;
-    const int gl = lane / 4;
+    const int gl = lane / LG;
 #pragma unroll
     for (int j = 0; j < kGsCols; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[(4 * q + i) * (kWave + 1) + 4 * gl + j] = acc[j][i];
+        for (int i = 0; i < 4; ++i) st[(4 * q + i) * (CW + 1) + kGsCols * gl + j] = acc[j][i];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int64_t c = (g - gl) * kGsCols + lane;
-    if (c < a.n_cols) {
-        const typename Act::Col ci = act.col(c);
-        for (int e = 0; e < a.n_elem; ++e) *act.out(ci, e) = st[e * (kWave + 1) + lane];
+    const int64_t cw0 = (g - gl) * kGsCols;
+#pragma unroll
+    for (int cc = lane; cc < CW; cc += kWave) {
+        const int64_t c = cw0 + cc;
+        if (c < a.n_cols) {
+            const typename Act::Col ci = act.col(c);
+            for (int e = 0; e < a.n_elem; ++e) *act.out(ci, e) = st[e * (CW + 1) + cc];
+        }
     }
 }
 

@@ -189,14 +189,14 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         order_inv[order[k]] = static_cast<int32_t>(k);
         ph_inv[ph_order[k]] = static_cast<int32_t>(k);
     }
-    // grouped row-sliced order (recurrent tables): a stable counting sort by (G row,
+    // grouped row-sliced order (backward dz walks): a stable counting sort by (G row,
     // column in group), then by (group, row slice); each (group, slice) segment is padded to
     // a multiple of kGsPad with copies of its last row marked as column 7 (weight +0.0f)
     const int64_t n_rows = static_cast<int64_t>(n_types) * n_post;
     std::vector<int32_t> gs_seg, gs_src;
     std::vector<uint2> gs_pw;
     int64_t n_groups = 0, n_gs = 0;
-    if (n_delay_slots > 1 && n_syn > 0 && n_rows <= static_cast<int64_t>(kGsRowMask) + 1) {
+    if (n_syn > 0 && n_rows <= static_cast<int64_t>(kGsRowMask) + 1) {
         n_groups = (n_cols + kGsCols - 1) / kGsCols;
         std::vector<int64_t> key(n_syn);
         for (int64_t i = 0; i < n_syn; ++i)
