@@ -25,6 +25,7 @@ constexpr int kGsSlices = 4;
 constexpr int kGsPad = 8;
 constexpr int kGsRowBits = 29;
 constexpr uint32_t kGsRowMask = (1u << kGsRowBits) - 1u;
+static_assert(kGsCols < 7, "column-in-group 7 marks padding (3 bits above the row)");
 
 // ---- error plumbing -------------------------------------------------------
 void set_error(const std::string &msg);

@@ -288,7 +288,7 @@ __device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
 
 // ---- grouped row-sliced backward (16-float G rows) ------------------------------
 // dz of every column over the grouped row-sliced order: lane group g (4 lanes, lane q
-// holding floats 4q..4q+3 of a row) owns columns kGsCols*g ..; it walks its entries of
+// holding floats 4q..4q+3 of a row) owns columns kGsCols*g .. (4 of them); it walks its entries of
 // one G-row slice at a time, 8 per step (one 64-byte load, lane q holding entries 2q and
 // 2q+1, shared in the group by DPP), and adds w * G[row] into the column's accumulator.
 // Every wave finishes a slice before starting the next, so the waves in flight gather
@@ -330,9 +330,10 @@ __device__ inline uint32_t group_bcast(uint32_t v, int src) {
                     : static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xF5, 0xF, 0xF, false));
 }
 
-// LDS floats per wave for the dz staging of bwd_groups: [R][columns per wave + 1], at most
-// 16 x 65 (LG = 4) or 8 x 129 (LG = 2)
-constexpr int kGsStage = 16 * (kWave + 1);
+// LDS floats per wave for the dz staging of bwd_groups: [R][columns per wave + 1] for
+// LG = 4 (16 floats x 16 kGsCols columns) or LG = 2 (8 x 32 kGsCols), whichever is larger
+constexpr int kGsStage = 16 * (16 * kGsCols + 1) > 8 * (32 * kGsCols + 1) ? 16 * (16 * kGsCols + 1)
+                                                                           : 8 * (32 * kGsCols + 1);
 
 // LG lanes per G row (R = 4 LG floats, LG = 2 or 4), lane q holding floats 4q..4q+3; a chunk
 // of 8 entries is 8 / LG entries per lane (one or two 16-byte loads).  stage: kGsStage floats
