@@ -349,9 +349,13 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
     load_basis_lds(basis_lds, a.basis, k.n_types * k.nb);
     const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (gt >= static_cast<int64_t>(k.B) * k.Np) return;  // whole waves only (Np % 64 == 0)
-    const int b = static_cast<int>(gt / k.Np);
-    const int n = static_cast<int>(gt % k.Np);
+    // wave w: batch entry w % B of neurons 64 (w / B) ..: the B waves of a neuron block run
+    // back to back and share its background table entries in cache
     const int lane = threadIdx.x & (kWave - 1);
+    const int64_t wv =
+        static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int b = static_cast<int>(wv % k.B);
+    const int n = static_cast<int>(wv / k.B) * kWave + lane;
     constexpr int nb = NB;
     const int t = a.t;
     bool spike = false, refr = false;
