@@ -44,8 +44,9 @@ def _args():
                     help="mse: the configuration's firing-rate MSE against lognormal(4 Hz) targets; "
                          "reference: the reference's rate-distribution target + voltage regularization")
     ap.add_argument("--seq-len", type=int, default=None)
-    ap.add_argument("--cpu-steps", type=int, default=10,
-                    help="timesteps of the CPU baseline sample (0: skip)")
+    ap.add_argument("--cpu-steps", type=int, default=30,
+                    help="timesteps of the CPU baseline sample, timed with one thread and with the "
+                         "host's cores (0: skip)")
     ap.add_argument("--forward-only", action="store_true")
     ap.add_argument("--op", action="store_true",
                     help="time the op-level entry points instead (calculate_synaptic_currents forward in "
@@ -412,34 +413,47 @@ def main():
                 "algorithmic_bytes_per_launch": int(alg_bytes), "basis": unit_desc,
                 "avg_launch_us": round(avg_ms * 1000.0, 2), "launches_timed": launches}
 
-    # CPU baseline: the C restatement on a bounded prefix of the same workload
-    cpu = None
+    # CPU baseline: the C restatement on a bounded prefix of the same workload, timed with
+    # one thread and with the host's cores (its OpenMP loops keep every sum's order, so both
+    # give the same bits)
+    cpu = cpu_1t = None
     if args.cpu_steps > 0:
+        from oracle import cpu as orc_cpu
         from oracle.cpu import OracleCell
         Tc = min(args.cpu_steps, T)
         oc = OracleCell(tb, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.5, pseudo_gauss=True)
-        c0 = time.perf_counter()
-        oz, ov, oref, _ = oc.forward(lgn_np[:Tc], bkg_np[:Tc])
-        if not args.forward_only:
-            from oracle.rate_loss_ref import rate_dist_loss, rate_mse
-            cnt = oz.reshape(Tc, B, N).sum((0, 1))
-            gv = None
-            if args.loss == "mse":
-                _, gzn = rate_mse(cnt, Tc * B, targets_np)
-            else:
-                ids = np.concatenate([rate_loss.populations[k] for k in rate_loss.populations])
-                tgt = np.concatenate([rate_loss.target_rates[k]["sorted_target_rates"] for k in rate_loss.populations])
-                ptrs = np.concatenate([[0], np.cumsum([rate_loss.populations[k].size for k in rate_loss.populations])])
-                _, gzn = rate_dist_loss(cnt, Tc * B, ids, ptrs, tgt, rate_cost=10000.0, shuffle=True)
-                gv = (np.float32(2.0 / (Tc * B * N)) * (ov - np.float32(1.0))).astype(np.float32)
-            oc.backward(lgn_np[:Tc], bkg_np[:Tc], oz, oref, ov, gz_neuron=gzn, gv_loss=gv,
-                        want=("rec", "lgn"))
-        cpu_s = time.perf_counter() - c0
-        cpu = {"value": round(B * N * Tc / cpu_s, 1), "unit": "neuron-timesteps/s", "cores": 1,
-               "kind": "port",
-               "sample": f"oracle/glif_oracle.c single thread, first {Tc} of {T} timesteps of the same "
-                         f"workload (B={B}, N={N}), {'forward only' if args.forward_only else 'forward + BPTT'}, "
-                         f"{cpu_s:.1f} s"}
+
+        def cpu_run(threads):
+            used = orc_cpu.set_threads(threads)
+            c0 = time.perf_counter()
+            oz, ov, oref, _ = oc.forward(lgn_np[:Tc], bkg_np[:Tc])
+            if not args.forward_only:
+                from oracle.rate_loss_ref import rate_dist_loss, rate_mse
+                cnt = oz.reshape(Tc, B, N).sum((0, 1))
+                gv = None
+                if args.loss == "mse":
+                    _, gzn = rate_mse(cnt, Tc * B, targets_np)
+                else:
+                    ids = np.concatenate([rate_loss.populations[k] for k in rate_loss.populations])
+                    tgt = np.concatenate([rate_loss.target_rates[k]["sorted_target_rates"] for k in rate_loss.populations])
+                    ptrs = np.concatenate([[0], np.cumsum([rate_loss.populations[k].size for k in rate_loss.populations])])
+                    _, gzn = rate_dist_loss(cnt, Tc * B, ids, ptrs, tgt, rate_cost=10000.0, shuffle=True)
+                    gv = (np.float32(2.0 / (Tc * B * N)) * (ov - np.float32(1.0))).astype(np.float32)
+                oc.backward(lgn_np[:Tc], bkg_np[:Tc], oz, oref, ov, gz_neuron=gzn, gv_loss=gv,
+                            want=("rec", "lgn"))
+            return used, time.perf_counter() - c0
+
+        what = (f"first {Tc} of {T} timesteps of the same workload (B={B}, N={N}), "
+                f"{'forward only' if args.forward_only else 'forward + BPTT'}")
+        n1, s1 = cpu_run(1)
+        cpu_1t = {"value": round(B * N * Tc / s1, 1), "unit": "neuron-timesteps/s", "cores": n1, "kind": "port",
+                  "sample": f"oracle/glif_oracle.c single thread, {what}, {s1:.1f} s"}
+        cores = min(len(os.sched_getaffinity(0)), 16)
+        nt, st = cpu_run(cores) if cores > 1 else (n1, s1)
+        cpu = {"value": round(B * N * Tc / st, 1), "unit": "neuron-timesteps/s", "cores": nt, "kind": "port",
+               "sample": f"oracle/glif_oracle.c, {nt} OpenMP threads (batch entries and columns in parallel, "
+                         f"same sums as one thread), {what}, {st:.1f} s"}
+        orc_cpu.set_threads(1)
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "neuron-timesteps/s", "n_gpus": 1,
@@ -453,6 +467,7 @@ def main():
                    "loss": None if args.forward_only else args.loss},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baseline_1t": cpu_1t,
         "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(bwd_ms, 3),
         "synaptic_events_per_s": round((e_rec + e_lgn + e_bkg) / (fwd_ms / 1000.0), 1) if fwd_ms else None,
         "mean_rate_hz": round(float(sc_host.mean()) / T * 1000.0, 3),

@@ -49,11 +49,19 @@ def lib():
             L.orc_forward.restype = C.c_int
             L.orc_forward.argtypes = [C.POINTER(OrcCell), C.c_int, C.c_int, u8p, u8p, f32p, f32p,
                                       i32p, f32p, f32p, f32p, u8p, f32p, u8p]
+            L.orc_set_threads.restype = C.c_int
+            L.orc_set_threads.argtypes = [C.c_int]
             L.orc_backward.restype = C.c_int
             L.orc_backward.argtypes = [C.POINTER(OrcCell), C.c_int, C.c_int, u8p, u8p, u8p, u8p,
                                        f32p, f32p, f32p, f32p, f32p, f32p, f32p, f32p]
             _lib = L
     return _lib
+
+
+def set_threads(n):
+    """Threads of the oracle's OpenMP loops (results are the same for any count); returns
+    the number in use."""
+    return int(lib().orc_set_threads(int(n)))
 
 
 def _p(a, t):

@@ -27,16 +27,36 @@
  *                     the spike buffer and of v, refractory-masked surrogate).
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off: every a*b+c rounds twice, as
- * TF's separate Mul/Add kernels do).
+ * TF's separate Mul/Add kernels do; -fopenmp).  The OpenMP loops split work only where
+ * every output element keeps its serial summation order: batch entries (forward scatter,
+ * dz scatter, adjoint) and presynaptic columns (dW: each synapse belongs to one column and
+ * still adds its batch entries in ascending order), so any thread count gives the same
+ * bits as one thread.
  */
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
 #define ORC_EINVAL (-22)
 #define ORC_ERANGE (-34)
 #define ORC_ENOMEM (-12)
+
+/* Threads of the OpenMP loops (n < 1: 1); the number in use. */
+int orc_set_threads(int n)
+{
+#ifdef _OPENMP
+    omp_set_num_threads(n < 1 ? 1 : n);
+    return omp_get_max_threads();
+#else
+    (void)n;
+    return 1;
+#endif
+}
 
 /* -------------------------------------------- CSR (pre_ind_table) build ---- */
 /* Returns 0, or ORC_EINVAL (n_cols <= 0), or ORC_ERANGE with *bad_index set to the
@@ -83,6 +103,7 @@ void orc_syn_fwd(int B, int64_t n_post, int64_t n_cols, int nb, const float *act
                  const int64_t *post, const float *w, const uint8_t *sid, const float *basis,
                  const int64_t *order, const int64_t *row_splits, float *I)
 {
+#pragma omp parallel for schedule(static) if (B > 1)
     for (int b = 0; b < B; ++b)
         for (int64_t c = 0; c < n_cols; ++c) {
             float a = act[(int64_t)b * n_cols + c];
@@ -110,19 +131,25 @@ void orc_syn_bwd(int B, int64_t n_post, int64_t n_cols, int nb, int64_t S, const
     if (dz) {
         memset(dz, 0, sizeof(float) * (size_t)B * (size_t)n_cols);
         for (int r = 0; r < nb; ++r) {
-            memset(scratch, 0, sizeof(float) * (size_t)B * (size_t)n_cols);
-            for (int64_t s = 0; s < S; ++s) {
-                float wr = w[s] * basis[(int64_t)sid[s] * nb + r];
-                for (int b = 0; b < B; ++b)
-                    scratch[(int64_t)b * n_cols + col[s]] +=
-                        dy[((int64_t)b * n_post + post[s]) * nb + r] * wr;
+#pragma omp parallel for schedule(static) if (B > 1)
+            for (int b = 0; b < B; ++b) {
+                float *sc = scratch + (int64_t)b * n_cols;
+                memset(sc, 0, sizeof(float) * (size_t)n_cols);
+                for (int64_t s = 0; s < S; ++s) {
+                    float wr = w[s] * basis[(int64_t)sid[s] * nb + r];
+                    sc[col[s]] += dy[((int64_t)b * n_post + post[s]) * nb + r] * wr;
+                }
             }
+#pragma omp parallel for schedule(static)
             for (int64_t i = 0; i < (int64_t)B * n_cols; ++i) dz[i] += scratch[i];
         }
     }
     if (dW) {
-        for (int b = 0; b < B; ++b)
-            for (int64_t c = 0; c < n_cols; ++c) {
+        /* column-parallel: synapse s belongs to one column and adds its events in
+         * ascending b, the order of the serial b-outer loop */
+#pragma omp parallel for schedule(dynamic, 256)
+        for (int64_t c = 0; c < n_cols; ++c)
+            for (int b = 0; b < B; ++b) {
                 float a = act[(int64_t)b * n_cols + c];
                 if (!(a > 0.0f)) continue;
                 for (int64_t k = row_splits[c]; k < row_splits[c + 1]; ++k) {
@@ -186,7 +213,7 @@ int orc_forward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint8
     float *Ibkg = (float *)calloc((size_t)BN * nb, sizeof(float));
     float *xl = (float *)malloc(sizeof(float) * (size_t)B * (size_t)(c->lgn.n_cols + 1));
     float *xb = (float *)malloc(sizeof(float) * (size_t)B * (size_t)(c->bkg.n_cols + 1));
-    float *znew = (float *)malloc(sizeof(float) * (size_t)N);
+    float *znew = (float *)malloc(sizeof(float) * (size_t)BN);
     if (!Irec || !Ilgn || !Ibkg || !xl || !xb || !znew) {
         free(Irec); free(Ilgn); free(Ibkg); free(xl); free(xb); free(znew);
         return ORC_ENOMEM;
@@ -211,6 +238,7 @@ int orc_forward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint8
         orc_syn_fwd(B, N, c->bkg.n_cols, nb, xb, 1, c->bkg.post, c->bkg.w, c->bkg.sid, c->basis,
                     c->bkg.order, c->bkg.row_splits, Ibkg);
 
+#pragma omp parallel for schedule(static) if (B > 1)
         for (int b = 0; b < B; ++b) {
             for (int64_t n = 0; n < N; ++n) {
                 const int64_t bn = (int64_t)b * N + n;
@@ -239,12 +267,12 @@ int orc_forward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint8
                 if (z_out) z_out[(int64_t)t * BN + bn] = (uint8_t)z;
                 if (v_out) v_out[(int64_t)t * BN + bn] = vn;
                 if (ref_out) ref_out[(int64_t)t * BN + bn] = (uint8_t)(rn > 0);
-                znew[n] = z;
+                znew[bn] = z;
             }
             /* new_z_buf = concat([new_z, z_buf[:, :-N]]) (models.py:1117) */
             float *zb = zbuf + (int64_t)b * D * N;
             memmove(zb + N, zb, sizeof(float) * (size_t)((D - 1) * N));
-            memcpy(zb, znew, sizeof(float) * (size_t)N);
+            memcpy(zb, znew + (int64_t)b * N, sizeof(float) * (size_t)N);
         }
     }
     free(Irec); free(Ilgn); free(Ibkg); free(xl); free(xb); free(znew);
@@ -290,6 +318,7 @@ int orc_backward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint
 
     for (int t = T - 1; t >= 0; --t) {
         float *slot = ring + (int64_t)(t % (D + 1)) * BN;
+#pragma omp parallel for schedule(static) if (B > 1)
         for (int b = 0; b < B; ++b)
             for (int64_t n = 0; n < N; ++n) {
                 const int64_t bn = (int64_t)b * N + n, tbn = (int64_t)t * BN + bn;

@@ -273,3 +273,29 @@ def test_bptt_per_neuron_loss_gradient_equals_dense():
     b = oc.backward(lgn, bkg, z, ref, v, gz_loss=np.broadcast_to(gn, z.shape).copy())
     for k in a:
         np.testing.assert_array_equal(a[k], b[k])
+
+
+def test_threaded_oracle_gives_the_same_bits():
+    """The OpenMP loops split batch entries and columns only, so every sum keeps its
+    serial order: 1 and 4 threads give identical spikes, voltages and gradients (counts
+    on the background table exercise the count-scaled dW)."""
+    cfg = tiny_config(n=150, fanin=20, n_lgn=40, rs=2.0, ins=3.0)
+    _, tb = network(cfg, seed=4, dense_basis=True)
+    T, B = 25, 3
+    lgn, bkg = sy.make_inputs(cfg, seed=4, seq_len=T, batch=B)
+    out = []
+    try:
+        for threads in (1, 4):
+            assert orc.set_threads(threads) >= 1
+            oc = orc.OracleCell(tb)
+            z, v, ref, _ = oc.forward(lgn, bkg)
+            gz = np.random.default_rng(3).normal(0, 1, z.shape).astype(np.float32)
+            out.append((z, v, oc.backward(lgn, bkg, z, ref, v, gz_loss=gz)))
+    finally:
+        orc.set_threads(1)
+    (z1, v1, g1), (z4, v4, g4) = out
+    assert z1.sum() > 0
+    np.testing.assert_array_equal(z1, z4)
+    np.testing.assert_array_equal(v1.view(np.uint32), v4.view(np.uint32))
+    for k in g1:
+        np.testing.assert_array_equal(g1[k].view(np.uint32), g4[k].view(np.uint32))
