@@ -137,6 +137,34 @@ def test_backward_grouped_walk_matches_oracle(B, n, T):
         assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
 
 
+@pytest.mark.parametrize("B", [2, 5])
+def test_many_synapse_types_forward_and_backward(B):
+    """40 synapse types over 4 receptors (the real network has one basis row per synaptic
+    model): G has 40 row blocks, the grouped walk's rows span all of them (B = 5) and the
+    type-phased walk has 40 phases (B = 2); deterministic forward bit-exact, BPTT within
+    the bar."""
+    import dataclasses
+    cfg = dataclasses.replace(tiny_config(rs=3.0, ins=4.0), n_syn_types=40, n_basis=4)
+    tn = network(cfg, seed=11, dense_basis=True)
+    T = 40
+    lgn, bkg = _inputs(cfg, T, B, seed=12)
+    cell = _cell(tn, "deterministic", **CELL_KW)
+    z, v, _ = cell.rollout(lgn, bkg)
+    oc = _oracle(tn[1], **ORC_KW)
+    oz, ov, oref, _ = oc.forward(lgn, bkg)
+    assert oz.sum() > 0
+    np.testing.assert_array_equal(z.cpu().numpy().astype(np.uint8), oz)
+    np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), ov.view(np.uint32))
+    gz = np.random.default_rng(13).normal(0, 1, oz.shape).astype(np.float32)
+    g = cell.backward(gz=torch.tensor(gz, device="cuda"))
+    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz)
+    for k in ("rec", "lgn", "bkg"):
+        a, e = g[k].cpu().numpy(), og[k]
+        scale = np.max(np.abs(e))
+        assert scale > 0, k
+        assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
+
+
 def test_backward_rate_loss_per_neuron_grad():
     """gz broadcast per neuron (the rate-loss form) equals the dense form."""
     cfg = tiny_config(rs=2.0, ins=1.0)
