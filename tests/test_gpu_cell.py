@@ -139,12 +139,12 @@ def test_backward_grouped_walk_matches_oracle(B, n, T):
 
 @pytest.mark.parametrize("B", [2, 5])
 def test_many_synapse_types_forward_and_backward(B):
-    """40 synapse types over 4 receptors (the real network has one basis row per synaptic
-    model): G has 40 row blocks, the grouped walk's rows span all of them (B = 5) and the
-    type-phased walk has 40 phases (B = 2); deterministic forward bit-exact, BPTT within
-    the bar."""
+    """121 synapse types over 4 receptors, the shape of the reference's basis table
+    (synaptic_data/basis_function_weights.csv: one row per synaptic model): G has 121 row
+    blocks, the grouped walk's rows span all of them (B = 5) and the type-phased walk has
+    121 phases (B = 2); deterministic forward bit-exact, BPTT within the bar."""
     import dataclasses
-    cfg = dataclasses.replace(tiny_config(rs=3.0, ins=4.0), n_syn_types=40, n_basis=4)
+    cfg = dataclasses.replace(tiny_config(rs=3.0, ins=4.0), n_syn_types=121, n_basis=4)
     tn = network(cfg, seed=11, dense_basis=True)
     T = 40
     lgn, bkg = _inputs(cfg, T, B, seed=12)
