@@ -768,10 +768,9 @@ struct RecDwArgs {
     float *dw;  // column-grouped order, accumulated
 };
 
-__global__ void __launch_bounds__(kBlock) k_bwd_rec_dw(RecDwArgs a, ActWin act) {
+__device__ inline void rec_dw_body(const RecDwArgs &a, const ActWin &act, int64_t bid) {
     const int lane = threadIdx.x % kWave;
-    const int64_t c0 =
-        static_cast<int64_t>(blockIdx.x) * blockDim.x + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave;
+    const int64_t c0 = bid * blockDim.x + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave;
     if (c0 >= a.n_cols) return;  // the whole wave leaves together
     const int64_t c = c0 + lane;
     uint32_t m = 0;
@@ -856,11 +855,11 @@ struct BwdInArgs {
 // (reverse time, then batch), the order in which the reference's per-step
 // gradients accumulate.
 template <bool COUNTS>
-__global__ void __launch_bounds__(kBlock) k_bwd_in(BwdInArgs a) {
+__device__ inline void bwd_in_body(const BwdInArgs &a, int64_t bid, int64_t nblk) {
     constexpr int L = kWave;
-    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t gt = bid * blockDim.x + threadIdx.x;
     const int lane_s = threadIdx.x % L;
-    const int64_t n_subs = static_cast<int64_t>(gridDim.x) * blockDim.x / L;
+    const int64_t n_subs = nblk * blockDim.x / L;
     const int64_t i0 = a.off[a.j], units = (a.off[a.j + 1] - i0) * a.chunks;
     for (int64_t u = gt / L; u < units; u += n_subs) {
         const int64_t it = i0 + u / a.chunks;
@@ -897,6 +896,23 @@ static void launch_bwd_rec(const ColArgs &ca, int R, const ActWin &act, hipStrea
     else if (LG == 2) hipLaunchKernelGGL(k_bwd_rec<2>, grid, dim3(kBlock), 0, s, ca, act);
     else if (LG == 4) hipLaunchKernelGGL(k_bwd_rec<4>, grid, dim3(kBlock), 0, s, ca, act);
     else hipLaunchKernelGGL(k_bwd_rec<8>, grid, dim3(kBlock), 0, s, ca, act);
+}
+
+__global__ void __launch_bounds__(kBlock) k_bwd_rec_dw(RecDwArgs a, ActWin act) { rec_dw_body(a, act, blockIdx.x); }
+
+template <bool COUNTS>
+__global__ void __launch_bounds__(kBlock) k_bwd_in(BwdInArgs a) {
+    bwd_in_body<COUNTS>(a, blockIdx.x, gridDim.x);
+}
+
+// The recurrent dW pass and the LGN dW of one window in one launch: blocks [0, rec_blocks)
+// run the first, the rest the second.  Both are chains of dependent loads with little
+// traffic, so sharing the machine overlaps their latencies.
+__global__ void __launch_bounds__(kBlock) k_bwd_dw_rec_lgn(RecDwArgs a, ActWin act, BwdInArgs la, int rec_blocks) {
+    if (static_cast<int>(blockIdx.x) < rec_blocks)
+        rec_dw_body(a, act, blockIdx.x);
+    else
+        bwd_in_body<false>(la, blockIdx.x - rec_blocks, gridDim.x - rec_blocks);
 }
 
 static void launch_bwd_in(const BwdInArgs &ia, int64_t max_units, hipStream_t s) {
@@ -1321,17 +1337,21 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         act.s0 = s0;
         {
             ProfScope p(kProfBwdRec, s);
+            la.j = j;
+            la.s0 = s0;
             if (gs) {
                 hipLaunchKernelGGL(k_bwd_rec_gs, dim3(ceil_div(ga.n_groups * 4, kBlock)), dim3(kBlock), 0, s, ga, act);
-                if (dw_rec)
-                    hipLaunchKernelGGL(k_bwd_rec_dw, dim3(ceil_div(tr->n_cols, kBlock)), dim3(kBlock), 0, s, da, act);
+                const int rec_blocks = ceil_div(tr->n_cols, kBlock);
+                if (dw_rec && dw_lgn)  // the LGN dW rides along (timed here)
+                    hipLaunchKernelGGL(k_bwd_dw_rec_lgn, dim3(rec_blocks + grid_subwaves(lgn_units, kWave)),
+                                       dim3(kBlock), 0, s, da, act, la, rec_blocks);
+                else if (dw_rec)
+                    hipLaunchKernelGGL(k_bwd_rec_dw, dim3(rec_blocks), dim3(kBlock), 0, s, da, act);
             } else {
                 launch_bwd_rec(ca, Rg, act, s);
             }
         }
-        if (dw_lgn) {
-            la.j = j;
-            la.s0 = s0;
+        if (dw_lgn && !(gs && dw_rec)) {
             ProfScope p(kProfBwdLgn, s);
             launch_bwd_in(la, lgn_units, s);
         }
