@@ -405,13 +405,18 @@ def main():
         # of the window's active events (the algorithm's bytes, whichever table layout
         # the library walks)
         steps_per_launch = (T - 2) / max(launches / args.steps, 1)
-        active = e_rec / max(T, 1) * steps_per_launch
-        # the LGN weight gradient of the window runs in the same launch as the recurrent
-        # dW: its events' table entry (4 B) and dW read-modify-write (8 B)
-        active_lgn = e_lgn / max(T, 1) * steps_per_launch
-        alg_bytes = (S * 8 + (nt * D * N + 1) * 4 + steps_per_launch * B * D * N * 4 + N * nt * Rg * 4
-                     + (steps_per_launch + D) * B * words * 8 + active * 8 + active_lgn * 12)
-        unit_desc = f"bytes per backward window of {Wwin} timesteps (recurrent dz + dW, LGN dW)"
+        if Rg == 16:
+            # the grouped dz walk alone (the window's weight gradients run with the next
+            # window's adjoint): one 8-byte entry per synapse, the per-column pointers, the
+            # dz rows of the window's steps, G read once
+            alg_bytes = (S * 8 + (D * N + 1) * 4 + steps_per_launch * B * D * N * 4 + N * nt * Rg * 4)
+            unit_desc = f"bytes per backward window of {Wwin} timesteps (recurrent dz)"
+        else:
+            # dz and the dW of the window's active events in one pass
+            active = e_rec / max(T, 1) * steps_per_launch
+            alg_bytes = (S * 8 + (nt * D * N + 1) * 4 + steps_per_launch * B * D * N * 4 + N * nt * Rg * 4
+                         + (steps_per_launch + D) * B * words * 8 + active * 8)
+            unit_desc = f"bytes per backward window of {Wwin} timesteps (recurrent dz + dW)"
     else:
         # per launch = one timestep's pushed events: the 8-byte table entry (post |
         # syn_id, weight) and one 4-byte fp32 atomic each (identity basis)

@@ -57,7 +57,7 @@ struct CellWs {
     uint8_t *bkg_cnt;   // [T][B][n_bkg]
     void *scratch;
     float *dZ;          // [ring][B][D * N]
-    float *G;           // [n_types][N][R]
+    float *G;           // [2][n_types][N][R]   (windows alternate between the two)
     float *gV;          // [B][N]
     float *gP, *gR;     // [nb][B][N]
     float *vloss_part;  // [kVlossBlocks] partial sums of the voltage penalty
@@ -100,7 +100,7 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.bkg_cnt = cv.take<uint8_t>(static_cast<size_t>(T) * B * nk);
     w.scratch = cv.take<char>(std::max(compact_scratch_bytes(T, nl), compact_scratch_bytes(T, nk)));
     w.dZ = cv.take<float>(static_cast<size_t>(ring_size(c)) * B * c->D * c->N);
-    w.G = cv.take<float>(static_cast<size_t>(c->N) * c->n_types * g_row(Wwin, B));
+    w.G = cv.take<float>(2 * static_cast<size_t>(c->N) * c->n_types * g_row(Wwin, B));
     w.gV = cv.take<float>(BN);
     w.gP = cv.take<float>(BN * c->nb);
     w.gR = cv.take<float>(BN * c->nb);
@@ -559,7 +559,7 @@ struct AdjArgs {
 // its G rows in LDS until the window's ticks are done, then writes whole rows.
 // Otherwise: thread per (n, b), batch fastest, G written in place.
 template <int NB, bool STAGE>
-__global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
+__device__ inline void adj_body(const AdjArgs &a, int64_t bid) {
     extern __shared__ float lds_f[];
     float *basis_lds = lds_f;
     const CellConst &k = a.k;
@@ -568,7 +568,7 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
     int n, b;
     float *Gl = nullptr;
     const int nr = kBlock / k.B;
-    const int32_t n0 = static_cast<int32_t>(blockIdx.x) * nr;
+    const int32_t n0 = static_cast<int32_t>(bid) * nr;
     if (STAGE) {
         Gl = lds_f + k.n_types * k.nb;
         const int rows = k.n_types * nr * a.R;
@@ -577,7 +577,7 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
         b = static_cast<int>(threadIdx.x) / nr;
         n = n0 + static_cast<int>(threadIdx.x) - b * nr;
     } else {
-        const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+        const int64_t gt = bid * blockDim.x + threadIdx.x;
         // batch fastest: neighbouring lanes write neighbouring G entries
         n = static_cast<int>(gt / k.B);
         b = static_cast<int>(gt - static_cast<int64_t>(n) * k.B);
@@ -705,6 +705,11 @@ __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
             a.G[(static_cast<int64_t>(s) * k.N + n0) * a.R + rem] = Gl[s * nr * a.R + rem];
         }
     }
+}
+
+template <int NB, bool STAGE>
+__global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
+    adj_body<NB, STAGE>(a, blockIdx.x);
 }
 
 // ------------------------------------------------------ backward synapses ----
@@ -915,6 +920,29 @@ __global__ void __launch_bounds__(kBlock) k_bwd_dw_rec_lgn(RecDwArgs a, ActWin a
         bwd_in_body<false>(la, blockIdx.x - rec_blocks, gridDim.x - rec_blocks);
 }
 
+// The adjoint of window j (blocks [0, adj_blocks), writing G buffer j % 2) with the weight
+// gradients of window j - 1 (the rest: the recurrent dW pass, then the LGN dW, reading G
+// buffer (j - 1) % 2): the adjoint streams state through HBM while the dW passes are chains
+// of dependent loads, and one launch keeps the dW work out of window j's dz walk.
+struct DwPrev {
+    RecDwArgs da;
+    ActWin act;
+    BwdInArgs la;
+    int32_t rec_blocks, lgn_blocks;
+};
+
+template <int NB, bool STAGE>
+__global__ void __launch_bounds__(kBlock) k_adj_dw(AdjArgs a, int adj_blocks, DwPrev p) {
+    const int64_t bid = blockIdx.x;
+    if (bid < adj_blocks) {
+        adj_body<NB, STAGE>(a, bid);
+    } else if (bid < adj_blocks + p.rec_blocks) {
+        rec_dw_body(p.da, p.act, bid - adj_blocks);
+    } else {
+        bwd_in_body<false>(p.la, bid - adj_blocks - p.rec_blocks, p.lgn_blocks);
+    }
+}
+
 static void launch_bwd_in(const BwdInArgs &ia, int64_t max_units, hipStream_t s) {
     const dim3 grid(grid_subwaves(max_units, kWave));
     if (ia.cnt)
@@ -941,18 +969,24 @@ static size_t adj_stage_lds(const CellConst &k, int R) {
     return sizeof(float) * (static_cast<size_t>(k.n_types) * k.nb + static_cast<size_t>(k.n_types) * nr * R);
 }
 
-static void launch_adj(const AdjArgs &aa, int nb, size_t lds, hipStream_t s) {
+// prev: the weight-gradient passes of the previous window to run in the same launch, or null
+static void launch_adj(const AdjArgs &aa, int nb, size_t lds, hipStream_t s, const DwPrev *prev = nullptr) {
     const CellConst &k = aa.k;
     const size_t slds = adj_stage_lds(k, aa.R);
     const bool stage = slds <= kAdjStageLds;
-    const dim3 grid = stage ? dim3(ceil_div(k.N, kBlock / k.B))
-                            : dim3(ceil_div(static_cast<int64_t>(k.B) * k.N, kBlock));
+    const int adj_blocks = stage ? ceil_div(k.N, kBlock / k.B) : ceil_div(static_cast<int64_t>(k.B) * k.N, kBlock);
     const size_t use = stage ? slds : lds;
+    const dim3 grid(adj_blocks + (prev ? prev->rec_blocks + prev->lgn_blocks : 0));
     switch (nb) {
-#define GLIF_ADJ(NB)                                                                              \
-    case NB:                                                                                      \
-        if (stage) hipLaunchKernelGGL((k_adj<NB, true>), grid, dim3(kBlock), use, s, aa);         \
-        else hipLaunchKernelGGL((k_adj<NB, false>), grid, dim3(kBlock), use, s, aa);              \
+#define GLIF_ADJ(NB)                                                                                 \
+    case NB:                                                                                         \
+        if (prev) {                                                                                  \
+            if (stage) hipLaunchKernelGGL((k_adj_dw<NB, true>), grid, dim3(kBlock), use, s, aa, adj_blocks, *prev); \
+            else hipLaunchKernelGGL((k_adj_dw<NB, false>), grid, dim3(kBlock), use, s, aa, adj_blocks, *prev); \
+        } else {                                                                                     \
+            if (stage) hipLaunchKernelGGL((k_adj<NB, true>), grid, dim3(kBlock), use, s, aa);        \
+            else hipLaunchKernelGGL((k_adj<NB, false>), grid, dim3(kBlock), use, s, aa);             \
+        }                                                                                            \
         break;
         GLIF_ADJ(1) GLIF_ADJ(2) GLIF_ADJ(3) GLIF_ADJ(4) GLIF_ADJ(5) GLIF_ADJ(6) GLIF_ADJ(7) GLIF_ADJ(8)
 #undef GLIF_ADJ
@@ -1254,8 +1288,8 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         (rc = launch_fill_u32(w.gR, 0u, BN * c->nb, s)))
         return rc;
     // padding elements of each G row stay zero
-    if ((rc = launch_fill_u32(w.G, 0u, static_cast<size_t>(c->N) * c->n_types * g_row(win_width(B), B), s)))
-        return rc;
+    const size_t g_elems = static_cast<size_t>(c->N) * c->n_types * g_row(win_width(B), B);
+    if ((rc = launch_fill_u32(w.G, 0u, 2 * g_elems, s))) return rc;
     // the grouped row-sliced walk serves 16-float G rows
     const bool gs = tr->n_gs > 0 && g_row(win_width(B), B) == 16;
     if (dw_rec && (rc = launch_fill_u32(w.dw_rec, 0u, tr->n_syn, s))) return rc;
@@ -1323,35 +1357,44 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     const int64_t lgn_units = tl->n_cols * static_cast<int64_t>(la.chunks);
     const int64_t bkg_units = tb->n_cols * static_cast<int64_t>(ka.chunks);
 
+    // With the grouped walk, the weight-gradient passes of window j (recurrent, then LGN)
+    // run in window j + 1's adjoint launch (k_adj_dw); windows alternate between two G
+    // buffers so that launch reads one while the adjoint writes the other.
+    const bool defer = gs && dw_rec;
+    DwPrev prev{};
+    bool have_prev = false;
     int j = 0;
     for (int t0 = T - 1; t0 >= 2; t0 -= Wwin, ++j) {
         const int nw = std::min(Wwin, t0 - 1);
         const int s0 = t0 - 2;
+        float *Gj = w.G + static_cast<size_t>(j & 1) * g_elems;
+        aa.G = Gj;
+        ca.G = ga.G = da.G = la.G = ka.G = Gj;
         aa.t0 = t0;
         aa.nw = nw;
         {
             ProfScope p(kProfAdj, s);
-            launch_adj(aa, c->nb, lds, s);
+            launch_adj(aa, c->nb, lds, s, have_prev ? &prev : nullptr);
         }
         ca.n_elem = ga.n_elem = da.n_elem = nw * B;
         act.s0 = s0;
+        la.j = j;
+        la.s0 = s0;
         {
             ProfScope p(kProfBwdRec, s);
-            la.j = j;
-            la.s0 = s0;
-            if (gs) {
+            if (gs)
                 hipLaunchKernelGGL(k_bwd_rec_gs, dim3(ceil_div(ga.n_groups * 4, kBlock)), dim3(kBlock), 0, s, ga, act);
-                const int rec_blocks = ceil_div(tr->n_cols, kBlock);
-                if (dw_rec && dw_lgn)  // the LGN dW rides along (timed here)
-                    hipLaunchKernelGGL(k_bwd_dw_rec_lgn, dim3(rec_blocks + grid_subwaves(lgn_units, kWave)),
-                                       dim3(kBlock), 0, s, da, act, la, rec_blocks);
-                else if (dw_rec)
-                    hipLaunchKernelGGL(k_bwd_rec_dw, dim3(rec_blocks), dim3(kBlock), 0, s, da, act);
-            } else {
+            else
                 launch_bwd_rec(ca, Rg, act, s);
-            }
         }
-        if (dw_lgn && !(gs && dw_rec)) {
+        if (defer) {
+            prev.da = da;
+            prev.act = act;
+            prev.la = la;
+            prev.rec_blocks = ceil_div(tr->n_cols, kBlock);
+            prev.lgn_blocks = dw_lgn ? grid_subwaves(lgn_units, kWave) : 0;
+            have_prev = true;
+        } else if (dw_lgn) {
             ProfScope p(kProfBwdLgn, s);
             launch_bwd_in(la, lgn_units, s);
         }
@@ -1361,6 +1404,14 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
             ProfScope p(kProfBwdBkg, s);
             launch_bwd_in(ka, bkg_units, s);
         }
+    }
+    if (have_prev) {  // the last window's weight gradients
+        ProfScope p(kProfAdj, s);
+        if (prev.lgn_blocks)
+            hipLaunchKernelGGL(k_bwd_dw_rec_lgn, dim3(prev.rec_blocks + prev.lgn_blocks), dim3(kBlock), 0, s, prev.da,
+                               prev.act, prev.la, prev.rec_blocks);
+        else
+            hipLaunchKernelGGL(k_bwd_rec_dw, dim3(prev.rec_blocks), dim3(kBlock), 0, s, prev.da, prev.act);
     }
     GLIF_HIP(hipGetLastError());
     if (dw_rec && (rc = launch_gather_f32(dw_rec, w.dw_rec, gs ? tr->order_inv : tr->ph_inv, tr->n_syn, s))) return rc;
