@@ -75,7 +75,7 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     CellWs w{};
     const int64_t BN = static_cast<int64_t>(B) * c->N;
     const int64_t nl = c->lgn->n_cols, nk = c->bkg->n_cols;
-    w.I = cv.take<float>(BN * c->nb);
+    w.I = cv.take<float>(2 * BN * c->nb);   // event mode alternates between the two halves by tick
     w.R = cv.take<float>(BN * c->nb);
     w.P = cv.take<float>(BN * c->nb);
     w.A = cv.take<float>(BN * 2);
@@ -230,6 +230,8 @@ __global__ void __launch_bounds__(kBlock)
 // ------------------------------------------------------------ event push ----
 struct PushArgs {
     int32_t t, D, N, B, W, nb, n_types, chunks_lgn;
+    int32_t d_lo, d_hi;   // delay slots pushed (1-based, inclusive)
+    int32_t lgn;          // push the step's LGN events too
     const uint64_t *zbits;  // [(T + D)][B][W] spike bits, slot s + D holds z_s
     const int32_t *rec_colptr;
     const uint32_t *rec_ps;
@@ -252,24 +254,23 @@ struct PushArgs {
 // counter that every spiking wave would have to increment.
 constexpr int kChunkIters = 4;
 
-__global__ void __launch_bounds__(kBlock) k_push(PushArgs a) {
+__device__ inline void push_body(const PushArgs &a, int64_t bid, int64_t nblk) {
     constexpr int L = kWave;
     extern __shared__ float basis_lds[];
     load_basis_lds(basis_lds, a.basis, a.n_types * a.nb);
     const int64_t BW = static_cast<int64_t>(a.B) * a.W;
-    const int64_t n_words = static_cast<int64_t>(a.D) * BW;
-    const int64_t l0 = a.lgn_off[a.t], n_lgn = a.lgn_off[a.t + 1] - l0;
+    const int64_t n_words = static_cast<int64_t>(a.d_hi - a.d_lo + 1) * BW;
+    const int64_t l0 = a.lgn_off[a.t], n_lgn = a.lgn ? a.lgn_off[a.t + 1] - l0 : 0;
     const int64_t units = n_words + n_lgn * a.chunks_lgn;
     const int lane_s = threadIdx.x % L;
-    const int64_t n_subs = static_cast<int64_t>(gridDim.x) * blockDim.x / L;
+    const int64_t n_subs = nblk * blockDim.x / L;
     const int64_t BN = static_cast<int64_t>(a.B) * a.N;
     // the unit index is uniform across the wave: keep it (and the spike word) scalar
-    const int64_t u0 = static_cast<int64_t>(blockIdx.x) * (blockDim.x / L) +
-                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / L));
+    const int64_t u0 = bid * (blockDim.x / L) + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / L));
     for (int64_t u = u0; u < units; u += n_subs) {
         if (u < n_words) {
-            const int d = static_cast<int>(u / BW) + 1;
-            const int64_t rem = u - static_cast<int64_t>(d - 1) * BW;
+            const int d = static_cast<int>(u / BW) + a.d_lo;
+            const int64_t rem = u - static_cast<int64_t>(d - a.d_lo) * BW;
             const int b = static_cast<int>(rem / a.W);
             const int wi = static_cast<int>(rem - static_cast<int64_t>(b) * a.W);
             uint64_t word = a.zbits[(static_cast<int64_t>(a.t - d + a.D) * a.B + b) * a.W + wi];
@@ -292,6 +293,8 @@ __global__ void __launch_bounds__(kBlock) k_push(PushArgs a) {
         }
     }
 }
+
+__global__ void __launch_bounds__(kBlock) k_push(PushArgs a) { push_body(a, blockIdx.x, gridDim.x); }
 
 // ------------------------------------------------------------- GLIF step ----
 struct StepArgs {
@@ -343,17 +346,16 @@ struct StepArgs {
 //   r'     = max(r + z_prev * tref - 1, 0); hard reset: V' = 0 while r' > 0
 //   z      = r' > 0 ? 0 : (V' - 1 > 0)
 template <bool DET, int NB>
-__global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
+__device__ inline void step_body(const StepArgs &a, int64_t bid) {
     extern __shared__ float basis_lds[];
     const CellConst &k = a.k;
     load_basis_lds(basis_lds, a.basis, k.n_types * k.nb);
-    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t gt = bid * blockDim.x + threadIdx.x;
     if (gt >= static_cast<int64_t>(k.B) * k.Np) return;  // whole waves only (Np % 64 == 0)
     // wave w: batch entry w % B of neurons 64 (w / B) ..: the B waves of a neuron block run
     // back to back and share its background table entries in cache
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t wv =
-        static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int64_t wv = bid * (blockDim.x / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int b = static_cast<int>(wv % k.B);
     const int n = static_cast<int>(wv / k.B) * kWave + lane;
     constexpr int nb = NB;
@@ -466,6 +468,24 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
         a.refbits[static_cast<int64_t>(t) * k.B * k.W + word] = rb;
         if (DET && zb) atomicOr(a.abits + static_cast<int64_t>(t + k.D) * k.W + (n >> 6), zb);
     }
+}
+
+template <bool DET, int NB>
+__global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
+    step_body<DET, NB>(a, blockIdx.x);
+}
+
+// Event mode: the step of tick t - 1 (blocks [0, step_blocks)) with the push of tick t's
+// events that do not depend on it (delay slots >= 2 and the LGN inputs; the rest of the
+// blocks) into the other current buffer: the step streams state through HBM while the push
+// is bound by atomics, and one launch overlaps them.
+template <int NB>
+__global__ void __launch_bounds__(kBlock) k_step_push(StepArgs sa, int step_blocks, PushArgs pa) {
+    const int64_t bid = blockIdx.x;
+    if (bid < step_blocks)
+        step_body<false, NB>(sa, bid);
+    else
+        push_body(pa, bid - step_blocks, gridDim.x - step_blocks);
 }
 
 // ------------------------------------------------- voltage regularization ----
@@ -951,6 +971,19 @@ static void launch_bwd_in(const BwdInArgs &ia, int64_t max_units, hipStream_t s)
         hipLaunchKernelGGL(k_bwd_in<false>, grid, dim3(kBlock), 0, s, ia);
 }
 
+static void launch_step_push(const StepArgs &sa, int step_blocks, const PushArgs &pa, int push_blocks, int nb,
+                             size_t lds, hipStream_t s) {
+    const dim3 grid(step_blocks + push_blocks);
+    switch (nb) {
+#define GLIF_STEP_PUSH(NB) \
+    case NB: hipLaunchKernelGGL((k_step_push<NB>), grid, dim3(kBlock), lds, s, sa, step_blocks, pa); break;
+        GLIF_STEP_PUSH(1) GLIF_STEP_PUSH(2) GLIF_STEP_PUSH(3) GLIF_STEP_PUSH(4) GLIF_STEP_PUSH(5)
+        GLIF_STEP_PUSH(6) GLIF_STEP_PUSH(7) GLIF_STEP_PUSH(8)
+#undef GLIF_STEP_PUSH
+        default: break;
+    }
+}
+
 template <bool DET>
 static void launch_step(const StepArgs &sa, int nb, dim3 grid, size_t lds, hipStream_t s) {
     switch (nb) {
@@ -1120,7 +1153,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                        w.zbits, event ? nullptr : w.zmask,
                        event ? nullptr : w.abits);
     GLIF_HIP(hipGetLastError());
-    if (event && (rc = launch_fill_u32(w.I, 0u, static_cast<size_t>(B) * c->N * c->nb, s))) return rc;
+    if (event && (rc = launch_fill_u32(w.I, 0u, 2 * static_cast<size_t>(B) * c->N * c->nb, s))) return rc;
     const int64_t BNs = static_cast<int64_t>(B) * c->N;
     hipLaunchKernelGGL(k_state_layout, dim3(ceil_div(BNs, kBlock)), dim3(kBlock), 0, s, st->psc_rise, st->psc,
                        st->asc, w.R, w.P, w.A, BNs, c->nb, 1);
@@ -1175,6 +1208,9 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     pa.nb = c->nb;
     pa.n_types = c->n_types;
     pa.chunks_lgn = chunks_for(tl, kWave);
+    pa.d_lo = 1;
+    pa.d_hi = c->D;
+    pa.lgn = 1;
     pa.zbits = w.zbits;
     pa.W = c->W;
     pa.rec_colptr = tr->col_ptr;
@@ -1237,18 +1273,44 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         }
     }
 
+    // Event mode: tick t's currents accumulate in half t % 2 of I.  One launch runs the step
+    // of tick t - 1 with the push of tick t's delay-2..D and LGN events (which do not depend
+    // on it); the delay-1 events, spikes of tick t - 1, follow in a launch of their own.
+    float *Ih[2] = {w.I, w.I + static_cast<size_t>(B) * c->N * c->nb};
+    auto step_args = [&](int t) {
+        StepArgs x = sa;
+        x.t = t;
+        x.I = Ih[t & 1];
+        x.lgn_x = lgn + static_cast<int64_t>(t) * B * tl->n_cols;
+        x.bkg_x = bkg + static_cast<int64_t>(t) * B * tb->n_cols;
+        return x;
+    };
     for (int t = 0; t < T; ++t) {
         sa.t = t;
         sa.lgn_x = lgn + static_cast<int64_t>(t) * B * tl->n_cols;
         sa.bkg_x = bkg + static_cast<int64_t>(t) * B * tb->n_cols;
         if (event) {
-            pa.t = t;
+            PushArgs early = pa, late = pa;
+            early.t = late.t = t;
+            early.I = late.I = Ih[t & 1];
+            early.d_lo = 2;   // d_hi = D; nothing recurrent when D = 1
+            late.d_lo = late.d_hi = 1;
+            late.lgn = 0;
+            if (t == 0) {
+                ProfScope p(kProfPush, s);
+                hipLaunchKernelGGL(k_push, dim3(push_grid), dim3(kBlock), lds, s, early);
+            } else {
+                ProfScope p(kProfStep, s);
+                launch_step_push(step_args(t - 1), static_cast<int>(step_grid.x), early, push_grid, c->nb, lds, s);
+            }
             {
                 ProfScope p(kProfPush, s);
-                hipLaunchKernelGGL(k_push, dim3(push_grid), dim3(kBlock), lds, s, pa);
+                hipLaunchKernelGGL(k_push, dim3(push_grid), dim3(kBlock), lds, s, late);
             }
-            ProfScope p(kProfStep, s);
-            launch_step<false>(sa, c->nb, step_grid, lds, s);
+            if (t == T - 1) {
+                ProfScope p(kProfStep, s);
+                launch_step<false>(step_args(t), c->nb, step_grid, lds, s);
+            }
         } else {
             pl.t = t;
             {
