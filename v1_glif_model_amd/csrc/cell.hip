@@ -1224,7 +1224,9 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     pa.lgn_w = tl->w_col;
     pa.basis = tr->basis;
     pa.I = w.I;
-    const int push_grid = 2048;
+    // Push grids (blocks of 256 that stride over the events): 2048 where a push runs alone,
+    // 1024 beside the step in the fused launch, which fills the rest of the chip.
+    const int push_grid = 2048, fused_push_grid = 1024;
     const dim3 step_grid(ceil_div(static_cast<int64_t>(B) * c->Np, kBlock));
 
     PullArgs pl{};
@@ -1301,7 +1303,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                 hipLaunchKernelGGL(k_push, dim3(push_grid), dim3(kBlock), lds, s, early);
             } else {
                 ProfScope p(kProfStep, s);
-                launch_step_push(step_args(t - 1), static_cast<int>(step_grid.x), early, push_grid, c->nb, lds, s);
+                launch_step_push(step_args(t - 1), static_cast<int>(step_grid.x), early, fused_push_grid, c->nb, lds, s);
             }
             {
                 ProfScope p(kProfPush, s);
