@@ -336,6 +336,12 @@ struct StepArgs {
     const uint8_t *bkg_x;  // [B][n_bkg] of step t
     int32_t n_bkg;
     const float *basis;
+    // event mode: each wave pushes the delay-1 columns of its spikes into the next tick's
+    // currents (nullptr: no push)
+    float *I_next;
+    const int32_t *p1_colptr;
+    const uint32_t *p1_ps;
+    const float *p1_w;
 };
 
 // One GLIF_3 update per thread (b, n), models.py:979-1028 and 1059-1135:
@@ -468,6 +474,20 @@ __device__ inline void step_body(const StepArgs &a, int64_t bid) {
         a.refbits[static_cast<int64_t>(t) * k.B * k.W + word] = rb;
         if (DET && zb) atomicOr(a.abits + static_cast<int64_t>(t + k.D) * k.W + (n >> 6), zb);
     }
+    if (!DET && a.I_next) {
+        // the wave's spikes (a wave-uniform word) reach their delay-1 posts at tick t + 1:
+        // column pre + 0 * N of the recurrent table, all 64 lanes over its synapses
+        const int64_t BN = static_cast<int64_t>(k.B) * k.N;
+        const int32_t n0 = n & ~(kWave - 1);
+        uint64_t zw = zb;
+        while (zw) {
+            const int bit = __builtin_ctzll(zw);
+            zw &= zw - 1ull;
+            const int32_t col = n0 + bit;
+            push_column<kWave>(lane, a.p1_colptr[col], a.p1_colptr[col + 1], 1u << b, MultOne{}, a.p1_ps, a.p1_w,
+                               basis_lds, nb, k.N, 1, BN, a.I_next);
+        }
+    }
 }
 
 template <bool DET, int NB>
@@ -475,10 +495,11 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
     step_body<DET, NB>(a, blockIdx.x);
 }
 
-// Event mode: the step of tick t - 1 (blocks [0, step_blocks)) with the push of tick t's
-// events that do not depend on it (delay slots >= 2 and the LGN inputs; the rest of the
-// blocks) into the other current buffer: the step streams state through HBM while the push
-// is bound by atomics, and one launch overlaps them.
+// Event mode: the step of tick t - 1 (blocks [0, step_blocks); each wave also pushes its
+// spikes' delay-1 events) with the push of tick t's events that do not depend on it (delay
+// slots >= 2 and the LGN inputs; the rest of the blocks), all into tick t's current buffer:
+// the step streams state through HBM while the push is bound by atomics, and one launch
+// overlaps them.
 template <int NB>
 __global__ void __launch_bounds__(kBlock) k_step_push(StepArgs sa, int step_blocks, PushArgs pa) {
     const int64_t bid = blockIdx.x;
@@ -1275,9 +1296,9 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         }
     }
 
-    // Event mode: tick t's currents accumulate in half t % 2 of I.  One launch runs the step
-    // of tick t - 1 with the push of tick t's delay-2..D and LGN events (which do not depend
-    // on it); the delay-1 events, spikes of tick t - 1, follow in a launch of their own.
+    // Event mode: tick t's currents accumulate in half t % 2 of I.  One launch per tick runs
+    // the step of tick t - 1, whose waves push their spikes' delay-1 events, with the push of
+    // tick t's delay-2..D and LGN events (which do not depend on it).
     float *Ih[2] = {w.I, w.I + static_cast<size_t>(B) * c->N * c->nb};
     auto step_args = [&](int t) {
         StepArgs x = sa;
@@ -1292,22 +1313,22 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         sa.lgn_x = lgn + static_cast<int64_t>(t) * B * tl->n_cols;
         sa.bkg_x = bkg + static_cast<int64_t>(t) * B * tb->n_cols;
         if (event) {
-            PushArgs early = pa, late = pa;
-            early.t = late.t = t;
-            early.I = late.I = Ih[t & 1];
-            early.d_lo = 2;   // d_hi = D; nothing recurrent when D = 1
-            late.d_lo = late.d_hi = 1;
-            late.lgn = 0;
+            PushArgs early = pa;
+            early.t = t;
+            early.I = Ih[t & 1];
             if (t == 0) {
+                // tick 0: every delay slot (the initial history) and the LGN inputs
                 ProfScope p(kProfPush, s);
                 hipLaunchKernelGGL(k_push, dim3(push_grid), dim3(kBlock), lds, s, early);
             } else {
+                early.d_lo = 2;   // d_hi = D; nothing recurrent when D = 1
+                StepArgs x = step_args(t - 1);
+                x.I_next = Ih[t & 1];
+                x.p1_colptr = tr->col_ptr;
+                x.p1_ps = tr->ps;
+                x.p1_w = tr->w_col;
                 ProfScope p(kProfStep, s);
-                launch_step_push(step_args(t - 1), static_cast<int>(step_grid.x), early, fused_push_grid, c->nb, lds, s);
-            }
-            {
-                ProfScope p(kProfPush, s);
-                hipLaunchKernelGGL(k_push, dim3(push_grid), dim3(kBlock), lds, s, late);
+                launch_step_push(x, static_cast<int>(step_grid.x), early, fused_push_grid, c->nb, lds, s);
             }
             if (t == T - 1) {
                 ProfScope p(kProfStep, s);
