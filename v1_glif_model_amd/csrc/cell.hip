@@ -259,7 +259,7 @@ __device__ inline void push_body(const PushArgs &a, int64_t bid, int64_t nblk) {
     extern __shared__ float basis_lds[];
     load_basis_lds(basis_lds, a.basis, a.n_types * a.nb);
     const int64_t BW = static_cast<int64_t>(a.B) * a.W;
-    const int64_t n_words = static_cast<int64_t>(a.d_hi - a.d_lo + 1) * BW;
+    const int64_t n_words = a.d_hi >= a.d_lo ? static_cast<int64_t>(a.d_hi - a.d_lo + 1) * BW : 0;
     const int64_t l0 = a.lgn_off[a.t], n_lgn = a.lgn ? a.lgn_off[a.t + 1] - l0 : 0;
     const int64_t units = n_words + n_lgn * a.chunks_lgn;
     const int lane_s = threadIdx.x % L;
