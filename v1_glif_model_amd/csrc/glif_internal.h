@@ -83,6 +83,7 @@ struct Table {
     uint2 *ph_pw = nullptr;       // [n_syn]       {post, weight bits}
     int32_t *order_inv = nullptr; // [n_syn]       position of synapse s in the column-grouped order
     int32_t *ph_inv = nullptr;    // [n_syn]       position of synapse s in the type-phased order
+    int32_t *ph_src = nullptr;    // [n_syn]       column-grouped position of type-phased position k
     // grouped row-sliced order (backward dz walks over 8- and 16-float G rows): lane group g owns
     // columns kGsCols*g ..; its entries in G-row slice p (rows syn_id * n_post + post, slice p
     // = rows [n_rows * p / kGsSlices, n_rows * (p + 1) / kGsSlices)) are positions
@@ -93,7 +94,7 @@ struct Table {
     int64_t n_groups = 0;
     int32_t *gs_seg = nullptr;    // [n_groups * (kGsSlices + 1)]
     uint2 *gs_pw = nullptr;       // [n_gs]        {row | column-in-group << kGsRowBits, weight bits}
-    int32_t *gs_src = nullptr;    // [n_gs]        synapse id, -1 for padding
+    int32_t *gs_src = nullptr;    // [n_gs]        column-grouped position of the synapse, -1 for padding
     float *basis_host = nullptr;  // host copy [n_types][n_basis]
 };
 

@@ -98,7 +98,7 @@ static void free_table(Table *t) {
     if (!t) return;
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
                     t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
-                    t->chunk_desc, t->pidx, t->order_inv, t->ph_inv, t->gs_seg, t->gs_pw, t->gs_src};
+                    t->chunk_desc, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete[] t->basis_host;
@@ -184,11 +184,15 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
 
     // inverse permutations: position of synapse s in the column-grouped and type-phased
     // orders (gradients go back to reference order with coalesced writes)
-    std::vector<int32_t> order_inv(n_syn), ph_inv(n_syn);
+    std::vector<int32_t> order_inv(n_syn), ph_inv(n_syn), ph_src(n_syn);
     for (int64_t k = 0; k < n_syn; ++k) {
         order_inv[order[k]] = static_cast<int32_t>(k);
         ph_inv[ph_order[k]] = static_cast<int32_t>(k);
     }
+    // the weight copies other than w_col are gathered from w_col, whose order is close to
+    // theirs (the type-phased order sweeps it once per type; a group's grouped entries come
+    // from its own columns), rather than from the reference order
+    for (int64_t k = 0; k < n_syn; ++k) ph_src[k] = order_inv[ph_order[k]];
     // grouped row-sliced order (backward dz walks): a stable counting sort by (G row,
     // column in group), then by (group, row slice); each (group, slice) segment is padded to
     // a multiple of kGsPad with copies of its last row marked as column 7 (weight +0.0f)
@@ -225,7 +229,7 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
                         const int32_t sidx = ord2[r];
                         last = static_cast<uint32_t>(static_cast<int64_t>(syn_id[sidx]) * n_post + post[sidx]);
                         gs_pw[pos] = make_uint2(last | static_cast<uint32_t>(col[sidx] % kGsCols) << kGsRowBits, 0u);
-                        gs_src[pos] = sidx;
+                        gs_src[pos] = order_inv[sidx];
                     }
                     for (; pos % kGsPad; ++pos) {
                         gs_pw[pos] = make_uint2(last | 7u << kGsRowBits, 0u);
@@ -320,6 +324,7 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         (rc = upload(&t->ph_order, ph_order.data(), ph_order.size())) ||
         (rc = upload(&t->order_inv, order_inv.data(), order_inv.size())) ||
         (rc = upload(&t->ph_inv, ph_inv.data(), ph_inv.size())) ||
+        (rc = upload(&t->ph_src, ph_src.data(), ph_src.size())) ||
         (rc = upload(&t->ph_pw, ph_pw.data(), ph_pw.size())) ||
         (ell_len && (rc = upload(&t->ell_pw, ell_pw.data(), ell_pw.size()))) ||
         (ell_len && (rc = upload(&t->ell_src, ell_src.data(), ell_src.size()))) ||
@@ -361,14 +366,15 @@ int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = launch_gather_f32(t->w_col, w, t->order, t->n_syn, s);
     if (rc) return rc;
+    // the type-phased and grouped copies from w_col (near-sequential reads)
     if (t->n_syn) {
-        hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(t->n_syn)), dim3(kBlock), 0, s, t->ph_pw, w,
-                           t->ph_order, t->n_syn);
+        hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(t->n_syn)), dim3(kBlock), 0, s, t->ph_pw, t->w_col,
+                           t->ph_src, t->n_syn);
         GLIF_HIP(hipGetLastError());
     }
     if (t->n_gs) {
-        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(t->n_gs)), dim3(kBlock), 0, s, t->gs_pw, w, t->gs_src,
-                           t->n_gs);
+        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(t->n_gs)), dim3(kBlock), 0, s, t->gs_pw, t->w_col,
+                           t->gs_src, t->n_gs);
         GLIF_HIP(hipGetLastError());
     }
     if (t->ell_len) {
