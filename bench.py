@@ -431,6 +431,12 @@ def main():
                 "traffic": traffic.get("bytes_per_launch") if traffic else None,
                 "algorithmic_bytes_per_launch": int(alg_bytes), "basis": unit_desc,
                 "avg_launch_us": round(avg_ms * 1000.0, 2), "launches_timed": launches}
+    if traffic and avg_ms > 0:
+        # the measured L2 <-> memory-fabric bytes (FETCH_SIZE + WRITE_SIZE: HBM and
+        # Infinity Cache) over the same live launch time
+        tg = traffic["bytes_per_launch"] / (avg_ms / 1000.0) / 1e9
+        roofline["traffic_gbs"] = round(tg, 1)
+        roofline["traffic_frac"] = round(tg / HBM_PEAK_GBS, 4)
 
     # CPU baseline: the C restatement on a bounded prefix of the same workload, timed with
     # one thread and with the host's cores (its OpenMP loops keep every sum's order, so both
