@@ -195,9 +195,11 @@ def sweep_rates(args):
                      "event_ms_per_step": round(ev_ms, 4), "pull_ms_per_step": round(pl_ms, 4),
                      "event_kernel_us_per_step": ev_k, "pull_kernel_us_per_step": pl_k,
                      "rec_events_per_step": round(events),
-                     # push bytes: 8-byte entry + one 4-byte atomic per event; pull: every
-                     # post-row entry (4 bytes) + the active entries' weight and type (5)
-                     "event_push_GBps": round(events * 12 / (ev_k.get("push", 1e9) * 1e-6) / 1e9, 1),
+                     # push bytes: 8-byte entry + one 4-byte atomic per event, over the whole
+                     # event forward's kernel time (the pushes run inside the step launch);
+                     # pull: every post-row entry (4 bytes) + the active entries' weight and
+                     # type (5), over the pull kernel's time
+                     "event_push_GBps": round(events * 12 / (sum(ev_k.values()) * 1e-6) / 1e9, 1),
                      "pull_GBps": round((S * 4 + events * 5) / (pl_k.get("push", 1e9) * 1e-6) / 1e9, 1)})
         print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
     best5 = min((r for r in rows), key=lambda r: abs(r["target_hz"] - 5.0)) if rows else None
