@@ -363,7 +363,12 @@ def main():
         step()
     torch.cuda.synchronize()
     sc_host = spike_count.cpu().numpy()
-    dominant = "push" if args.forward_only else "bwd_rec"
+    if not args.forward_only:
+        dominant = "bwd_rec"
+    else:
+        # event mode: one fused launch per tick (the step of t - 1 beside the pushes), timed
+        # as "step"; deterministic mode: the row pull, timed as "push"
+        dominant = "push" if args.mode == "deterministic" else "step"
     _lib.prof_enable([dominant])
     _lib.prof_collect()
     fwd_ms = bwd_ms = 0.0
@@ -419,12 +424,22 @@ def main():
             alg_bytes = (S * 8 + (nt * D * N + 1) * 4 + steps_per_launch * B * D * N * 4 + N * nt * Rg * 4
                          + (steps_per_launch + D) * B * words * 8 + active * 8)
             unit_desc = f"bytes per backward window of {Wwin} timesteps (recurrent dz + dW)"
-    else:
-        # per launch = one timestep's pushed events: the 8-byte table entry (post |
-        # syn_id, weight) and one 4-byte fp32 atomic each (identity basis)
+    elif dominant == "step":
+        # per launch = one tick: the GLIF_3 step's state stream per (b, n) -- reads I, R, P
+        # (nb floats each), A (2 floats), v, r (int16); writes I (cleared), R, P, A, v, r and
+        # the saved voltage -- the per-neuron constants (7 floats), the background rows (8 bytes
+        # per synapse), and the tick's pushed events (8-byte entry + one 4-byte atomic each)
         active = (e_rec + e_lgn) / max(T, 1)
-        alg_bytes = active * 12
-        unit_desc = "bytes per forward timestep"
+        per_bn = (3 * nb * 4 + 14) + (3 * nb * 4 + 18)
+        alg_bytes = B * N * per_bn + N * 28 + tb.bkg.n_syn * 8 + active * 12
+        unit_desc = "bytes per forward timestep (GLIF_3 step + the tick's pushed events)"
+    else:
+        # per launch = one timestep's row pull: every recurrent and LGN entry's bitmap index
+        # (4 bytes), the row pointers, each active entry's batch mask, weight and type (9
+        # bytes), and the currents written (rec and LGN halves)
+        active = (e_rec + e_lgn) / max(T, 1)
+        alg_bytes = ((S + tb.lgn.n_syn) * 4 + 2 * (N + 1) * 4 + active * 9 + 2 * nb * B * N * 4)
+        unit_desc = "bytes per forward timestep (deterministic row pull)"
     avg_ms = tot_ms / max(launches, 1)
     achieved = alg_bytes / (avg_ms / 1000.0) / 1e9 if avg_ms > 0 else 0.0
     traffic = load_traffic(dominant)
