@@ -83,26 +83,36 @@ def test_event_forward_matches_config0():
     assert agree >= 0.999
 
 
-@pytest.mark.parametrize("D", [1, 3, 5])
-def test_event_forward_delays_and_split_rollout(D):
+@pytest.mark.parametrize("D,B", [(1, 3), (3, 3), (5, 3), (5, 20)])
+def test_event_forward_delays_and_split_rollout(D, B):
     """Event mode over max delays 1, 3 and 5 (with D = 1 the push beside the step has no
-    recurrent delay slots; the step's waves push every recurrent event) and a rollout split
-    in two, whose second part starts with spikes in the carried history that its tick 0
-    pushes.  Spike trains equal the oracle's; voltages within 1e-4 (the event sums differ
-    from the oracle's order by rounding only)."""
+    recurrent delay slots; the step's waves push every recurrent event), batch 3 and 20, and
+    a rollout split in two, whose second part starts with spikes in the carried history that
+    its tick 0 pushes.  Spike trains equal the oracle's; voltages within 1e-4 (the event sums
+    differ from the oracle's order by rounding only); the BPTT after the one-piece event
+    rollout (the training path) within 1e-5 of the oracle's."""
     cfg = tiny_config(rs=2.0, ins=3.0, delays=D)
     tn = network(cfg, seed=8, dense_basis=True)
-    T, B, T1 = 50, 3, 33
+    T, T1 = 50, 33
     lgn, bkg = _inputs(cfg, T, B, seed=9)
-    oz, ov, _, _ = _oracle(tn[1], **ORC_KW).forward(lgn, bkg)
+    oc = _oracle(tn[1], **ORC_KW)
+    oz, ov, oref, _ = oc.forward(lgn, bkg)
     assert oz[T1 - D:T1].sum() > 0   # the split point carries spikes in its history
     cell = _cell(tn, "event", **CELL_KW)
-    z, v, _ = cell.rollout(lgn, bkg)
     z1, v1, state = cell.rollout(lgn[:T1], bkg[:T1], state=cell.zero_state(B))
     z2, v2, _ = cell.rollout(lgn[T1:], bkg[T1:], state=state)
+    z, v, _ = cell.rollout(lgn, bkg)
     for zz, vv in ((z, v), (torch.cat([z1, z2]), torch.cat([v1, v2]))):
         np.testing.assert_array_equal(zz.cpu().numpy().astype(np.uint8), oz)
         assert np.max(np.abs(vv.cpu().numpy() - ov)) <= 1e-4
+    gz = np.random.default_rng(D * 10 + B).normal(0, 1, oz.shape).astype(np.float32)
+    g = cell.backward(gz=torch.tensor(gz, device="cuda"))
+    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz)
+    for k in ("rec", "lgn", "bkg"):
+        a, e = g[k].cpu().numpy(), og[k]
+        scale = np.max(np.abs(e))
+        assert scale > 0, k
+        assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
 
 
 @pytest.mark.parametrize("pseudo_gauss,hard_reset", [(True, False), (False, False), (True, True)])
