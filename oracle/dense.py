@@ -44,12 +44,16 @@ def syn_fwd_f64(table, z, basis, use_count=False, absolute=False):
     B = mult.shape[0]
     N, nb = table.n_post, basis.shape[1]
     w = table.weight.astype(np.float64)
-    terms = (mult * w[None, :])[:, :, None] * basis[table.syn_id][None, :, :]   # [B, S, nb]
-    if absolute:
-        terms = np.abs(terms)
     I = np.zeros((B, N, nb))
     for b in range(B):
-        np.add.at(I[b], table.post, terms[b])
+        # bincount adds each bin's terms in input order, as a scatter-add would; zero terms
+        # (inactive columns) are left out, which does not change a float64 sum
+        on = mult[b] != 0
+        terms = (mult[b][on] * w[on])[:, None] * basis[table.syn_id[on]]   # [active, nb]
+        if absolute:
+            terms = np.abs(terms)
+        for r in range(nb):
+            I[b, :, r] = np.bincount(table.post[on], weights=terms[:, r], minlength=N)
     return I.reshape(B * N, nb)
 
 
@@ -73,8 +77,9 @@ def syn_bwd_f64(table, z, basis, dy, use_count=False):
     for b in range(B):
         prod = dy[b][table.post] * bs                 # [S, nb]
         g = prod.sum(1)
-        np.add.at(dz[b], table.col, w * g)
-        np.add.at(dz_abs[b], table.col, np.abs(w[:, None] * prod).sum(1))
+        pa = np.abs(prod).sum(1)
+        dz[b] = np.bincount(table.col, weights=w * g, minlength=table.n_cols)
+        dz_abs[b] = np.bincount(table.col, weights=np.abs(w) * pa, minlength=table.n_cols)
         dW += mult[b] * g
-        dW_abs += np.abs(mult[b])[:, None].ravel() * np.abs(prod).sum(1)
+        dW_abs += np.abs(mult[b]) * pa
     return dz, dW, dz_abs, dW_abs

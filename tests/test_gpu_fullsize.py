@@ -83,3 +83,36 @@ def test_config2_bptt(config2):
         print(k, "max|dW|", scale, "max err", err, "nonzero", int(np.count_nonzero(e)), flush=True)
         assert scale > 0, k
         assert err <= 1e-5 * scale + 1e-6, k
+
+
+def test_config2_op_level(config2):
+    """calculate_synaptic_currents on the full config-2 recurrent table (models.py:103-263):
+    z_buf [5][D*N] at 5 Hz, dy [5*N][nb] normal.  Deterministic forward bit-exact with the
+    oracle; event forward, dz and dW within 1e-5 of the float64 brute force's sum of absolute
+    terms (+1e-6)."""
+    from oracle import dense
+    from v1_glif_model_amd.ops import SynapseTable
+    cfg, net, tb = config2
+    N, D, B, nb = tb.n_neurons, tb.max_delay, 5, tb.n_basis
+    t = SynapseTable(np.stack([tb.rec.post, tb.rec.col], -1), tb.rec.syn_id, (N, tb.rec.n_cols), tb.basis,
+                     n_delay_slots=D)
+    t.set_weights(torch.tensor(tb.rec.weight, device="cuda"))
+    rng = np.random.default_rng(3)
+    z = (rng.uniform(size=(B, D * N)) < 0.005).astype(np.float32)
+    dy = rng.normal(0, 1, (B * N, nb)).astype(np.float32)
+    zt, dyt = torch.tensor(z, device="cuda"), torch.tensor(dy, device="cuda")
+    det = t.forward(zt, mode="deterministic").cpu().numpy()
+    ev = t.forward(zt, mode="event").cpu().numpy()
+    dz, dw = t.backward(zt, dyt)
+    dz, dw = dz.cpu().numpy(), dw.cpu().numpy()
+    ref = orc.syn_fwd(tb.rec, z, tb.basis)
+    np.testing.assert_array_equal(det.view(np.uint32), ref.view(np.uint32))
+    scale = dense.syn_fwd_abs(tb.rec, z, tb.basis)
+    assert np.max(np.abs(ev - ref) - 1e-5 * scale) <= 1e-6
+    rdz, rdw = orc.syn_bwd(tb.rec, z, tb.basis, dy)
+    _, _, dz_abs, dw_abs = dense.syn_bwd_f64(tb.rec, z, tb.basis, dy)
+    print("events", int(np.count_nonzero(z)), "max |dz|", float(np.abs(rdz).max()),
+          "nonzero dW", int(np.count_nonzero(rdw)), flush=True)
+    assert np.count_nonzero(rdw) > 0
+    assert np.max(np.abs(dz - rdz) - 1e-5 * dz_abs) <= 1e-6
+    assert np.max(np.abs(dw - rdw) - 1e-5 * dw_abs) <= 1e-6
