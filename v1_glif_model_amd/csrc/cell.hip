@@ -495,18 +495,22 @@ __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
     step_body<DET, NB>(a, blockIdx.x);
 }
 
-// Event mode: the step of tick t - 1 (blocks [0, step_blocks); each wave also pushes its
-// spikes' delay-1 events) with the push of tick t's events that do not depend on it (delay
-// slots >= 2 and the LGN inputs; the rest of the blocks), all into tick t's current buffer:
+// Event mode: the push of tick t's events that do not depend on the step of tick t - 1
+// (delay slots >= 2 and the LGN inputs; the first gridDim.x - step_blocks blocks) with that
+// step (the last step_blocks blocks; each wave also pushes its spikes' delay-1 events), all
+// into tick t's current buffer:
 // the step streams state through HBM while the push is bound by atomics, and one launch
 // overlaps them.
 template <int NB>
 __global__ void __launch_bounds__(kBlock) k_step_push(StepArgs sa, int step_blocks, PushArgs pa) {
+    // the push blocks come first, so the atomic-bound push (the longer part) starts at once
+    // and the step blocks fill the machine behind it
     const int64_t bid = blockIdx.x;
-    if (bid < step_blocks)
-        step_body<false, NB>(sa, bid);
+    const int64_t push_blocks = gridDim.x - step_blocks;
+    if (bid < push_blocks)
+        push_body(pa, bid, push_blocks);
     else
-        push_body(pa, bid - step_blocks, gridDim.x - step_blocks);
+        step_body<false, NB>(sa, bid - push_blocks);
 }
 
 // ------------------------------------------------- voltage regularization ----
