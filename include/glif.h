@@ -244,7 +244,10 @@ int glif_sample_poisson(float lam, float exp_neg_lam, int64_t n, uint64_t seed, 
 /* ------------------------------------------------------------ profiling ------
  * No reference counterpart (the reference times whole steps with time(),
  * callbacks.py:1442-1449).  Kernel classes: 0 push, 1 step, 2 adj, 3 bwd_rec,
- * 4 bwd_lgn, 5 bwd_bkg, 6 syn_fwd, 7 syn_bwd.  While bit k of `mask` is set, every
+ * 4 bwd_lgn, 5 bwd_bkg, 6 syn_fwd, 7 syn_bwd.  In the cell's event mode "step" is the
+ * one launch per tick that runs the step beside that tick's pushes and "push" only the
+ * push of tick 0; in deterministic mode "push" is the row pull.  "adj" includes the
+ * previous window's weight-gradient passes that share its launch.  While bit k of `mask` is set, every
  * launch of class k is bracketed by two HIP events on its stream.
  * glif_prof_collect waits for the recorded events and returns, per class, the
  * summed elapsed milliseconds and the number of launches since the last collect. */
