@@ -52,7 +52,7 @@ def lib():
             L.orc_set_threads.restype = C.c_int
             L.orc_set_threads.argtypes = [C.c_int]
             L.orc_backward.restype = C.c_int
-            L.orc_backward.argtypes = [C.POINTER(OrcCell), C.c_int, C.c_int, u8p, u8p, u8p, u8p,
+            L.orc_backward.argtypes = [C.POINTER(OrcCell), C.c_int, C.c_int, u8p, u8p, f32p, u8p, u8p,
                                        f32p, f32p, f32p, f32p, f32p, f32p, f32p, f32p]
             _lib = L
     return _lib
@@ -229,7 +229,10 @@ class OracleCell:
         return z, v, ref, st
 
     def backward(self, lgn, bkg, z, ref, v, gz_loss=None, gz_neuron=None, gv_loss=None,
-                 want=("rec", "lgn", "bkg"), want_gz=False):
+                 want=("rec", "lgn", "bkg"), want_gz=False, zbuf0=None):
+        """BPTT of a forward with outputs z, ref, v (and initial spike history zbuf0
+        [B, D*N], None for zero); returns the weight gradients {rec, lgn, bkg}."""
+        zb0 = None if zbuf0 is None else np.ascontiguousarray(zbuf0, np.float32)
         lgn = np.ascontiguousarray(lgn, np.uint8)
         bkg = np.ascontiguousarray(bkg, np.uint8)
         T, B = lgn.shape[:2]
@@ -242,7 +245,9 @@ class OracleCell:
         dW = {k: (np.zeros(getattr(self, k).post.size, np.float32) if k in want else None)
               for k in ("rec", "lgn", "bkg")}
         gz_out = np.zeros((T, B, self.N), np.float32) if want_gz else None
-        rc = lib().orc_backward(C.byref(self.c), T, B, _p(lgn, u8p), _p(bkg, u8p), _p(z, u8p),
+        if zb0 is not None and zb0.shape != (B, self.D * self.N):
+            raise OracleError("zbuf0 must be [B, D*N]")
+        rc = lib().orc_backward(C.byref(self.c), T, B, _p(lgn, u8p), _p(bkg, u8p), _p(zb0, f32p), _p(z, u8p),
                                 _p(ref, u8p), _p(v, f32p), _p(gzl, f32p), _p(gzn, f32p),
                                 _p(gvl, f32p), _p(dW["rec"], f32p), _p(dW["lgn"], f32p),
                                 _p(dW["bkg"], f32p), _p(gz_out, f32p))
@@ -251,3 +256,28 @@ class OracleCell:
         if want_gz:
             return dW, gz_out
         return dW
+
+
+def abs_tables(tables):
+    """The cell tables with every weight and basis entry replaced by its absolute value."""
+    import dataclasses
+    tb = tables
+    return dataclasses.replace(
+        tb, basis=np.abs(np.asarray(tb.basis, np.float32)),
+        rec=dataclasses.replace(tb.rec, weight=np.abs(tb.rec.weight)),
+        lgn=dataclasses.replace(tb.lgn, weight=np.abs(tb.lgn.weight)),
+        bkg=dataclasses.replace(tb.bkg, weight=np.abs(tb.bkg.weight)))
+
+
+def bptt_abs_scale(tables, lgn, bkg, z, ref, v, gz_loss=None, gz_neuron=None, gv_loss=None,
+                   want=("rec", "lgn", "bkg"), zbuf0=None, **cell_kw):
+    """Per-element scale of the BPTT weight gradients: the same reverse pass with every
+    signed factor (weights, basis entries, loss gradients) replaced by its absolute value.
+    Every other factor of the adjoint (surrogate, decays, current factors, PSC constants,
+    dampening scales) is non-negative, so each output is the sum of the absolute values of
+    all the terms that make up that gradient element -- the quantity fp32 rounding errors of
+    any summation order are proportional to."""
+    ab = lambda a: None if a is None else np.abs(np.asarray(a, np.float32))
+    oc = OracleCell(abs_tables(tables), **cell_kw)
+    return oc.backward(lgn, bkg, z, ref, v, gz_loss=ab(gz_loss), gz_neuron=ab(gz_neuron),
+                       gv_loss=ab(gv_loss), want=want, zbuf0=zbuf0)

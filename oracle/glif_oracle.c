@@ -280,14 +280,16 @@ int orc_forward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint8
 }
 
 /* BPTT through orc_forward.  Saved forward data: z [T][B][N], ref (r_t > 0)
- * [T][B][N] uint8, v [T][B][N] float (all from orc_forward with zero initial
- * state), inputs lgn/bkg as in orc_forward.
+ * [T][B][N] uint8, v [T][B][N] float (all from orc_forward), inputs lgn/bkg as in
+ * orc_forward; zbuf0 [B][D*N] the forward's initial spike history (slot d-1 = z_{-d}),
+ * whose spikes feed the recurrent dW of the first D steps (NULL: no history).  The
+ * adjoint starts from zero at T and does not flow into the initial state.
  * Loss gradients: gz_loss [T][B][N] (or NULL) plus gz_neuron [N] broadcast over
  * (t, b) (or NULL); gv_loss [T][B][N] (or NULL).
  * Outputs: dW_rec [S_rec], dW_lgn [S_lgn], dW_bkg [S_bkg] accumulated (each may be
  * NULL); gz_out [T][B][N] total spike gradient (may be NULL). */
 int orc_backward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint8_t *bkg,
-                 const uint8_t *zs, const uint8_t *refs, const float *vs,
+                 const float *zbuf0, const uint8_t *zs, const uint8_t *refs, const float *vs,
                  const float *gz_loss, const float *gz_neuron, const float *gv_loss,
                  float *dW_rec, float *dW_lgn, float *dW_bkg, float *gz_out)
 {
@@ -345,7 +347,8 @@ int orc_backward(const orc_cell *c, int T, int B, const uint8_t *lgn, const uint
             for (int64_t d = 1; d <= D; ++d)
                 for (int64_t n = 0; n < N; ++n)
                     act[(int64_t)b * DN + (d - 1) * N + n] =
-                        (t - d >= 0) ? (float)zs[(int64_t)(t - d) * BN + (int64_t)b * N + n] : 0.0f;
+                        (t - d >= 0) ? (float)zs[(int64_t)(t - d) * BN + (int64_t)b * N + n]
+                        : (zbuf0 && zbuf0[(int64_t)b * DN + (d - t - 1) * N + n] > 0.0f ? 1.0f : 0.0f);
         orc_syn_bwd(B, N, DN, nb, c->rec.S, act, 0, c->rec.post, c->rec.col, c->rec.w, c->rec.sid,
                     c->basis, c->rec.order, c->rec.row_splits, dy, dz, dW_rec, scr);
         for (int b = 0; b < B; ++b)

@@ -60,9 +60,10 @@ def _syn(z_src, table, w, basis, B, N, nb):
 
 
 def bptt(tb, lgn, bkg, z_forced, gz, gv, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.5,
-         pseudo_gauss=True, hard_reset=False):
+         pseudo_gauss=True, hard_reset=False, zbuf0=None):
     """Returns ({'rec','lgn','bkg'}: dL/dW float64 arrays, v [T,B,N]) for
-    L = sum(z * gz) + sum(v * gv)."""
+    L = sum(z * gz) + sum(v * gv), from a zero state with the spike history zbuf0 [B, D*N]
+    (None: no spikes); the history's spikes are inputs (no gradient flows into them)."""
     T, B = lgn.shape[:2]
     N, D, nb = tb.n_neurons, tb.max_delay, tb.n_basis
     f = lambda a: torch.tensor(np.asarray(a, dtype=np.float64))
@@ -78,6 +79,8 @@ def bptt(tb, lgn, bkg, z_forced, gz, gv, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.
     x_bkg = torch.tensor(np.asarray(bkg).astype(np.float64))
 
     z_buf = torch.zeros((B, D * N), dtype=torch.float64)
+    if zbuf0 is not None:
+        z_buf = torch.tensor(np.asarray(zbuf0, dtype=np.float64))
     v = torch.zeros((B, N), dtype=torch.float64)
     r = torch.zeros((B, N), dtype=torch.int64)
     asc = torch.zeros((B, N, 2), dtype=torch.float64)

@@ -57,3 +57,33 @@ def device_to_numpy(dev_ptr, n, dtype):
                        ctypes.c_size_t(out.nbytes), ctypes.c_int(2))  # hipMemcpyDeviceToHost
     assert rc == 0, rc
     return out
+
+
+def assert_grads_per_element(got, exp, scale, what="", rtol=RTOL, atol=ATOL):
+    """North star's bar per gradient element: |got - exp| <= rtol * scale + atol, with scale
+    the element's sum of absolute terms (oracle.cpu.bptt_abs_scale).  Returns the largest
+    |got - exp| / scale over the elements with a nonzero scale (the error distribution's
+    tail, printed by the callers)."""
+    a = np.asarray(got, dtype=np.float64)
+    e = np.asarray(exp, dtype=np.float64)
+    s = np.asarray(scale, dtype=np.float64)
+    assert a.shape == e.shape == s.shape, (what, a.shape, e.shape, s.shape)
+    err = np.abs(a - e)
+    bad = err > rtol * s + atol
+    if np.any(bad):
+        i = np.flatnonzero(bad)[0]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} elements outside {rtol:g}*sum|terms| + "
+                             f"{atol:g}; first at {i}: {a.flat[i]!r} vs {e.flat[i]!r} (scale {s.flat[i]!r})")
+    nz = s > 0
+    return float(np.max(err[nz] / s[nz])) if np.any(nz) else 0.0
+
+
+def error_summary(got, exp, scale):
+    """Quantiles of |got - exp| / scale over the nonzero-scale elements."""
+    a, e, s = (np.asarray(x, dtype=np.float64) for x in (got, exp, scale))
+    nz = s > 0
+    if not np.any(nz):
+        return {}
+    r = np.abs(a - e)[nz] / s[nz]
+    return {"n": int(nz.sum()), "p50": float(np.quantile(r, 0.5)), "p99": float(np.quantile(r, 0.99)),
+            "max": float(r.max()), "exact_frac": float(np.mean(r == 0))}

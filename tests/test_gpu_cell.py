@@ -286,9 +286,10 @@ def test_fused_voltage_regularization(mode, core):
         pen, dpen = (vn - 1.0) ** 2, 2.0 * (vn - 1.0)
     sel = np.ones(N, bool) if mask is None else mask
     expect = cost * pen[:, :, sel].mean()
+    # the tensor form (autograd's) switches the fused gradient off, the fused form on again
+    assert abs(float(reg(v)) - expect) <= 1e-6 * abs(expect) + 1e-12
     loss = float(reg())
     assert abs(loss - expect) <= 1e-6 * abs(expect) + 1e-12
-    assert abs(float(reg(v)) - loss) <= 1e-6 * abs(loss) + 1e-12
     oc = _oracle(tn[1], **ORC_KW)
     oz, ov, oref, _ = oc.forward(lgn, bkg)
     rng = np.random.default_rng(7)
@@ -348,3 +349,63 @@ def test_short_sequences_forward_and_backward(T, B, mode):
     for k in ("rec", "lgn", "bkg"):
         a, e = g[k].cpu().numpy(), og[k]
         assert np.max(np.abs(a - e)) <= 1e-5 * max(np.max(np.abs(e)), 1e-30) + 1e-6, k
+
+
+def test_voltage_regularization_through_autograd_is_not_doubled():
+    """reg(v) on RSNNRollout's voltage output (the reference's usage) differentiated by
+    autograd: the gradient reaches the cell as dL/dv once, and the fused form (switched off
+    by that call) adds nothing; equals the oracle's BPTT given that dL/dv."""
+    from v1_glif_model_amd.losses import VoltageRegularization
+    from v1_glif_model_amd.models import RSNNRollout
+    cfg = tiny_config(rs=2.0, ins=3.0)
+    tn = network(cfg, seed=5, dense_basis=True)
+    T, B = 30, 3
+    lgn, bkg = _inputs(cfg, T, B, seed=6)
+    cell = _cell(tn, "deterministic", train_input=True, train_recurrent_per_type=False, **CELL_KW)
+    reg = VoltageRegularization(cell, voltage_cost=0.5, penalty_mode="threshold")
+    w = (cell.recurrent_weight_values, cell.input_weight_values, cell.bkg_input_weights)
+    z, v = RSNNRollout.apply(cell, torch.tensor(lgn, device="cuda"), torch.tensor(bkg, device="cuda"), *w)
+    loss = reg(v)
+    loss.backward()
+    vn = v.detach().cpu().numpy().astype(np.float64)
+    gv = (0.5 * 2.0 * (vn - 1.0) / vn.size).astype(np.float32)
+    oc = _oracle(tn[1], **ORC_KW)
+    oz, ov, oref, _ = oc.forward(lgn, bkg)
+    og = oc.backward(lgn, bkg, oz, oref, ov, gv_loss=gv)
+    for k, t in zip(("rec", "lgn", "bkg"), w):
+        a, e = t.grad.cpu().numpy(), og[k]
+        scale = np.max(np.abs(e))
+        assert scale > 0
+        assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
+    del reg
+
+
+def test_two_rollouts_before_backward():
+    """Each RSNNRollout node keeps its own workspace: two rollouts, then the backward of the
+    first, give the first's gradients; a V1Column.backward whose rollout's workspace was
+    overwritten raises instead of using the later rollout's activations."""
+    from v1_glif_model_amd.models import RSNNRollout
+    cfg = tiny_config(rs=2.0, ins=3.0)
+    tn = network(cfg, seed=7, dense_basis=True)
+    T, B = 25, 2
+    lgn, bkg = _inputs(cfg, T, B, seed=8)
+    lgn2, bkg2 = _inputs(cfg, T, B, seed=9)
+    cell = _cell(tn, "deterministic", train_recurrent_per_type=False, **CELL_KW)
+    w = (cell.recurrent_weight_values, cell.input_weight_values, cell.bkg_input_weights)
+    gz = torch.tensor(np.random.default_rng(1).normal(0, 1, (T, B, tn[1].n_neurons)).astype(np.float32),
+                      device="cuda")
+    dev = lambda a: torch.tensor(a, device="cuda")
+    z1, _ = RSNNRollout.apply(cell, dev(lgn), dev(bkg), *w)
+    z2, _ = RSNNRollout.apply(cell, dev(lgn2), dev(bkg2), *w)
+    (z1 * gz).sum().backward()
+    g_two = w[0].grad.clone()
+    w[0].grad = None
+    z1b, _ = RSNNRollout.apply(cell, dev(lgn), dev(bkg), *w)
+    (z1b * gz).sum().backward()
+    np.testing.assert_array_equal(g_two.cpu().numpy(), w[0].grad.cpu().numpy())
+    # the shared workspace: a second rollout invalidates the first one's record
+    cell.rollout(lgn, bkg)
+    first = cell._last
+    cell.rollout(lgn2, bkg2)
+    with pytest.raises(RuntimeError, match="overwritten"):
+        cell.backward(gz=gz, rollout=first)

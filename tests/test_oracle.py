@@ -234,10 +234,16 @@ def test_threshold_is_strict():
 
 
 # ----------------------------------------------------------------- BPTT ----
-@pytest.mark.parametrize("pseudo_gauss,hard_reset,rd,vgd", [
-    (True, False, 0.5, 0.5), (False, False, 0.5, 0.5), (True, True, 0.5, 0.5),
-    (True, False, 0.2, 0.0), (False, False, 1.0, 0.3)])
-def test_bptt_matches_autograd_restatement(pseudo_gauss, hard_reset, rd, vgd):
+@pytest.mark.parametrize("pseudo_gauss,hard_reset,rd,vgd,gauss_std,damp,history", [
+    (True, False, 0.5, 0.5, 0.5, 0.5, False), (False, False, 0.5, 0.5, 0.5, 0.5, False),
+    (True, True, 0.5, 0.5, 0.5, 0.5, False), (True, False, 0.2, 0.0, 0.5, 0.5, False),
+    (False, False, 1.0, 0.3, 0.5, 0.5, False),
+    # width != amplitude and d != 1 - d (the reference's training defaults among them,
+    # multi_training.py:1071-1074), and a start from a carried spike history
+    (True, False, 0.2, 0.3, 0.7, 0.3, False), (True, True, 0.1, 0.5, 0.3, 0.1, False),
+    (False, True, 0.1, 0.5, 0.3, 0.1, False), (False, False, 0.2, 0.3, 0.7, 0.3, True),
+    (True, False, 0.1, 0.5, 0.3, 0.1, True)])
+def test_bptt_matches_autograd_restatement(pseudo_gauss, hard_reset, rd, vgd, gauss_std, damp, history):
     torch = pytest.importorskip("torch")
     torch.set_num_threads(4)
     from oracle import torch_ref
@@ -245,15 +251,21 @@ def test_bptt_matches_autograd_restatement(pseudo_gauss, hard_reset, rd, vgd):
     _, tb = network(cfg, seed=1, dense_basis=True)
     T, B = 30, 2
     lgn, bkg = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
-    kw = dict(pseudo_gauss=pseudo_gauss, hard_reset=hard_reset, rd=rd, vgd=vgd, gauss_std=0.5, damp=0.5)
+    kw = dict(pseudo_gauss=pseudo_gauss, hard_reset=hard_reset, rd=rd, vgd=vgd, gauss_std=gauss_std, damp=damp)
     oc = orc.OracleCell(tb, **kw)
-    z, v, ref, _ = oc.forward(lgn, bkg)
+    zbuf0 = None
+    st = oc.zero_state(B)
+    if history:
+        # spikes in every delay slot of the initial history (their dW terms enter at ticks < D)
+        zbuf0 = (np.random.default_rng(9).uniform(size=st["zbuf"].shape) < 0.2).astype(np.float32)
+        st["zbuf"][...] = zbuf0
+    z, v, ref, _ = oc.forward(lgn, bkg, state=st)
     assert z.sum() > 0
     rng = np.random.default_rng(5)
     gz = rng.normal(0, 1, z.shape).astype(np.float32)
     gv = rng.normal(0, 0.1, z.shape).astype(np.float32)
-    og = oc.backward(lgn, bkg, z, ref, v, gz_loss=gz, gv_loss=gv)
-    tg, tv = torch_ref.bptt(tb, lgn, bkg, z, gz, gv, **kw)
+    og = oc.backward(lgn, bkg, z, ref, v, gz_loss=gz, gv_loss=gv, zbuf0=zbuf0)
+    tg, tv = torch_ref.bptt(tb, lgn, bkg, z, gz, gv, zbuf0=zbuf0, **kw)
     assert np.max(np.abs(tv - v)) < 1e-5
     for k in ("rec", "lgn", "bkg"):
         scale = np.max(np.abs(tg[k]))

@@ -8,9 +8,17 @@ the (trimmed) ticks, so no [T, B, N] spike gradient has to exist.
 
 ``VoltageRegularization`` (loss_functions.py:1047-1119): the penalty of the cell's output
 voltages, "range" relu(|v - 0.5| - 0.5)^2 or "threshold" (v - 1)^2, cost * mean over
-(B, T, N) -- over the core-mask neurons only when a ``core_mask`` is given.  Constructing it enables the fused form on the cell: the loss of the last
-rollout is reduced from the voltages the cell keeps for BPTT, and ``V1Column.backward``
-adds the gradient inside the adjoint, so no [T, B, N] voltage tensor has to exist.
+(B, T, N) -- over the core-mask neurons only when a ``core_mask`` is given.  Two forms:
+
+* ``reg()`` (fused): the loss of the cell's last rollout is reduced from the voltages the
+  cell keeps for BPTT, and the next ``V1Column.backward`` adds the gradient inside the
+  adjoint, so no [T, B, N] voltage tensor has to exist;
+* ``reg(voltages)``: the reference's form on a voltage tensor (e.g. the ``v`` output of
+  ``RSNNRollout``), differentiated by autograd, which hands dL/dv to the backward as ``gv``.
+  This call switches the fused gradient off, so the gradient is never applied twice.
+
+Constructing the object selects the fused form; it is switched off again when the object
+is deleted or ``disable()`` is called.
 """
 from __future__ import annotations
 
@@ -51,11 +59,28 @@ class VoltageRegularization:
             check(lib().glif_cell_set_voltage_mask(cell.handle, ptr(self._mask_u8), int(m.sum().item())))
         else:
             check(lib().glif_cell_set_voltage_mask(cell.handle, None, 0))
-        check(lib().glif_cell_set_voltage_loss(cell.handle, _MODES[penalty_mode], self._voltage_cost))
+        self._set_fused(True)
+
+    def _set_fused(self, on: bool):
+        mode, cost = (_MODES[self._penalty_mode], self._voltage_cost) if on else (0, 0.0)
+        check(lib().glif_cell_set_voltage_loss(self._cell.handle, mode, cost))
+        self._fused = on
 
     def disable(self):
-        check(lib().glif_cell_set_voltage_loss(self._cell.handle, 0, 0.0))
-        check(lib().glif_cell_set_voltage_mask(self._cell.handle, None, 0))
+        """Switch the fused gradient off and release the core mask on the cell."""
+        cell = getattr(self, "_cell", None)
+        if cell is None or getattr(cell, "handle", None) is None:
+            return
+        check(lib().glif_cell_set_voltage_loss(cell.handle, 0, 0.0))
+        check(lib().glif_cell_set_voltage_mask(cell.handle, None, 0))
+        self._fused = False
+        self._cell = None
+
+    def __del__(self):
+        try:
+            self.disable()
+        except Exception:
+            pass
 
     @staticmethod
     def penalty(v, mode="range"):
@@ -66,16 +91,22 @@ class VoltageRegularization:
 
     def __call__(self, voltages=None):
         """Loss of ``voltages`` [T, B, N] if given, else (fused) of the cell's last rollout."""
+        cell = self._cell
+        if cell is None:
+            raise RuntimeError("this VoltageRegularization was disabled")
         if voltages is not None:
+            # autograd carries this gradient (as gv): the fused one must not be added too
+            if self._fused:
+                check(lib().glif_cell_set_voltage_loss(cell.handle, 0, 0.0))
+                self._fused = False
             if self._core_mask is not None:
                 voltages = voltages[:, :, self._core_mask]   # tf.boolean_mask(..., axis=2)
             return self.penalty(voltages, self._penalty_mode).mean() * self._voltage_cost
-        cell = self._cell
-        if getattr(cell, "_last", None) is None:
-            raise RuntimeError("no rollout to take the voltages from")
-        B, T, ws = cell._last
+        if not self._fused:
+            self._set_fused(True)
+        rec = cell.check_rollout()
         out = torch.empty((), dtype=torch.float32, device=cell.device)
-        check(lib().glif_cell_voltage_loss(cell.handle, B, T, ptr(out), ptr(ws), ws.numel(),
+        check(lib().glif_cell_voltage_loss(cell.handle, rec.B, rec.T, ptr(out), ptr(rec.ws), rec.ws.numel(),
                                            stream_ptr(cell.device)))
         return out
 

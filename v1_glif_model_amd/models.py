@@ -9,8 +9,8 @@ Differences from the reference, by necessity:
   (keys ``tau_basis`` / ``basis``) instead of ``synaptic_data/tau_basis.npy`` and the
   network's pickle (models.py:518, 614-622).
 * The background Poisson counts are an input (``bkg`` tensors): TF's stateless
-  Poisson stream (models.py:865-887) cannot be reproduced.  ``call`` samples them
-  with torch when they are not given.
+  Poisson stream (models.py:865-887) cannot be reproduced.  ``call`` draws them from
+  the device Philox sampler (``inputs.poisson``) when they are not given.
 * The refractory state is int16 (the reference uses int8, int16 above 127 steps).
 """
 from __future__ import annotations
@@ -24,9 +24,9 @@ import torch
 from . import _lib
 from ._lib import check, lib, ptr, stream_ptr
 from .ops import MODES, SynapseTable
-from .tables import build_cell_tables
+from .tables import build_cell_tables, trainable_populations
 
-__all__ = ["V1Column", "RSNNRollout"]
+__all__ = ["V1Column", "RSNNRollout", "Rollout"]
 
 
 class V1Column:
@@ -70,13 +70,12 @@ class V1Column:
         self.bkg_table = SynapseTable(tb.bkg.indices, tb.bkg.syn_id, (tb.n_neurons, tb.bkg.n_cols),
                                       tb.basis)
         dev = self.device
-        individual = bool(train_recurrent) and not bool(train_recurrent_per_type)
+        tr = trainable_populations(train_recurrent, train_recurrent_per_type, train_input, train_noise)
         # trainable weight vectors in reference order (models.py:663-669, 725-731, 758-764)
-        self.recurrent_weight_values = torch.tensor(tb.rec.weight, device=dev).requires_grad_(
-            bool(train_recurrent))
-        self.input_weight_values = torch.tensor(tb.lgn.weight, device=dev).requires_grad_(bool(train_input))
-        self.bkg_input_weights = torch.tensor(tb.bkg.weight, device=dev).requires_grad_(bool(train_noise))
-        self._individual_training = individual
+        self.recurrent_weight_values = torch.tensor(tb.rec.weight, device=dev).requires_grad_(tr["rec"])
+        self.input_weight_values = torch.tensor(tb.lgn.weight, device=dev).requires_grad_(tr["lgn"])
+        self.bkg_input_weights = torch.tensor(tb.bkg.weight, device=dev).requires_grad_(tr["bkg"])
+        self._individual_training = tr["rec"]
         # sign masks for SignedConstraint (models.py:419-427)
         self.recurrent_weight_positive = torch.tensor(tb.rec.weight >= 0, device=dev)
         self.input_weight_positive = torch.tensor(tb.lgn.weight >= 0, device=dev)
@@ -95,6 +94,9 @@ class V1Column:
                                      self.bkg_table.handle, C.byref(h)))
         self.handle = h
         self._ws = {}
+        self._gen = 0          # rollouts run so far
+        self._ws_gen = {}      # workspace data_ptr -> the rollout that last wrote it
+        self._last = None
 
     def __del__(self):
         h = getattr(self, "handle", None)
@@ -176,7 +178,13 @@ class V1Column:
                                       C.byref(cstate), ptr(z), ptr(v), ptr(spike_count), ptr(ws),
                                       ws.numel(), stream_ptr(self.device)))
         st[6] = st[6] + T
-        self._last = (B, T, ws)
+        self._gen += 1
+        key = ws.data_ptr()
+        self._ws_gen.pop(key, None)
+        self._ws_gen[key] = self._gen
+        while len(self._ws_gen) > 64:   # records of workspaces long gone
+            self._ws_gen.pop(next(iter(self._ws_gen)))
+        self._last = Rollout(B, T, ws, self._gen)
         return z, v, tuple(st)
 
     def call(self, inputs, state, bkg_counts=None, constants=None):
@@ -196,12 +204,26 @@ class V1Column:
     __call__ = call
 
     # ---- backward ------------------------------------------------------------
-    def backward(self, gz=None, gz_neuron=None, gv=None, want=("rec", "lgn", "bkg")):
-        """BPTT through the last `rollout` (zero initial adjoint).
+    def check_rollout(self, rollout: Optional["Rollout"] = None) -> "Rollout":
+        """The rollout record a backward or fused loss reads (default: the last rollout); raises
+        if a later rollout has overwritten its workspace (saved voltages, spike bits)."""
+        rec = self._last if rollout is None else rollout
+        if rec is None:
+            raise RuntimeError("no rollout to take the saved activations from")
+        if self._ws_gen.get(rec.ws.data_ptr()) != rec.gen:
+            raise RuntimeError("the workspace of this rollout was overwritten by a later rollout on the same "
+                               "workspace; give each rollout that is to be differentiated its own workspace "
+                               "(rollout(..., ws=...)) or run its backward first")
+        return rec
+
+    def backward(self, gz=None, gz_neuron=None, gv=None, want=("rec", "lgn", "bkg"),
+                 rollout: Optional["Rollout"] = None):
+        """BPTT through a rollout (default: the last one; zero initial adjoint).
 
         gz / gv: dL/dz, dL/dv [T, B, N] (or None); gz_neuron: dL/dz [N] broadcast over
         (t, b).  Returns dict of weight gradients in reference order."""
-        B, T, ws = self._last
+        rec = self.check_rollout(rollout)
+        B, T, ws = rec.B, rec.T, rec.ws
         dev = self.device
         out = {}
         for name, table in (("rec", self.rec_table), ("lgn", self.lgn_table), ("bkg", self.bkg_table)):
@@ -214,18 +236,34 @@ class V1Column:
         return out
 
 
+class Rollout:
+    """What a backward needs of one rollout: its batch, length and workspace (which holds the
+    saved voltages and spike bits), and the rollout's number on its cell."""
+    __slots__ = ("B", "T", "ws", "gen")
+
+    def __init__(self, B, T, ws, gen):
+        self.B, self.T, self.ws, self.gen = B, T, ws, gen
+
+
 class RSNNRollout(torch.autograd.Function):
-    """Autograd node over a whole rollout: weights -> (z [T,B,N], v [T,B,N])."""
+    """Autograd node over a whole rollout: weights -> (z [T,B,N], v [T,B,N]).
+
+    Each node runs on a workspace of its own (from torch's caching allocator), so several
+    rollouts, or per-step ``call``s, may run before the backward of any of them."""
 
     @staticmethod
     def forward(ctx, cell: V1Column, lgn, bkg, w_rec, w_lgn, w_bkg):
-        z, v, _ = cell.rollout(lgn, bkg)
+        T, B = int(lgn.shape[0]), int(lgn.shape[1])
+        n = int(lib().glif_cell_workspace(cell.handle, B, T))
+        ws = torch.empty(n, dtype=torch.uint8, device=cell.device)
+        z, v, _ = cell.rollout(lgn, bkg, ws=ws)
         ctx.cell = cell
+        ctx.rollout = cell._last
         ctx.want = tuple(n for n, w in (("rec", w_rec), ("lgn", w_lgn), ("bkg", w_bkg)) if w.requires_grad)
         return z, v
 
     @staticmethod
     def backward(ctx, gz, gv):
-        g = ctx.cell.backward(gz=gz, gv=gv, want=ctx.want)
+        g = ctx.cell.backward(gz=gz, gv=gv, want=ctx.want, rollout=ctx.rollout)
         return None, None, None, g["rec"], g["lgn"], g["bkg"]
 

@@ -188,18 +188,36 @@ def where_gt0(z: torch.Tensor) -> torch.Tensor:
     return pairs[: int(count.item())]
 
 
+def _array_key(a):
+    """Identity of a table input: the object (held by the cache entry, so its id is not
+    reused), its shape and, for a tensor, its in-place version counter."""
+    if torch.is_tensor(a):
+        return (id(a), tuple(a.shape), a._version)
+    return (id(a), tuple(np.shape(a)))
+
+
 def _table_for(pre_ind_table: PreIndTable, synapse_indices, syn_ids, dense_shape, basis):
-    key = (int(dense_shape[0]), int(dense_shape[1]))
-    t = pre_ind_table._tables.get(key)
-    if t is None:
-        n_post, n_cols = key
+    """The device table of these arrays, built on first use and cached on ``pre_ind_table``.
+    The cache is keyed on the dense shape and on the identity of ``synapse_indices``,
+    ``syn_ids`` and ``basis`` (new objects, or a tensor modified in place, build a new table;
+    the reference builds its tables once, models.py:636-705)."""
+    key = ((int(dense_shape[0]), int(dense_shape[1])), _array_key(synapse_indices), _array_key(syn_ids),
+           _array_key(basis))
+    hit = pre_ind_table._tables.get(key)
+    if hit is None:
+        n_post, n_cols = key[0]
         slots = n_cols // n_post if n_cols % n_post == 0 and n_cols > n_post else 1
         ind = synapse_indices.cpu().numpy() if torch.is_tensor(synapse_indices) else synapse_indices
         sid = syn_ids.cpu().numpy() if torch.is_tensor(syn_ids) else syn_ids
         bs = basis.detach().cpu().numpy() if torch.is_tensor(basis) else basis
-        t = SynapseTable(ind, sid, key, bs, n_delay_slots=slots)
-        pre_ind_table._tables[key] = t
-    return t
+        if np.asarray(ind).shape[0] != pre_ind_table.values.size:
+            raise ValueError("synapse_indices and pre_ind_table hold different numbers of synapses")
+        t = SynapseTable(ind, sid, key[0], bs, n_delay_slots=slots)
+        # one table per pre_ind_table: a new key replaces the old entry (and frees its device table)
+        pre_ind_table._tables.clear()
+        hit = (t, (synapse_indices, syn_ids, basis))
+        pre_ind_table._tables[key] = hit
+    return hit[0]
 
 
 class _SynCurrents(torch.autograd.Function):

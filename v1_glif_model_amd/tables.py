@@ -11,6 +11,8 @@ from identical numbers:
   float64 then cast to float32 (`models.py:518-526`);
 * ``t_ref_steps = max(ceil(t_ref / dt), 1)`` (`models.py:574-583`);
 * ``asc_decay = exp(-dt * sigmoid(logit(k)))`` in float32 (`models.py:556-593`);
+* ``max_delay = min(ceil(max delay / dt), flag)`` over the recurrent delays and the LGN /
+  background ``delays`` when present (`models.py:528-539`);
 * recurrent weights ``w / voltage_scale[post] * recurrent_weight_scale / lr_scale``,
   delays ``round(clip(d, dt, max_delay) / dt)``, column ``pre + N * (delay - 1)``,
   dense shape ``(N, max_delay * N)`` (`models.py:625-669`);
@@ -22,7 +24,18 @@ from __future__ import annotations
 import dataclasses
 import numpy as np
 
-__all__ = ["SynapseTable", "CellTables", "build_cell_tables"]
+__all__ = ["SynapseTable", "CellTables", "build_cell_tables", "trainable_populations"]
+
+
+def trainable_populations(train_recurrent=True, train_recurrent_per_type=True, train_input=False,
+                          train_noise=True) -> dict:
+    """Which weight vectors V1Column trains (models.py:651-669, 728-731, 761-764): the
+    individual recurrent weights only with train_recurrent and not train_recurrent_per_type
+    (the per-type factors of that mode are commented out in the reference, so the recurrent
+    weights are then frozen), the LGN weights with train_input, the background weights with
+    train_noise."""
+    return {"rec": bool(train_recurrent) and not bool(train_recurrent_per_type),
+            "lgn": bool(train_input), "bkg": bool(train_noise)}
 
 
 @dataclasses.dataclass
@@ -106,7 +119,12 @@ def build_cell_tables(net: dict, dt: float = 1.0, max_delay: int = 0, lr_scale: 
     syn = network["synapses"]
     indices = np.array(syn["indices"], dtype=np.int64)
     delays = np.asarray(syn["delays"], dtype=np.float64)
-    data_max_delay = int(np.ceil(np.max(delays) / dt)) if delays.size else 1
+    # models.py:528-539: the largest delay of the recurrent synapses and of the LGN and
+    # background populations when they carry one (their delays are not applied, :715-718)
+    all_delays = [delays] + [np.asarray(pop["delays"], dtype=np.float64).reshape(-1)
+                             for pop in (lgn_input, bkg_input) if "delays" in pop]
+    all_delays = np.concatenate(all_delays)
+    data_max_delay = int(np.ceil(np.max(all_delays) / dt)) if all_delays.size else 1
     D = min(data_max_delay, max_delay) if max_delay > 0 else data_max_delay
     w = (np.asarray(syn["weights"], dtype=np.float32) / vs[type_ids[indices[:, 0]]]).astype(np.float32)
     d_steps = np.round(np.clip(delays, dt, D) / dt).astype(np.int64)
