@@ -47,6 +47,9 @@ def _args():
     ap.add_argument("--cpu-steps", type=int, default=30,
                     help="timesteps of the CPU baseline sample, timed with one thread and with the "
                          "host's cores (0: skip)")
+    ap.add_argument("--cpu-start", type=int, default=200,
+                    help="first tick of the CPU baseline sample (the state there comes from the GPU's "
+                         "deterministic rollout; config 2 is silent for its first ~70 ms)")
     ap.add_argument("--forward-only", action="store_true")
     ap.add_argument("--syn-types", type=int, default=None,
                     help="synapse types of the generated network (the configurations use 5; the "
@@ -300,7 +303,7 @@ def main():
     t_gen = time.time()
     net = sy.make_network(cfg, seed=0, dense_basis=args.dense_basis)
     lgn_np, bkg_np = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
-    cell = V1Column(net, mode=args.mode, gauss_std=0.5, dampening_factor=0.5,
+    cell = V1Column(net, mode=args.mode, gauss_std=0.5, dampening_factor=0.5, train_recurrent_per_type=False,
                     recurrent_dampening_factor=0.5, voltage_gradient_dampening=0.5,
                     pseudo_gauss=True, train_input=True)
     t_gen = time.time() - t_gen
@@ -455,20 +458,31 @@ def main():
         roofline["traffic_gbs"] = round(tg, 1)
         roofline["traffic_frac"] = round(tg / HBM_PEAK_GBS, 4)
 
-    # CPU baseline: the C restatement on a bounded prefix of the same workload, timed with
-    # one thread and with the host's cores (its OpenMP loops keep every sum's order, so both
-    # give the same bits)
+    # CPU baseline: the C restatement on a bounded window of the same workload, timed with one
+    # thread and with the cores this process may use (its OpenMP loops keep every sum's order,
+    # so both give the same bits).  The window starts at tick --cpu-start (past the network's
+    # silent onset, so the recurrent events are those of the active regime) from the state the
+    # deterministic GPU rollout reaches there (bit-exact with the oracle's own trajectory).
     cpu = cpu_1t = None
     if args.cpu_steps > 0:
         from oracle import cpu as orc_cpu
         from oracle.cpu import OracleCell
-        Tc = min(args.cpu_steps, T)
+        t_a = min(max(args.cpu_start, 0), T - 1)
+        Tc = min(args.cpu_steps, T - t_a)
         oc = OracleCell(tb, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.5, pseudo_gauss=True)
+        st_dev = [z.clone() for z in zero]
+        if t_a > 0:
+            cell.rollout(lgn[:t_a], bkg[:t_a], state=st_dev, record_z=False, record_v=False, mode="deterministic")
+            torch.cuda.synchronize()
+        st0 = dict(zbuf=st_dev[0].cpu().numpy(), v=st_dev[1].cpu().numpy(),
+                   r=st_dev[2].cpu().numpy().astype(np.int32), asc=st_dev[3].cpu().numpy(),
+                   psc_rise=st_dev[4].cpu().numpy(), psc=st_dev[5].cpu().numpy())
+        lw, bw = lgn_np[t_a:t_a + Tc], bkg_np[t_a:t_a + Tc]
 
         def cpu_run(threads):
             used = orc_cpu.set_threads(threads)
             c0 = time.perf_counter()
-            oz, ov, oref, _ = oc.forward(lgn_np[:Tc], bkg_np[:Tc])
+            oz, ov, oref, _ = oc.forward(lw, bw, state=st0)
             if not args.forward_only:
                 from oracle.rate_loss_ref import rate_dist_loss, rate_mse
                 cnt = oz.reshape(Tc, B, N).sum((0, 1))
@@ -481,17 +495,19 @@ def main():
                     ptrs = np.concatenate([[0], np.cumsum([rate_loss.populations[k].size for k in rate_loss.populations])])
                     _, gzn = rate_dist_loss(cnt, Tc * B, ids, ptrs, tgt, rate_cost=10000.0, shuffle=True)
                     gv = (np.float32(2.0 / (Tc * B * N)) * (ov - np.float32(1.0))).astype(np.float32)
-                oc.backward(lgn_np[:Tc], bkg_np[:Tc], oz, oref, ov, gz_neuron=gzn, gv_loss=gv,
-                            want=("rec", "lgn"))
-            return used, time.perf_counter() - c0
+                oc.backward(lw, bw, oz, oref, ov, gz_neuron=gzn, gv_loss=gv, want=("rec", "lgn"), zbuf0=st0["zbuf"])
+            return used, time.perf_counter() - c0, int(oz.sum())
 
-        what = (f"first {Tc} of {T} timesteps of the same workload (B={B}, N={N}), "
+        n1, s1, spk = cpu_run(1)
+        what = (f"ticks {t_a}-{t_a + Tc - 1} of {T} of the same workload (B={B}, N={N}, {spk} spikes in the window), "
                 f"{'forward only' if args.forward_only else 'forward + BPTT'}")
-        n1, s1 = cpu_run(1)
         cpu_1t = {"value": round(B * N * Tc / s1, 1), "unit": "neuron-timesteps/s", "cores": n1, "kind": "port",
                   "sample": f"oracle/glif_oracle.c single thread, {what}, {s1:.1f} s"}
-        cores = min(len(os.sched_getaffinity(0)), 16)
-        nt, st = cpu_run(cores) if cores > 1 else (n1, s1)
+        # every core this process may use (OMP_NUM_THREADS, where set, is the host's share for it)
+        cores = len(os.sched_getaffinity(0))
+        if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+            cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+        nt, st, _ = cpu_run(cores) if cores > 1 else (n1, s1, spk)
         cpu = {"value": round(B * N * Tc / st, 1), "unit": "neuron-timesteps/s", "cores": nt, "kind": "port",
                "sample": f"oracle/glif_oracle.c, {nt} OpenMP threads (batch entries and columns in parallel, "
                          f"same sums as one thread), {what}, {st:.1f} s"}

@@ -110,3 +110,34 @@ def test_gpu_exp_adam_matches_oracle(amsgrad, constrained):
     np.testing.assert_allclose(s["m"].cpu().numpy(), m, rtol=1e-6, atol=1e-12)
     np.testing.assert_allclose(s["v"].cpu().numpy(), v, rtol=1e-6, atol=1e-12)
     assert opt.iterations == 7
+
+
+@pytest.mark.gpu
+def test_gpu_update_reaches_the_next_rollout():
+    """The optimizer writes the weights through a raw pointer; the next rollout must use the
+    updated weights (the synapse tables refresh their copies when the tensor's version moves):
+    a rollout after the step equals one of a fresh cell given the updated weights."""
+    import torch
+    from tests.helpers import network, tiny_config
+    from v1_glif_model_amd import synthetic as sy
+    from v1_glif_model_amd.models import V1Column
+    from v1_glif_model_amd.optim import ExponentiatedAdam
+    cfg = tiny_config(rs=2.0, ins=3.0)
+    net, tb = network(cfg, seed=12, dense_basis=True)
+    lgn, bkg = sy.make_inputs(cfg, seed=13, seq_len=30, batch=2)
+    kw = dict(gauss_std=0.5, dampening_factor=0.5, pseudo_gauss=True, train_recurrent_per_type=False)
+    a = V1Column(net, mode="deterministic", **kw)
+    a.rollout(lgn, bkg)
+    g = {k: torch.tensor(np.random.default_rng(1).normal(0, 1, n).astype(f32), device="cuda")
+         for k, n in (("rec", tb.rec.n_syn), ("lgn", tb.lgn.n_syn))}
+    ExponentiatedAdam(learning_rate=0.3).apply_gradients(
+        [(g["rec"], a.recurrent_weight_values), (g["lgn"], a.input_weight_values)])
+    za, va, _ = a.rollout(lgn, bkg)
+    b = V1Column(net, mode="deterministic", **kw)
+    with torch.no_grad():
+        b.recurrent_weight_values.copy_(a.recurrent_weight_values)
+        b.input_weight_values.copy_(a.input_weight_values)
+    zb, vb, _ = b.rollout(lgn, bkg)
+    assert not torch.equal(a.recurrent_weight_values, torch.tensor(tb.rec.weight, device="cuda"))
+    np.testing.assert_array_equal(za.cpu().numpy(), zb.cpu().numpy())
+    np.testing.assert_array_equal(va.cpu().numpy().view(np.uint32), vb.cpu().numpy().view(np.uint32))

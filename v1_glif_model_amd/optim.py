@@ -89,4 +89,7 @@ class ExponentiatedAdam:
                 check(lib().glif_exp_adam(ptr(var), ptr(s["m"]), ptr(s["v"]), ptr(s["vhat"]), ptr(g),
                                           ptr(pos), var.numel(), float(alpha), float(self.beta_1),
                                           float(self.beta_2), float(self.epsilon), stream_ptr(var.device)))
+            # the kernel wrote through a raw pointer: mark the tensor modified, so the weight
+            # copies the synapse tables keep (keyed on the tensor's version) are refreshed
+            torch.autograd.graph.increment_version(var)
         self.iterations += 1
