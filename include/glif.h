@@ -93,6 +93,20 @@ int glif_table_set_weights(glif_table *t, const float *w, void *stream);
 size_t glif_syn_workspace(const glif_table *t, int32_t B);
 int glif_syn_fwd(const glif_table *t, const float *z, int32_t B, int32_t counts, int32_t mode,
                  float *I, void *ws, size_t ws_bytes, void *stream);
+/* No counterpart in the reference.  glif_syn_fwd for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * the same arguments, results and errors minus the workspace, whose place takes a static
+ * device array of GLIF_NOALLOC_SCRATCH_BYTES in the library -- one per GPU the library runs
+ * on, held until the process ends, its address looked up on the first call on each device.
+ * The forward needs about 12 bytes of scratch per column (n_cols): 32 MiB covers tables of up
+ * to ~2.7M columns (the 230k-neuron, 5-delay recurrent table has 1.15M); larger ones fail with
+ * GLIF_ENOMEM.  Calls on one GPU share the array: calls that overlap on one GPU (other
+ * streams, other threads) race, so serialise them.  The stream must belong to the calling
+ * thread's current device.  No allocation, no synchronisation. */
+#define GLIF_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int glif_syn_fwd_noalloc(const glif_table *t, const float *z, int32_t B, int32_t counts, int32_t mode,
+                         float *I, void *stream);
+
 /* Custom gradient (models.py:174-261): dy [B*n_post][n_basis] float32 device;
  * out dz [B][n_cols] (the gradient w.r.t. rec_z_buf, dense over all synapses; NULL
  * to skip) and dw [n_syn] (w.r.t. weight_values, reference order; NULL to skip),

@@ -49,6 +49,7 @@ SIGNATURES = {
     "glif_syn_workspace": (sz, [vp, i32]),
     "glif_syn_fwd": (C.c_int, [vp, vp, i32, i32, i32, vp, vp, sz, vp]),
     "glif_syn_bwd": (C.c_int, [vp, vp, vp, i32, i32, vp, vp, vp, sz, vp]),
+    "glif_syn_fwd_noalloc": (C.c_int, [vp, vp, i32, i32, i32, vp, vp]),
     "glif_cell_create": (C.c_int, [C.POINTER(CellConfig), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                    C.POINTER(vp)]),
     "glif_cell_destroy": (None, [vp]),

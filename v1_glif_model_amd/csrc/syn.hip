@@ -1,6 +1,7 @@
 // Op-level entry points of calculate_synaptic_currents (models.py:103-263):
 // forward (event push or deterministic pull) and the custom gradient.
 #include <algorithm>
+#include <mutex>
 
 #include "compact.h"
 #include "glif_internal.h"
@@ -216,7 +217,8 @@ struct SynWs {
     void *scratch;
 };
 
-static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes) {
+// with_G: the backward's projection G too (the forward does not use it)
+static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes, bool with_G = true) {
     Carver cv(ws, SIZE_MAX);
     SynWs w{};
     const int64_t pre_pad = (static_cast<int64_t>(t->n_pre) + 63) / 64 * 64;
@@ -225,39 +227,21 @@ static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes) {
     w.row_off = cv.take<int64_t>(2);
     w.cols = cv.take<int32_t>(t->n_cols);
     w.masks = cv.take<uint32_t>(t->n_cols);
-    w.G = cv.take<float>(static_cast<size_t>(t->n_post) * t->n_types * batch_pad(B));
     w.scratch = cv.take<char>(compact_scratch_bytes(1, t->n_cols));
+    if (with_G) w.G = cv.take<float>(static_cast<size_t>(t->n_post) * t->n_types * batch_pad(B));
     if (bytes) *bytes = cv.off;
     return w;
 }
 
-}  // namespace glif
-
-using namespace glif;
-
-extern "C" {
-
-size_t glif_syn_workspace(const glif_table *tt, int32_t B) {
-    if (!tt || B <= 0) return 0;
-    size_t bytes = 0;
-    carve_syn(nullptr, reinterpret_cast<const Table *>(tt), B, &bytes);
-    return bytes;
-}
-
-int glif_syn_fwd(const glif_table *tt, const float *z, int32_t B, int32_t counts, int32_t mode,
-                 float *I, void *ws, size_t ws_bytes, void *stream) {
-    if (!tt || !z || !I) return fail(GLIF_EINVAL, "NULL argument");
-    if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
-    const Table *t = reinterpret_cast<const Table *>(tt);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    ProfScope prof(kProfSynFwd, s);
+// The op forward on a carved workspace (every buffer it reads is written first by this call,
+// so nothing in it has to start at zero).  Launches only; no allocation, no synchronisation.
+static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, int32_t mode, float *I,
+                   const SynWs &w, hipStream_t s) {
     const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     const int64_t nI = static_cast<int64_t>(B) * t->n_post;
     if (mode == GLIF_MODE_DETERMINISTIC) {
         if (!counts && t->pidx && t->chunk_desc) {
             // the resident chunk pull over activity bitmaps built from z (one step, t = 0)
-            if (!ws || ws_bytes < glif_syn_workspace(tt, B)) return fail(GLIF_ENOMEM, "workspace too small");
-            SynWs w = carve_syn(ws, t, B, nullptr);
             const int32_t pre_pad = static_cast<int32_t>((static_cast<int64_t>(t->n_pre) + 63) / 64 * 64);
             PullArgs pa{};
             pa.t = 0;
@@ -306,10 +290,6 @@ int glif_syn_fwd(const glif_table *tt, const float *z, int32_t B, int32_t counts
         GLIF_HIP(hipGetLastError());
         return GLIF_OK;
     }
-    if (mode != GLIF_MODE_EVENT) return fail(GLIF_EINVAL, "unknown mode");
-    size_t need = glif_syn_workspace(tt, B);
-    if (!ws || ws_bytes < need) return fail(GLIF_ENOMEM, "workspace too small");
-    SynWs w = carve_syn(ws, t, B, nullptr);
     int rc = launch_fill_u32(I, 0u, static_cast<size_t>(nI) * t->n_basis, s);
     if (rc) return rc;
     rc = build_col_mask_list_f32(z, B, t->n_cols, w.row_off, w.cols, w.masks, w.scratch, s);
@@ -326,6 +306,83 @@ int glif_syn_fwd(const glif_table *tt, const float *z, int32_t B, int32_t counts
 #undef GLIF_PUSH
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;
+}
+
+constexpr int kMaxDevices = 64;
+
+}  // namespace glif
+
+// Scratch of glif_syn_fwd_noalloc: a file-scope device array, so the entry point needs no
+// allocation.  Every GPU the library runs on holds its own copy until the process ends.  In host
+// code this name is only a handle for hipGetSymbolAddress, never a device address.
+static __device__ __align__(256) char scratch[GLIF_NOALLOC_SCRATCH_BYTES];
+
+namespace glif {
+
+static std::mutex g_scratch_mu;
+static void *g_scratch_dev[kMaxDevices];
+
+// The device address of `scratch` on the current device, looked up once per device.
+static int scratch_on_current_device(void **out) {
+    int dev = -1;
+    GLIF_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(GLIF_EINVAL, "device index beyond the library's table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(GLIF_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return GLIF_OK;
+}
+
+}  // namespace glif
+
+using namespace glif;
+
+extern "C" {
+
+size_t glif_syn_workspace(const glif_table *tt, int32_t B) {
+    if (!tt || B <= 0) return 0;
+    size_t bytes = 0;
+    carve_syn(nullptr, reinterpret_cast<const Table *>(tt), B, &bytes);
+    return bytes;
+}
+
+int glif_syn_fwd(const glif_table *tt, const float *z, int32_t B, int32_t counts, int32_t mode,
+                 float *I, void *ws, size_t ws_bytes, void *stream) {
+    if (!tt || !z || !I) return fail(GLIF_EINVAL, "NULL argument");
+    if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
+    if (mode != GLIF_MODE_EVENT && mode != GLIF_MODE_DETERMINISTIC) return fail(GLIF_EINVAL, "unknown mode");
+    const Table *t = reinterpret_cast<const Table *>(tt);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // the dense-row pull (counts, or a table without the chunk form) needs no workspace
+    const bool needs_ws = mode == GLIF_MODE_EVENT || (!counts && t->pidx && t->chunk_desc);
+    if (needs_ws && (!ws || ws_bytes < glif_syn_workspace(tt, B))) return fail(GLIF_ENOMEM, "workspace too small");
+    ProfScope prof(kProfSynFwd, s);
+    return syn_fwd(t, z, B, counts, mode, I, carve_syn(ws, t, B, nullptr), s);
+}
+
+int glif_syn_fwd_noalloc(const glif_table *tt, const float *z, int32_t B, int32_t counts, int32_t mode, float *I,
+                         void *stream) {
+    if (!tt || !z || !I) return fail(GLIF_EINVAL, "NULL argument");
+    if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
+    if (mode != GLIF_MODE_EVENT && mode != GLIF_MODE_DETERMINISTIC) return fail(GLIF_EINVAL, "unknown mode");
+    const Table *t = reinterpret_cast<const Table *>(tt);
+    size_t need = 0;
+    carve_syn(nullptr, t, B, &need, false);
+    if (need > GLIF_NOALLOC_SCRATCH_BYTES)
+        return fail(GLIF_ENOMEM, "glif_syn_fwd_noalloc: this table's forward at batch " + std::to_string(B) +
+                                     " needs " + std::to_string(need) + " bytes of scratch, above the " +
+                                     std::to_string(GLIF_NOALLOC_SCRATCH_BYTES) +
+                                     "-byte static array; call glif_syn_fwd with a workspace instead");
+    void *p = nullptr;
+    const int rc = scratch_on_current_device(&p);
+    if (rc) return rc;
+    return syn_fwd(t, z, B, counts, mode, I, carve_syn(p, t, B, nullptr, false), static_cast<hipStream_t>(stream));
 }
 
 int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t B, int32_t counts,
