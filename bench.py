@@ -55,6 +55,10 @@ def _args():
                     help="synapse types of the generated network (the configurations use 5; the "
                          "reference's basis table has 121)")
     ap.add_argument("--n-basis", type=int, default=None, help="receptors (basis functions) per neuron")
+    ap.add_argument("--target-rate", type=float, default=None, metavar="HZ",
+                    help="scale all three weight populations by one factor, found by bisection on "
+                         "deterministic rollouts, so the network fires at this mean rate (e.g. 5 for "
+                         "the many-type network, whose weights are not calibrated)")
     ap.add_argument("--dense-basis", action="store_true",
                     help="a dense random basis table instead of the identity (every type feeds every "
                          "receptor, as in the reference's table)")
@@ -101,6 +105,64 @@ def load_traffic(name):
         return json.load(f)
 
 
+class RateCalibrator:
+    """One global factor on all three weight populations of a cell, set by bisection in log
+    space on deterministic rollouts so that the mean firing rate meets a target (the
+    configurations fix the network's shape, not its rate; the factor is reported)."""
+
+    def __init__(self, cell, lgn, bkg):
+        import torch
+        self.cell, self.lgn, self.bkg = cell, lgn, bkg
+        self.ws = (cell.recurrent_weight_values, cell.input_weight_values, cell.bkg_input_weights)
+        self.base = [w.detach().clone() for w in self.ws]
+        B, N = lgn.shape[1], cell.tables.n_neurons
+        self.sc = torch.zeros((B, N), dtype=torch.int32, device=cell.device)
+
+    def set_scale(self, f):
+        import torch
+        with torch.no_grad():
+            for w, b0 in zip(self.ws, self.base):
+                w.copy_(b0 * f)
+        self.cell.refresh_weights(force=True)
+
+    def rate_hz(self, f, Tp):
+        import torch
+        self.set_scale(f)
+        self.sc.zero_()
+        self.cell.rollout(self.lgn[:Tp], self.bkg[:Tp], record_z=False, record_v=False, spike_count=self.sc,
+                          mode="deterministic")
+        torch.cuda.synchronize()
+        return float(self.sc.sum().item()) / self.sc.numel() / Tp * 1000.0
+
+    def find_scale(self, target, Tp):   # the whole rollout: the rate ramps up from rest
+        import numpy as np
+        lo, hi = None, None
+        f = 1.0
+        r = self.rate_hz(f, Tp)
+        for _ in range(10):   # bracket
+            if r < target:
+                lo = (f, r)
+                if hi is not None:
+                    break
+                f *= 2.0
+            else:
+                hi = (f, r)
+                if lo is not None:
+                    break
+                f *= 0.5
+            r = self.rate_hz(f, Tp)
+        if lo is None or hi is None:
+            return f
+        for _ in range(7):   # bisect in log space
+            f = float(np.sqrt(lo[0] * hi[0]))
+            r = self.rate_hz(f, Tp)
+            if r < target:
+                lo = (f, r)
+            else:
+                hi = (f, r)
+        return float(np.sqrt(lo[0] * hi[0]))
+
+
 def sweep_rates(args):
     """Config 4: forward throughput of the event push and the deterministic row pull
     at several mean firing rates.  One global factor scales all three weight
@@ -123,50 +185,12 @@ def sweep_rates(args):
     dev = cell.device
     lgn = torch.tensor(lgn_np, device=dev)
     bkg = torch.tensor(bkg_np, device=dev)
-    ws_all = (cell.recurrent_weight_values, cell.input_weight_values, cell.bkg_input_weights)
-    base = [w.detach().clone() for w in ws_all]
-    sc = torch.zeros((B, N), dtype=torch.int32, device=dev)
+    cal = RateCalibrator(cell, lgn, bkg)
+    sc = cal.sc
+    set_scale = cal.set_scale
 
-    def set_scale(f):
-        with torch.no_grad():
-            for w, b0 in zip(ws_all, base):
-                w.copy_(b0 * f)
-        cell.refresh_weights(force=True)
-
-    def rate_hz(f, Tp):
-        set_scale(f)
-        sc.zero_()
-        cell.rollout(lgn[:Tp], bkg[:Tp], record_z=False, record_v=False, spike_count=sc,
-                     mode="deterministic")
-        torch.cuda.synchronize()
-        return float(sc.sum().item()) / (B * N * Tp) * 1000.0
-
-    def find_scale(target, Tp=T):   # the whole rollout: the rate ramps up from rest
-        lo, hi = None, None
-        f = 1.0
-        r = rate_hz(f, Tp)
-        for _ in range(10):   # bracket
-            if r < target:
-                lo = (f, r)
-                if hi is not None:
-                    break
-                f *= 2.0
-            else:
-                hi = (f, r)
-                if lo is not None:
-                    break
-                f *= 0.5
-            r = rate_hz(f, Tp)
-        if lo is None or hi is None:
-            return f
-        for _ in range(7):   # bisect in log space
-            f = float(np.sqrt(lo[0] * hi[0]))
-            r = rate_hz(f, Tp)
-            if r < target:
-                lo = (f, r)
-            else:
-                hi = (f, r)
-        return float(np.sqrt(lo[0] * hi[0]))
+    def find_scale(target, Tp=T):
+        return cal.find_scale(target, Tp)
 
     def timed(mode, reps=2):
         ws = cell.workspace(B, T)
@@ -312,6 +336,13 @@ def main():
     N, S = tb.n_neurons, tb.rec.n_syn
     lgn = torch.tensor(lgn_np, device=dev)
     bkg = torch.tensor(bkg_np, device=dev)
+    weight_factor = None
+    if args.target_rate:
+        cal = RateCalibrator(cell, lgn, bkg)
+        weight_factor = cal.find_scale(args.target_rate, T)
+        cal.set_scale(weight_factor)
+        print(json.dumps({"calibration": {"target_hz": args.target_rate, "weight_factor": round(weight_factor, 4)}}),
+              file=sys.stderr, flush=True)
     ws = cell.workspace(B, T)
     spike_count = torch.zeros((B, N), dtype=torch.int32, device=dev)
     zero = cell.zero_state(B)
@@ -469,7 +500,13 @@ def main():
         from oracle.cpu import OracleCell
         t_a = min(max(args.cpu_start, 0), T - 1)
         Tc = min(args.cpu_steps, T - t_a)
-        oc = OracleCell(tb, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.5, pseudo_gauss=True)
+        tb_cpu = tb
+        if weight_factor:
+            import dataclasses
+            f32 = np.float32
+            tb_cpu = dataclasses.replace(tb, **{k: dataclasses.replace(getattr(tb, k), weight=(
+                getattr(tb, k).weight * f32(weight_factor)).astype(f32)) for k in ("rec", "lgn", "bkg")})
+        oc = OracleCell(tb_cpu, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.5, pseudo_gauss=True)
         st_dev = [z.clone() for z in zero]
         if t_a > 0:
             cell.rollout(lgn[:t_a], bkg[:t_a], state=st_dev, record_z=False, record_v=False, mode="deterministic")
@@ -524,6 +561,7 @@ def main():
                    "bkg_synapses": tb.bkg.n_syn, "batch": B, "seq_len": T, "mode": args.mode,
                    "syn_types": int(tb.basis.shape[0]), "receptors": int(tb.n_basis),
                    "basis": "dense" if args.dense_basis else "identity",
+                   "weight_factor": round(weight_factor, 4) if weight_factor else None,
                    "loss": None if args.forward_only else args.loss},
         "roofline": roofline,
         "cpu_baseline": cpu,

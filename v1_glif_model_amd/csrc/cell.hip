@@ -575,6 +575,7 @@ constexpr int kAdjMaxWin = 3;  // reverse ticks per window (3 when 3 * B <= 16, 
 struct AdjArgs {
     CellConst k;
     int32_t t0, nw, T, ring, R;
+    int32_t tc;      // types per staged chunk of G rows
     int32_t vmode;   // fused voltage regularization (0 off, 1 range, 2 threshold)
     float vscale;    // its cost / (T * B * selected neurons)
     const uint8_t *vmask;  // [N] the selected neurons (core mask), or nullptr: all
@@ -599,39 +600,32 @@ struct AdjArgs {
 //   dy_{t-2} = (gR_{t-2} * p0) * lr_scale;  G[s][n][w*B + b] = sum_r dy_r basis[s][r]
 // dZ_s for s >= T-2 is zero (nothing downstream of I_{T-2}, I_{T-1} is observed).
 // The ticks of one window only read dZ of earlier (later-in-time) windows.
-// STAGE: a workgroup takes nr = kBlock / B neurons x all B batch entries (thread
-// b * nr + i -> (b, n0 + i): every [B][N] access is a few contiguous runs) and keeps
-// its G rows in LDS until the window's ticks are done, then writes whole rows.
-// Otherwise: thread per (n, b), batch fastest, G written in place.
-template <int NB, bool STAGE>
+// A workgroup takes nr = kBlock / B neurons x all B batch entries (thread b * nr + i ->
+// (b, n0 + i): every [B][N] access is a few contiguous runs).  The window's dy stay in
+// registers until its ticks are done; then the G rows of the workgroup's neurons go out a
+// chunk of a.tc types at a time through LDS, each type's rows as one contiguous run (with 121
+// types x 4 receptors G is ~0.5 GB per window: written row by row, not element by element).
+template <int NB>
 __device__ inline void adj_body(const AdjArgs &a, int64_t bid) {
     extern __shared__ float lds_f[];
     float *basis_lds = lds_f;
     const CellConst &k = a.k;
     load_basis_lds(basis_lds, a.basis, k.n_types * k.nb);
     const int64_t BN = static_cast<int64_t>(k.B) * k.N;
-    int n, b;
-    float *Gl = nullptr;
+    float *Gl = lds_f + k.n_types * k.nb;   // [tc][nr][R]
     const int nr = kBlock / k.B;
     const int32_t n0 = static_cast<int32_t>(bid) * nr;
-    if (STAGE) {
-        Gl = lds_f + k.n_types * k.nb;
-        const int rows = k.n_types * nr * a.R;
-        for (int i = threadIdx.x; i < rows; i += blockDim.x) Gl[i] = 0.0f;
-        __syncthreads();
-        b = static_cast<int>(threadIdx.x) / nr;
-        n = n0 + static_cast<int>(threadIdx.x) - b * nr;
-    } else {
-        const int64_t gt = bid * blockDim.x + threadIdx.x;
-        // batch fastest: neighbouring lanes write neighbouring G entries
-        n = static_cast<int>(gt / k.B);
-        b = static_cast<int>(gt - static_cast<int64_t>(n) * k.B);
-    }
-    const bool live = STAGE ? (b < k.B && n < k.N) : (static_cast<int64_t>(n) * k.B + b < BN);
-    if (!STAGE && !live) return;
+    const int b = static_cast<int>(threadIdx.x) / nr;
+    const int n = n0 + static_cast<int>(threadIdx.x) - b * nr;
+    const bool live = b < k.B && n < k.N;
+    constexpr int nb = NB;
+    float dyw[kAdjMaxWin][kMaxBasis];
+#pragma unroll
+    for (int w = 0; w < kAdjMaxWin; ++w)
+#pragma unroll
+        for (int q = 0; q < kMaxBasis; ++q) dyw[w][q] = 0.0f;
     if (live) {
     const int64_t bn = static_cast<int64_t>(b) * k.N + n;
-    constexpr int nb = NB;
     const int64_t DN = static_cast<int64_t>(k.D) * k.N;
     float gVc = a.gV[bn];
     float gP[kMaxBasis], gR[kMaxBasis];
@@ -659,21 +653,10 @@ __device__ inline void adj_body(const AdjArgs &a, int64_t bid) {
         if (a.vmode && (!a.vmask || a.vmask[n])) gV = gV + vpenalty_grad(a.vmode, vsv) * a.vscale;
         gV = gV + (gVc * decay) * k.om;
         gVc = (k.hard_reset && refr) ? 0.0f : gV;
-        float dy[kMaxBasis];
         for (int q = 0; q < nb; ++q) {
             gP[q] = gP[q] * k.sd[q] + gVc * cfn;
             gR[q] = gR[q] * k.sd[q] + gP[q] * k.dtsd[q];
-            dy[q] = (gR[q] * k.p0[q]) * k.lr;
-        }
-        const int e = w * k.B + b;
-        for (int s = 0; s < k.n_types; ++s) {
-            const float *bs = basis_lds + s * nb;
-            float g = dy[0] * bs[0];
-            for (int r = 1; r < nb; ++r) g = g + dy[r] * bs[r];
-            if (STAGE)
-                Gl[(s * nr + (n - n0)) * a.R + e] = g;
-            else
-                a.G[(static_cast<int64_t>(s) * k.N + n) * a.R + e] = g;
+            dyw[w][q] = (gR[q] * k.p0[q]) * k.lr;
         }
     };
     auto refbit = [&](int t) {
@@ -718,7 +701,9 @@ __device__ inline void adj_body(const AdjArgs &a, int64_t bid) {
             tick(w, gz, rf[w], vs[w], gvw[w]);
         }
     } else {
-        for (int w = 0; w < a.nw; ++w) {
+#pragma unroll
+        for (int w = 0; w < kAdjMaxWin; ++w) {
+            if (w >= a.nw) break;
             const int t = a.t0 - w;
             float gz = 0.0f;
             for (int d = k.D; d >= 1; --d) {
@@ -740,21 +725,39 @@ __device__ inline void adj_body(const AdjArgs &a, int64_t bid) {
         a.gR[static_cast<int64_t>(q) * BN + bn] = gR[q];
     }
     }  // live
-    if (STAGE) {
+    // G[s][n][w*B + b] = sum_r dy_r basis[s][r], a.tc types at a time (elements of ticks past
+    // nw and the row padding are zero)
+    const int nn = min(nr, k.N - n0);
+    const int per_type = nn * a.R;
+    for (int s0 = 0; s0 < k.n_types; s0 += a.tc) {
+        const int ns = min(a.tc, k.n_types - s0);
+        for (int i = threadIdx.x; i < ns * nr * a.R; i += blockDim.x) Gl[i] = 0.0f;
         __syncthreads();
-        // whole G rows of this workgroup's neurons (padding elements stay zero)
-        const int nn = min(nr, k.N - n0);
-        const int per_type = nn * a.R;
-        for (int i = threadIdx.x; i < k.n_types * per_type; i += blockDim.x) {
-            const int s = i / per_type, rem = i - s * per_type;
-            a.G[(static_cast<int64_t>(s) * k.N + n0) * a.R + rem] = Gl[s * nr * a.R + rem];
+        if (live) {
+            for (int si = 0; si < ns; ++si) {
+                const float *bs = basis_lds + (s0 + si) * nb;
+#pragma unroll
+                for (int w = 0; w < kAdjMaxWin; ++w) {
+                    if (w >= a.nw) break;
+                    float g = dyw[w][0] * bs[0];
+#pragma unroll
+                    for (int r = 1; r < nb; ++r) g = g + dyw[w][r] * bs[r];
+                    Gl[(si * nr + (n - n0)) * a.R + w * k.B + b] = g;
+                }
+            }
         }
+        __syncthreads();
+        for (int i = threadIdx.x; i < ns * per_type; i += blockDim.x) {
+            const int si = i / per_type, rem = i - si * per_type;
+            a.G[(static_cast<int64_t>(s0 + si) * k.N + n0) * a.R + rem] = Gl[si * nr * a.R + rem];
+        }
+        __syncthreads();
     }
 }
 
-template <int NB, bool STAGE>
+template <int NB>
 __global__ void __launch_bounds__(kBlock) k_adj(AdjArgs a) {
-    adj_body<NB, STAGE>(a, blockIdx.x);
+    adj_body<NB>(a, blockIdx.x);
 }
 
 // ------------------------------------------------------ backward synapses ----
@@ -976,11 +979,11 @@ struct DwPrev {
     int32_t rec_blocks, lgn_blocks;
 };
 
-template <int NB, bool STAGE>
+template <int NB>
 __global__ void __launch_bounds__(kBlock) k_adj_dw(AdjArgs a, int adj_blocks, DwPrev p) {
     const int64_t bid = blockIdx.x;
     if (bid < adj_blocks) {
-        adj_body<NB, STAGE>(a, bid);
+        adj_body<NB>(a, bid);
     } else if (bid < adj_blocks + p.rec_blocks) {
         rec_dw_body(p.da, p.act, bid - adj_blocks);
     } else {
@@ -1020,31 +1023,33 @@ static void launch_step(const StepArgs &sa, int nb, dim3 grid, size_t lds, hipSt
     }
 }
 
-constexpr size_t kAdjStageLds = 64 * 1024;  // LDS budget of the staged adjoint
+constexpr size_t kAdjStageLds = 64 * 1024;  // LDS budget of the adjoint's G staging
 
-static size_t adj_stage_lds(const CellConst &k, int R) {
+// Types per staged chunk of the adjoint (as many as fit the budget beside the basis table).
+static int adj_type_chunk(const CellConst &k, int R) {
+    const size_t nr = kBlock / k.B;
+    const size_t basis = sizeof(float) * static_cast<size_t>(k.n_types) * k.nb;
+    const size_t per_type = sizeof(float) * nr * R;
+    const size_t fit = kAdjStageLds > basis ? (kAdjStageLds - basis) / per_type : 0;
+    return static_cast<int>(std::max<size_t>(1, std::min<size_t>(fit, static_cast<size_t>(k.n_types))));
+}
+
+static size_t adj_stage_lds(const CellConst &k, int R, int tc) {
     const int nr = kBlock / k.B;
-    return sizeof(float) * (static_cast<size_t>(k.n_types) * k.nb + static_cast<size_t>(k.n_types) * nr * R);
+    return sizeof(float) * (static_cast<size_t>(k.n_types) * k.nb + static_cast<size_t>(tc) * nr * R);
 }
 
 // prev: the weight-gradient passes of the previous window to run in the same launch, or null
-static void launch_adj(const AdjArgs &aa, int nb, size_t lds, hipStream_t s, const DwPrev *prev = nullptr) {
+static void launch_adj(const AdjArgs &aa, int nb, hipStream_t s, const DwPrev *prev = nullptr) {
     const CellConst &k = aa.k;
-    const size_t slds = adj_stage_lds(k, aa.R);
-    const bool stage = slds <= kAdjStageLds;
-    const int adj_blocks = stage ? ceil_div(k.N, kBlock / k.B) : ceil_div(static_cast<int64_t>(k.B) * k.N, kBlock);
-    const size_t use = stage ? slds : lds;
+    const size_t use = adj_stage_lds(k, aa.R, aa.tc);
+    const int adj_blocks = ceil_div(k.N, kBlock / k.B);
     const dim3 grid(adj_blocks + (prev ? prev->rec_blocks + prev->lgn_blocks : 0));
     switch (nb) {
-#define GLIF_ADJ(NB)                                                                                 \
-    case NB:                                                                                         \
-        if (prev) {                                                                                  \
-            if (stage) hipLaunchKernelGGL((k_adj_dw<NB, true>), grid, dim3(kBlock), use, s, aa, adj_blocks, *prev); \
-            else hipLaunchKernelGGL((k_adj_dw<NB, false>), grid, dim3(kBlock), use, s, aa, adj_blocks, *prev); \
-        } else {                                                                                     \
-            if (stage) hipLaunchKernelGGL((k_adj<NB, true>), grid, dim3(kBlock), use, s, aa);        \
-            else hipLaunchKernelGGL((k_adj<NB, false>), grid, dim3(kBlock), use, s, aa);             \
-        }                                                                                            \
+#define GLIF_ADJ(NB)                                                                                   \
+    case NB:                                                                                           \
+        if (prev) hipLaunchKernelGGL((k_adj_dw<NB>), grid, dim3(kBlock), use, s, aa, adj_blocks, *prev); \
+        else hipLaunchKernelGGL((k_adj<NB>), grid, dim3(kBlock), use, s, aa);                           \
         break;
         GLIF_ADJ(1) GLIF_ADJ(2) GLIF_ADJ(3) GLIF_ADJ(4) GLIF_ADJ(5) GLIF_ADJ(6) GLIF_ADJ(7) GLIF_ADJ(8)
 #undef GLIF_ADJ
@@ -1394,6 +1399,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     aa.T = T;
     aa.ring = ring;
     aa.R = Rg;
+    aa.tc = adj_type_chunk(k, Rg);
     aa.vmode = c->vloss_mode;
     aa.vmask = c->vloss_mask;
     aa.vscale = c->vloss_mode ? c->vloss_cost / (static_cast<float>(T) * static_cast<float>(B) *
@@ -1463,7 +1469,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         aa.nw = nw;
         {
             ProfScope p(kProfAdj, s);
-            launch_adj(aa, c->nb, lds, s, have_prev ? &prev : nullptr);
+            launch_adj(aa, c->nb, s, have_prev ? &prev : nullptr);
         }
         ca.n_elem = ga.n_elem = da.n_elem = nw * B;
         act.s0 = s0;
