@@ -62,6 +62,11 @@ def _args():
     ap.add_argument("--dense-basis", action="store_true",
                     help="a dense random basis table instead of the identity (every type feeds every "
                          "receptor, as in the reference's table)")
+    ap.add_argument("--expand-receptors", action="store_true",
+                    help="receptor-space form of a many-type network: every synapse becomes n_basis synapses "
+                         "(one per receptor r, weight w * basis[syn_id][r]) over an identity basis, so the "
+                         "backward's projection G holds dy itself (n_basis rows per neuron) instead of one "
+                         "row per synapse type; same currents, more synapses")
     ap.add_argument("--op", action="store_true",
                     help="time the op-level entry points instead (calculate_synaptic_currents forward in "
                          "both modes and its custom gradient) on the config-2 recurrent table, B=5, "
@@ -326,6 +331,8 @@ def main():
     B = cfg.batch
     t_gen = time.time()
     net = sy.make_network(cfg, seed=0, dense_basis=args.dense_basis)
+    if args.expand_receptors:
+        net = sy.expand_receptors(net)
     lgn_np, bkg_np = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
     cell = V1Column(net, mode=args.mode, gauss_std=0.5, dampening_factor=0.5, train_recurrent_per_type=False,
                     recurrent_dampening_factor=0.5, voltage_gradient_dampening=0.5,
@@ -560,7 +567,7 @@ def main():
                    "neurons": N, "recurrent_synapses": S, "lgn_synapses": tb.lgn.n_syn,
                    "bkg_synapses": tb.bkg.n_syn, "batch": B, "seq_len": T, "mode": args.mode,
                    "syn_types": int(tb.basis.shape[0]), "receptors": int(tb.n_basis),
-                   "basis": "dense" if args.dense_basis else "identity",
+                   "basis": ("dense" if args.dense_basis else "identity") + (", receptor-expanded" if args.expand_receptors else ""),
                    "weight_factor": round(weight_factor, 4) if weight_factor else None,
                    "loss": None if args.forward_only else args.loss},
         "roofline": roofline,

@@ -39,7 +39,7 @@ from typing import Optional
 import numpy as np
 
 __all__ = ["SynthConfig", "CONFIGS", "make_network", "make_inputs", "make_rate_targets",
-           "make_cell_types", "make_type_rates", "config"]
+           "make_cell_types", "make_type_rates", "config", "expand_receptors"]
 
 
 @dataclasses.dataclass(frozen=True)
@@ -255,4 +255,30 @@ def make_type_rates(seed: int = 4, n_units: int = 200):
     for name, _, mean_hz in _EXC_TYPES + _INH_TYPES:
         r = rng.lognormal(math.log(mean_hz) - 0.5, 1.0, n_units) / 1000.0
         out[name] = np.append(r, 0.0)
+    return out
+
+
+def expand_receptors(net):
+    """The network with each synapse split into one synapse per receptor r (syn_id r, weight
+    w * basis[syn_id][r], the same delay) over an identity basis: the same currents (each
+    receptor's term is the reference's product w * basis[syn_id][r], models.py:154), with the
+    backward's per-type projection reduced to the receptor rows of dy."""
+    basis = np.asarray(net["basis"], np.float32)
+    nb = basis.shape[1]
+
+    def split(pop, with_delays):
+        sid = np.asarray(pop["syn_ids"]).astype(np.int64)
+        w = np.asarray(pop["weights"], np.float32)
+        out = dict(pop, indices=np.repeat(np.asarray(pop["indices"]), nb, axis=0),
+                   weights=(w[:, None] * basis[sid]).astype(np.float32).reshape(-1),
+                   syn_ids=np.tile(np.arange(nb, dtype=np.uint8), sid.size))
+        if with_delays:
+            out["delays"] = np.repeat(np.asarray(pop["delays"]), nb)
+        return out
+
+    out = dict(net)
+    out["network"] = dict(net["network"], synapses=split(net["network"]["synapses"], True))
+    out["lgn_input"] = split(net["lgn_input"], False)
+    out["bkg_input"] = split(net["bkg_input"], False)
+    out["basis"] = np.eye(nb, dtype=np.float32)
     return out
