@@ -67,6 +67,14 @@ def _args():
                          "(one per receptor r, weight w * basis[syn_id][r]) over an identity basis, so the "
                          "backward's projection G holds dy itself (n_basis rows per neuron) instead of one "
                          "row per synapse type; same currents, more synapses")
+    ap.add_argument("--class-types", type=int, default=None, metavar="K",
+                    help="synapse types by (presynaptic class, postsynaptic class) over K neuron classes "
+                         "(K*K types, dense random basis, inputs of class 0), the structure of the "
+                         "reference's 121-type table: each neuron receives at most K of the types")
+    ap.add_argument("--g-layout", default="auto", choices=["auto", "type-major"],
+                    help="rows of the backward's per-type projection G: auto (compact rows, one per type "
+                         "reaching the neuron, when no neuron receives more than 3/4 of the types) or "
+                         "type-major (a row per type and neuron)")
     ap.add_argument("--op", action="store_true",
                     help="time the op-level entry points instead (calculate_synaptic_currents forward in "
                          "both modes and its custom gradient) on the config-2 recurrent table, B=5, "
@@ -331,12 +339,16 @@ def main():
     B = cfg.batch
     t_gen = time.time()
     net = sy.make_network(cfg, seed=0, dense_basis=args.dense_basis)
+    if args.class_types:
+        net = sy.class_types(net, n_classes=args.class_types)
     if args.expand_receptors:
         net = sy.expand_receptors(net)
     lgn_np, bkg_np = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
     cell = V1Column(net, mode=args.mode, gauss_std=0.5, dampening_factor=0.5, train_recurrent_per_type=False,
                     recurrent_dampening_factor=0.5, voltage_gradient_dampening=0.5,
                     pseudo_gauss=True, train_input=True)
+    if args.g_layout == "type-major":
+        cell.set_g_layout(False)
     t_gen = time.time() - t_gen
     dev = cell.device
     tb = cell.tables
@@ -567,7 +579,10 @@ def main():
                    "neurons": N, "recurrent_synapses": S, "lgn_synapses": tb.lgn.n_syn,
                    "bkg_synapses": tb.bkg.n_syn, "batch": B, "seq_len": T, "mode": args.mode,
                    "syn_types": int(tb.basis.shape[0]), "receptors": int(tb.n_basis),
-                   "basis": ("dense" if args.dense_basis else "identity") + (", receptor-expanded" if args.expand_receptors else ""),
+                   "basis": ("dense" if args.dense_basis or args.class_types else "identity")
+                            + (f", types by {args.class_types} neuron classes" if args.class_types else "")
+                            + (", receptor-expanded" if args.expand_receptors else ""),
+                   "g_rows_per_neuron": cell.g_layout()[0],
                    "weight_factor": round(weight_factor, 4) if weight_factor else None,
                    "loss": None if args.forward_only else args.loss},
         "roofline": roofline,

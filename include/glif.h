@@ -198,6 +198,17 @@ int glif_cell_set_voltage_mask(glif_cell *c, const uint8_t *mask, int32_t n_sele
  * gz_neuron over those ticks only.  Default 0, 0 (every tick). */
 int glif_cell_set_trim(glif_cell *c, int32_t pre_delay, int32_t post_delay);
 
+/* Layout of the backward's per-synapse-type projection G (no counterpart in the reference,
+ * whose gradient projects dy through the basis per receptor, models.py:182-241): rows per
+ * post neuron (n_types, or fewer when no post receives more than three quarters of the
+ * types: then *compact = 1 and each post keeps rows for its own types only). */
+int glif_cell_g_layout(const glif_cell *c, int32_t *rows_per_post, int32_t *compact);
+/* Choose the layout (for timing the two against each other): compact 0 = type-major rows,
+ * 1 = compact rows (GLIF_EINVAL when the cell has none).  The workspace size follows the
+ * layout: query glif_cell_workspace again, and run glif_cell_backward only after a forward
+ * made under the same layout. */
+int glif_cell_set_g_layout(glif_cell *c, int32_t compact);
+
 /* ----------------------------------------------------------------- losses -----
  * Rate-distribution loss (SpikeRateDistributionTarget.__call__, loss_functions.py:873-889
  * -> compute_spike_rate_target_loss :634-664 -> compute_spike_rate_distribution_loss

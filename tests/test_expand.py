@@ -35,3 +35,28 @@ def test_expanded_network_has_the_same_currents_and_gradients():
     b = tb.basis[tb.rec.syn_id.astype(np.int64)]                 # [S, nb]
     dw_chain = (dw1.reshape(-1, nb).astype(np.float64) * b).sum(1)
     assert np.max(np.abs(dw_chain - dw0)) <= 1e-5 * np.abs(dw0).max()
+
+
+def test_class_types_structure():
+    """synthetic.class_types: syn_id = pre_class * K + post_class (class 0 for the inputs), so a
+    neuron receives at most K distinct types out of K * K, and the tables keep every synapse."""
+    K = 11
+    cfg = tiny_config(n=400, fanin=40, delays=3)
+    net = sy.make_network(cfg, seed=5)
+    ct = sy.class_types(net, n_classes=K)
+    cls = ct["neuron_class"]
+    n_exc = net["network"]["n_exc"]
+    assert set(np.unique(cls[:n_exc])) <= set(range(1, K // 2 + 1))
+    assert set(np.unique(cls[n_exc:])) <= set(range(K // 2 + 1, K))
+    assert ct["basis"].shape == (K * K, net["basis"].shape[1])
+    seen = [set() for _ in range(cfg.n_neurons)]
+    for pop, src in ((ct["network"]["synapses"], cls), (ct["lgn_input"], None), (ct["bkg_input"], None)):
+        post, pre = np.asarray(pop["indices"]).T
+        sid = np.asarray(pop["syn_ids"]).astype(np.int64)
+        np.testing.assert_array_equal(sid % K, cls[post])
+        np.testing.assert_array_equal(sid // K, src[pre] if src is not None else 0)
+        for p, s in zip(post, sid):
+            seen[p].add(int(s))
+    assert max(len(s) for s in seen) <= K
+    tb = build_cell_tables(ct)
+    assert tb.rec.n_syn == len(net["network"]["synapses"]["weights"])

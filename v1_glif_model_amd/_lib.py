@@ -60,6 +60,8 @@ SIGNATURES = {
     "glif_cell_set_voltage_loss": (C.c_int, [vp, i32, C.c_float]),
     "glif_cell_voltage_loss": (C.c_int, [vp, i32, i32, vp, vp, sz, vp]),
     "glif_cell_set_trim": (C.c_int, [vp, i32, i32]),
+    "glif_cell_g_layout": (C.c_int, [vp, vp, vp]),
+    "glif_cell_set_g_layout": (C.c_int, [vp, i32]),
     "glif_cell_set_voltage_mask": (C.c_int, [vp, vp, i32]),
     "glif_rate_loss_workspace": (sz, [i64]),
     "glif_rate_mse_workspace": (sz, []),

@@ -57,7 +57,8 @@ struct CellWs {
     uint8_t *bkg_cnt;   // [T][B][n_bkg]
     void *scratch;
     float *dZ;          // [ring][B][D * N]
-    float *G;           // [2][n_types][N][R]   (windows alternate between the two)
+    float *G;           // [2][n_types][N][R], or [2][N][g_rows][R] with compact rows
+                        // (windows alternate between the two)
     float *gV;          // [B][N]
     float *gP, *gR;     // [nb][B][N]
     float *vloss_part;  // [kVlossBlocks] partial sums of the voltage penalty
@@ -100,7 +101,7 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.bkg_cnt = cv.take<uint8_t>(static_cast<size_t>(T) * B * nk);
     w.scratch = cv.take<char>(std::max(compact_scratch_bytes(T, nl), compact_scratch_bytes(T, nk)));
     w.dZ = cv.take<float>(static_cast<size_t>(ring_size(c)) * B * c->D * c->N);
-    w.G = cv.take<float>(2 * static_cast<size_t>(c->N) * c->n_types * g_row(Wwin, B));
+    w.G = cv.take<float>(2 * static_cast<size_t>(c->N) * c->g_rows * g_row(Wwin, B));
     w.gV = cv.take<float>(BN);
     w.gP = cv.take<float>(BN * c->nb);
     w.gR = cv.take<float>(BN * c->nb);
@@ -588,6 +589,8 @@ struct AdjArgs {
     const float *decay, *cf;
     float *G;
     const float *basis;
+    int32_t gk;             // compact G rows per post, 0: type-major rows
+    const uint8_t *gtype;   // [N][gk] syn_id of each compact row, 0xFF: none
 };
 
 // Lagged reverse ticks t = t0, t0-1, .., t0-nw+1 (nw <= window width; every t >= 2).
@@ -725,9 +728,42 @@ __device__ inline void adj_body(const AdjArgs &a, int64_t bid) {
         a.gR[static_cast<int64_t>(q) * BN + bn] = gR[q];
     }
     }  // live
+    const int nn = min(nr, k.N - n0);
+    if (a.gk) {
+        // compact rows: G[n * gk + q][w*B + b] = sum_r dy_r basis[gtype[n][q]][r], a.tc ranks at
+        // a time; a neuron's rows of one chunk are one contiguous run (the whole block's rows
+        // are one run when the chunk holds every rank)
+        for (int q0 = 0; q0 < a.gk; q0 += a.tc) {
+            const int nq = min(a.tc, a.gk - q0);
+            const int per_n = nq * a.R;
+            for (int i = threadIdx.x; i < nr * per_n; i += blockDim.x) Gl[i] = 0.0f;
+            __syncthreads();
+            if (live) {
+                for (int qi = 0; qi < nq; ++qi) {
+                    const int s = a.gtype[static_cast<int64_t>(n) * a.gk + q0 + qi];
+                    if (s == 0xFF) continue;
+                    const float *bs = basis_lds + s * nb;
+#pragma unroll
+                    for (int w = 0; w < kAdjMaxWin; ++w) {
+                        if (w >= a.nw) break;
+                        float g = dyw[w][0] * bs[0];
+#pragma unroll
+                        for (int r = 1; r < nb; ++r) g = g + dyw[w][r] * bs[r];
+                        Gl[(n - n0) * per_n + qi * a.R + w * k.B + b] = g;
+                    }
+                }
+            }
+            __syncthreads();
+            for (int i = threadIdx.x; i < nn * per_n; i += blockDim.x) {
+                const int ni = i / per_n, rem = i - ni * per_n;
+                a.G[(static_cast<int64_t>(n0 + ni) * a.gk + q0) * a.R + rem] = Gl[i];
+            }
+            __syncthreads();
+        }
+        return;
+    }
     // G[s][n][w*B + b] = sum_r dy_r basis[s][r], a.tc types at a time (elements of ticks past
     // nw and the row padding are zero)
-    const int nn = min(nr, k.N - n0);
     const int per_type = nn * a.R;
     for (int s0 = 0; s0 < k.n_types; s0 += a.tc) {
         const int ns = min(a.tc, k.n_types - s0);
@@ -812,9 +848,12 @@ __global__ void __launch_bounds__(kBlock) k_bwd_rec_gs(GsArgs a, ActWin act) {
 // sub-groups walk the column-grouped synapses of the active columns, a lane per synapse,
 // adding G[sid][post][e] for the set elements e in ascending order (reverse time, then
 // batch).
+// G row of entry p = (p >> 24) * hm + (p & kLow24) * lm: {syn_id | post} entries with
+// type-major rows (hm = n_post, lm = 1), {rank | post} entries with compact rows (hm = 1,
+// lm = rows per post).
 struct RecDwArgs {
     int64_t n_cols;
-    int32_t n_elem, n_post, R;
+    int32_t n_elem, hm, lm, R;
     const int32_t *col_ptr;
     const uint32_t *ps;
     const float *G;
@@ -872,7 +911,7 @@ __device__ inline void rec_dw_body(const RecDwArgs &a, const ActWin &act, int64_
             for (int u = 0; u < 4; ++u) {
                 const int32_t k = min(k0 + 16 * u + sl, chi - 1);
                 const uint32_t p = a.ps[k];
-                gp[u] = a.G + (static_cast<int64_t>(p >> 24) * a.n_post + (p & kLow24)) * a.R;
+                gp[u] = a.G + (static_cast<int64_t>(p >> 24) * a.hm + static_cast<int64_t>(p & kLow24) * a.lm) * a.R;
                 d[u] = a.dw[k];
             }
             uint32_t mb = mm;
@@ -890,7 +929,7 @@ __device__ inline void rec_dw_body(const RecDwArgs &a, const ActWin &act, int64_
 }
 
 struct BwdInArgs {
-    int32_t j, s0, B, R, n_post, chunks;
+    int32_t j, s0, B, R, hm, lm, chunks;  // G rows as in RecDwArgs
     int64_t n_in;
     const int64_t *off;
     const int32_t *pre;
@@ -923,7 +962,7 @@ __device__ inline void bwd_in_body(const BwdInArgs &a, int64_t bid, int64_t nblk
         const int32_t hi = min(a.col_ptr[c + 1], lo + L * kChunkIters);
         for (int32_t k = lo + lane_s; k < hi; k += L) {
             const uint32_t p = a.ps[k];
-            const float *g = a.G + (static_cast<int64_t>(p >> 24) * a.n_post + (p & kLow24)) * a.R;
+            const float *g = a.G + (static_cast<int64_t>(p >> 24) * a.hm + static_cast<int64_t>(p & kLow24) * a.lm) * a.R;
             float d = a.dw[k];
             uint32_t mm = m;
             while (mm) {
@@ -1025,13 +1064,14 @@ static void launch_step(const StepArgs &sa, int nb, dim3 grid, size_t lds, hipSt
 
 constexpr size_t kAdjStageLds = 64 * 1024;  // LDS budget of the adjoint's G staging
 
-// Types per staged chunk of the adjoint (as many as fit the budget beside the basis table).
-static int adj_type_chunk(const CellConst &k, int R) {
+// Types (type-major rows) or ranks (compact rows, rows = rows per post) per staged chunk of
+// the adjoint: as many as fit the budget beside the basis table.
+static int adj_type_chunk(const CellConst &k, int R, int rows) {
     const size_t nr = kBlock / k.B;
     const size_t basis = sizeof(float) * static_cast<size_t>(k.n_types) * k.nb;
     const size_t per_type = sizeof(float) * nr * R;
     const size_t fit = kAdjStageLds > basis ? (kAdjStageLds - basis) / per_type : 0;
-    return static_cast<int>(std::max<size_t>(1, std::min<size_t>(fit, static_cast<size_t>(k.n_types))));
+    return static_cast<int>(std::max<size_t>(1, std::min<size_t>(fit, static_cast<size_t>(rows))));
 }
 
 static size_t adj_stage_lds(const CellConst &k, int R, int tc) {
@@ -1055,6 +1095,64 @@ static void launch_adj(const AdjArgs &aa, int nb, hipStream_t s, const DwPrev *p
 #undef GLIF_ADJ
         default: break;
     }
+}
+
+// G rows per post.  Each post's G rows serve only the synapse types that reach it; with the
+// reference's basis table (a type per (presynaptic class, postsynaptic class) pair) a post
+// receives about one type in eleven, so when the most types any post receives (over the
+// three populations) is at most three quarters of n_types, the tables get compact rows
+// (post * rows + rank) and G shrinks by that factor.  Otherwise the rows stay type-major.
+static int plan_g_rows(Cell *c) {
+    const int N = c->N, nt = c->n_types, words = (nt + 63) / 64;
+    Table *ts[3] = {c->rec, c->lgn, c->bkg};
+    c->g_rows = nt;
+    c->g_compact = false;
+    if (nt > 255) return GLIF_OK;  // 0xFF marks an unused compact row
+    GLIF_HIP(hipDeviceSynchronize());
+    std::vector<uint32_t> ps[3];
+    std::vector<uint64_t> seen(static_cast<size_t>(N) * words, 0ull);
+    for (int i = 0; i < 3; ++i) {
+        ps[i].resize(ts[i]->n_syn);
+        if (ts[i]->n_syn)
+            GLIF_HIP(hipMemcpy(ps[i].data(), ts[i]->ps, ps[i].size() * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        for (const uint32_t p : ps[i]) {
+            const uint32_t sid = p >> 24;
+            seen[static_cast<size_t>(p & kLow24) * words + sid / 64] |= 1ull << (sid % 64);
+        }
+    }
+    int gk = 1;
+    for (int n = 0; n < N; ++n) {
+        int cnt = 0;
+        for (int q = 0; q < words; ++q) cnt += __builtin_popcountll(seen[static_cast<size_t>(n) * words + q]);
+        gk = std::max(gk, cnt);
+    }
+    if (gk * 4 > nt * 3) return GLIF_OK;
+    auto rank_of = [&](uint32_t p) {
+        const uint32_t sid = p >> 24;
+        const uint64_t *sn = &seen[static_cast<size_t>(p & kLow24) * words];
+        int r = 0;
+        for (uint32_t q = 0; q < sid / 64; ++q) r += __builtin_popcountll(sn[q]);
+        const uint64_t below = sid % 64 ? sn[sid / 64] & ((1ull << (sid % 64)) - 1ull) : 0ull;
+        return static_cast<uint8_t>(r + __builtin_popcountll(below));
+    };
+    std::vector<uint8_t> gtype(static_cast<size_t>(N) * gk, 0xFF);
+    for (int n = 0; n < N; ++n) {
+        int q = 0;
+        for (int sid = 0; sid < nt; ++sid)
+            if ((seen[static_cast<size_t>(n) * words + sid / 64] >> (sid % 64)) & 1ull)
+                gtype[static_cast<size_t>(n) * gk + q++] = static_cast<uint8_t>(sid);
+    }
+    for (int i = 0; i < 3; ++i) {
+        std::vector<uint8_t> rank(ps[i].size());
+        for (size_t k = 0; k < rank.size(); ++k) rank[k] = rank_of(ps[i][k]);
+        int rc = table_set_g_rows(ts[i], rank.data(), gk);
+        if (rc) return rc;
+    }
+    GLIF_HIP(hipMalloc(reinterpret_cast<void **>(&c->g_type), gtype.size()));
+    GLIF_HIP(hipMemcpy(c->g_type, gtype.data(), gtype.size(), hipMemcpyHostToDevice));
+    c->g_rows = c->g_compact_rows = gk;
+    c->g_compact = true;
+    return GLIF_OK;
 }
 
 static int chunks_for(const Table *t, int L) {
@@ -1123,6 +1221,10 @@ int glif_cell_create(const glif_cell_config *cfg, const float *decay, const floa
         glif_cell_destroy(reinterpret_cast<glif_cell *>(c));
         return hip_fail(e, "cell upload");
     }
+    if (int rc = plan_g_rows(c)) {
+        glif_cell_destroy(reinterpret_cast<glif_cell *>(c));
+        return rc;
+    }
     *out = reinterpret_cast<glif_cell *>(c);
     return GLIF_OK;
 }
@@ -1132,7 +1234,7 @@ void glif_cell_destroy(glif_cell *cc) {
     if (!c) return;
     for (void *p : {static_cast<void *>(c->decay), static_cast<void *>(c->cf),
                     static_cast<void *>(c->asc_decay), static_cast<void *>(c->asc_amps),
-                    static_cast<void *>(c->tref)})
+                    static_cast<void *>(c->tref), static_cast<void *>(c->g_type)})
         if (p) (void)hipFree(p);
     delete c;
 }
@@ -1382,24 +1484,27 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         (rc = launch_fill_u32(w.gR, 0u, BN * c->nb, s)))
         return rc;
     // padding elements of each G row stay zero
-    const size_t g_elems = static_cast<size_t>(c->N) * c->n_types * g_row(win_width(B), B);
+    const size_t g_elems = static_cast<size_t>(c->N) * c->g_rows * g_row(win_width(B), B);
     if ((rc = launch_fill_u32(w.G, 0u, 2 * g_elems, s))) return rc;
     // the grouped row-sliced walk serves 16-float G rows
-    const bool gs = tr->n_gs > 0 && g_row(win_width(B), B) == 16;
+    const bool cg = c->g_compact;
+    const bool gs = (cg ? tr->n_cgs : tr->n_gs) > 0 && g_row(win_width(B), B) == 16;
     if (dw_rec && (rc = launch_fill_u32(w.dw_rec, 0u, tr->n_syn, s))) return rc;
     if (dw_lgn && (rc = launch_fill_u32(w.dw_lgn, 0u, tl->n_syn, s))) return rc;
     if (dw_bkg && (rc = launch_fill_u32(w.dw_bkg, 0u, tb->n_syn, s))) return rc;
 
     const size_t lds = sizeof(float) * c->n_types * c->nb;
     const int Wwin = win_width(B), ring = ring_size(c), Rg = g_row(Wwin, B);
-    if (static_cast<int64_t>(c->n_types) * c->N * Rg * 4 >= (int64_t(1) << 32))
-        return fail(GLIF_ERANGE, "n_types * n_neurons * G row * 4 bytes must be < 4 GiB");
+    if (static_cast<int64_t>(c->g_rows) * c->N * Rg * 4 >= (int64_t(1) << 32))
+        return fail(GLIF_ERANGE, "G rows per neuron * n_neurons * G row * 4 bytes must be < 4 GiB");
     AdjArgs aa{};
     aa.k = k;
     aa.T = T;
     aa.ring = ring;
     aa.R = Rg;
-    aa.tc = adj_type_chunk(k, Rg);
+    aa.tc = adj_type_chunk(k, Rg, c->g_rows);
+    aa.gk = cg ? c->g_rows : 0;
+    aa.gtype = c->g_type;
     aa.vmode = c->vloss_mode;
     aa.vmask = c->vloss_mask;
     aa.vscale = c->vloss_mode ? c->vloss_cost / (static_cast<float>(T) * static_cast<float>(B) *
@@ -1421,15 +1526,20 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     aa.G = w.G;
     aa.basis = tr->basis;
 
-    ColArgs ca{tr->n_cols, c->N, c->n_types, 0, tr->ph_ptr, tr->ph_pw, w.G, 1, dw_rec ? w.dw_rec : nullptr};
-    GsArgs ga{tr->n_cols, tr->n_groups, 0, tr->gs_seg, tr->gs_pw, w.G};
-    RecDwArgs da{tr->n_cols, 0, c->N, Rg, tr->col_ptr, tr->ps, w.G, w.dw_rec};
+    // G rows of the {hi | post} entries: syn_id * N + post, or post * g_rows + rank
+    const int32_t hm = cg ? 1 : c->N, lm = cg ? c->g_rows : 1;
+    ColArgs ca{tr->n_cols, c->N, c->n_types, 0, tr->ph_ptr, cg ? tr->cph_pw : tr->ph_pw, w.G, 1,
+               dw_rec ? w.dw_rec : nullptr, nullptr, cg ? 1 : 0};
+    GsArgs ga{tr->n_cols, (tr->n_cols + kGsCols - 1) / kGsCols, 0, cg ? tr->cgs_seg : tr->gs_seg,
+              cg ? tr->cgs_pw : tr->gs_pw, w.G};
+    RecDwArgs da{tr->n_cols, 0, hm, lm, Rg, tr->col_ptr, cg ? tr->cps : tr->ps, w.G, w.dw_rec};
     ActWin act{w.zbits, w.dZ, tr->n_cols, 0, B, c->D, c->W, c->N, ring};
 
     BwdInArgs la{}, ka{};
     la.B = ka.B = B;
     la.R = ka.R = Rg;
-    la.n_post = ka.n_post = c->N;
+    la.hm = ka.hm = hm;
+    la.lm = ka.lm = lm;
     la.G = ka.G = w.G;
     la.chunks = chunks_for(tl, kWave);
     la.n_in = tl->n_cols;
@@ -1438,7 +1548,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     la.mask = w.lw_mask;
     la.cnt = nullptr;
     la.col_ptr = tl->col_ptr;
-    la.ps = tl->ps;
+    la.ps = cg ? tl->cps : tl->ps;
     la.dw = w.dw_lgn;
     ka.chunks = chunks_for(tb, kWave);
     ka.n_in = tb->n_cols;
@@ -1447,7 +1557,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     ka.mask = w.kw_mask;
     ka.cnt = w.bkg_cnt;
     ka.col_ptr = tb->col_ptr;
-    ka.ps = tb->ps;
+    ka.ps = cg ? tb->cps : tb->ps;
     ka.dw = w.dw_bkg;
     const int64_t lgn_units = tl->n_cols * static_cast<int64_t>(la.chunks);
     const int64_t bkg_units = tb->n_cols * static_cast<int64_t>(ka.chunks);
@@ -1540,6 +1650,24 @@ int glif_cell_set_trim(glif_cell *cc, int32_t pre_delay, int32_t post_delay) {
     if (pre_delay < 0 || post_delay < 0) return fail(GLIF_EINVAL, "pre_delay and post_delay must be >= 0");
     c->trim_pre = pre_delay;
     c->trim_post = post_delay;
+    return GLIF_OK;
+}
+
+int glif_cell_set_g_layout(glif_cell *cc, int32_t compact) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c) return fail(GLIF_EINVAL, "NULL cell");
+    if (compact && !c->g_compact_rows)
+        return fail(GLIF_EINVAL, "no compact G rows for this cell (some neuron receives > 3/4 of the types)");
+    c->g_compact = compact != 0;
+    c->g_rows = c->g_compact ? c->g_compact_rows : c->n_types;
+    return GLIF_OK;
+}
+
+int glif_cell_g_layout(const glif_cell *cc, int32_t *rows_per_post, int32_t *compact) {
+    const Cell *c = reinterpret_cast<const Cell *>(cc);
+    if (!c || !rows_per_post || !compact) return fail(GLIF_EINVAL, "NULL argument");
+    *rows_per_post = c->g_rows;
+    *compact = c->g_compact ? 1 : 0;
     return GLIF_OK;
 }
 

@@ -96,7 +96,24 @@ struct Table {
     uint2 *gs_pw = nullptr;       // [n_gs]        {row | column-in-group << kGsRowBits, weight bits}
     int32_t *gs_src = nullptr;    // [n_gs]        column-grouped position of the synapse, -1 for padding
     float *basis_host = nullptr;  // host copy [n_types][n_basis]
+    // compact G rows, set by a cell whose posts each receive few of the synapse types: the G
+    // row of a synapse is post * g_rows + rank, rank = the position of its syn_id among the
+    // types that reach that post from any of the cell's populations (ascending).  The
+    // type-major copies above stay as they are (the op-level entry points use them).
+    // g_rows = 0: not set.
+    int32_t g_rows = 0;
+    uint8_t *g_rank_host = nullptr;  // [n_syn] host copy of the ranks, column-grouped order
+    uint32_t *cps = nullptr;      // [n_syn] column-grouped: post | rank << 24
+    uint2 *cph_pw = nullptr;      // [n_syn] type-phased order: {compact row, weight bits}
+    int64_t n_cgs = 0;            // the grouped row-sliced order over compact rows (n_groups
+    int32_t *cgs_seg = nullptr;   // groups, as gs_*); n_cgs = 0: not built
+    uint2 *cgs_pw = nullptr;
+    int32_t *cgs_src = nullptr;
 };
+
+// Give a table compact G rows (rank: [n_syn] in column-grouped order, each < g_rows).  A table
+// that already has them keeps them if they are the same, else GLIF_EINVAL.  Synchronous.
+int table_set_g_rows(Table *t, const uint8_t *rank, int32_t g_rows);
 
 // ---- cell ------------------------------------------------------------------
 struct Cell {
@@ -116,6 +133,13 @@ struct Cell {
     // counts spikes of ticks [trim_pre, T - trim_post) and the backward broadcasts
     // gz_neuron over the same ticks
     int32_t trim_pre = 0, trim_post = 0;
+    // G rows per post: n_types (rows syn_id * N + post), or fewer when the tables carry
+    // compact rows (rows post * g_rows + rank, g_type[post * g_rows + rank] = syn_id, 0xFF
+    // past the post's types)
+    int32_t g_rows = 0;
+    bool g_compact = false;
+    int32_t g_compact_rows = 0;  // compact rows per post the tables carry, 0: none
+    uint8_t *g_type = nullptr;  // device [N * g_compact_rows]
 };
 
 // Small per-cell constants passed by value to kernels.

@@ -176,6 +176,9 @@ struct ColArgs {
     // when set, each synapse's dW is written once, straight to dw[dw_ref[k]] (reference
     // order, the caller zero-fills dw) instead of accumulated at position k
     const int32_t *dw_ref;
+    // 1: ph_pw[k].x is the synapse's G row itself (compact rows, post * rows per post +
+    // rank), not the post of a type-major row syn_id * n_post + post
+    int32_t compact;
 };
 
 // Op-level activity: z [B][n_cols] dense, element e = b.
@@ -215,7 +218,7 @@ __device__ inline void bwd_cols(const ColArgs &a, const Act &act) {
 #pragma unroll
     for (int o = 1; o < LG; o <<= 1) any |= __shfl_xor(any, o, kWave);
     const char *Gb = reinterpret_cast<const char *>(a.G) + static_cast<uint32_t>(q) * 16u;
-    const uint32_t type_bytes = static_cast<uint32_t>(a.n_post) * (R * 4u);
+    const uint32_t type_bytes = a.compact ? 0u : static_cast<uint32_t>(a.n_post) * (R * 4u);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // the next type's segment bounds are loaded while the current type is walked
     int32_t nlo = a.ph_ptr[c], nhi = a.ph_ptr[c + 1];

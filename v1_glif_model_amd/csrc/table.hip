@@ -94,15 +94,131 @@ static int upload(T **dst, const T *src, size_t n) {
     return GLIF_OK;
 }
 
+// Grouped row-sliced order (backward dz walks) over items 0..n-1 (synapses, or positions of
+// the column-grouped order) with G row row[i] < n_rows and column col[i]: a stable counting
+// sort by (G row, column in group), then by (group, row slice); each (group, slice) segment is
+// padded to a multiple of kGsPad with copies of its last row marked as column 7 (weight
+// +0.0f).  src[i] goes to gs_src.  False (nothing built) when the rows or positions do not fit.
+static bool build_gs(int64_t n, int64_t n_cols, int64_t n_rows, const int64_t *row, const int64_t *col,
+                     const int32_t *src, int64_t &n_groups, int64_t &n_gs, std::vector<int32_t> &gs_seg,
+                     std::vector<uint2> &gs_pw, std::vector<int32_t> &gs_src) {
+    n_groups = n_gs = 0;
+    if (n <= 0 || n_rows > static_cast<int64_t>(kGsRowMask) + 1) return false;
+    const int64_t groups = (n_cols + kGsCols - 1) / kGsCols;
+    std::vector<int64_t> key(n);
+    for (int64_t i = 0; i < n; ++i) key[i] = row[i] * kGsCols + col[i] % kGsCols;
+    std::vector<int32_t> ptr1(n_rows * kGsCols + 1), ord1(n);
+    counting_sort(key.data(), nullptr, n, n_rows * kGsCols, ptr1.data(), ord1.data());
+    for (int64_t i = 0; i < n; ++i) key[i] = (col[i] / kGsCols) * kGsSlices + row[i] * kGsSlices / n_rows;
+    const int64_t n_seg = groups * kGsSlices;
+    std::vector<int32_t> ptr2(n_seg + 1), ord2(n);
+    counting_sort(key.data(), ord1.data(), n, n_seg, ptr2.data(), ord2.data());
+    int64_t total = 0;
+    for (int64_t b = 0; b < n_seg; ++b) total += (ptr2[b + 1] - ptr2[b] + kGsPad - 1) / kGsPad * kGsPad;
+    if (total >= INT32_MAX) return false;
+    gs_seg.resize(groups * (kGsSlices + 1));
+    gs_pw.resize(total);
+    gs_src.resize(total);
+    int64_t pos = 0;
+    for (int64_t g = 0; g < groups; ++g) {
+        for (int p = 0; p < kGsSlices; ++p) {
+            const int64_t b = g * kGsSlices + p;
+            gs_seg[g * (kGsSlices + 1) + p] = static_cast<int32_t>(pos);
+            uint32_t last = 0;
+            for (int32_t r = ptr2[b]; r < ptr2[b + 1]; ++r, ++pos) {
+                const int32_t i = ord2[r];
+                last = static_cast<uint32_t>(row[i]);
+                gs_pw[pos] = make_uint2(last | static_cast<uint32_t>(col[i] % kGsCols) << kGsRowBits, 0u);
+                gs_src[pos] = src[i];
+            }
+            for (; pos % kGsPad; ++pos) {
+                gs_pw[pos] = make_uint2(last | 7u << kGsRowBits, 0u);
+                gs_src[pos] = -1;
+            }
+        }
+        gs_seg[g * (kGsSlices + 1) + kGsSlices] = static_cast<int32_t>(pos);
+    }
+    n_groups = groups;
+    n_gs = total;
+    return true;
+}
+
 static void free_table(Table *t) {
     if (!t) return;
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
                     t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
-                    t->chunk_desc, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src};
+                    t->chunk_desc, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src,
+                    t->cps, t->cph_pw, t->cgs_seg, t->cgs_pw, t->cgs_src};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete[] t->basis_host;
+    delete[] t->g_rank_host;
     delete t;
+}
+
+template <typename T>
+static int download(std::vector<T> &dst, const T *src, size_t n) {
+    dst.resize(n);
+    if (n) GLIF_HIP(hipMemcpy(dst.data(), src, n * sizeof(T), hipMemcpyDeviceToHost));
+    return GLIF_OK;
+}
+
+int table_set_g_rows(Table *t, const uint8_t *rank, int32_t g_rows) {
+    if (g_rows <= 0 || g_rows > 255) return fail(GLIF_EINVAL, "compact G rows per post must be in [1, 255]");
+    const int64_t n = t->n_syn;
+    if (t->g_rows) {
+        if (t->g_rows == g_rows && (n == 0 || std::memcmp(t->g_rank_host, rank, n) == 0)) return GLIF_OK;
+        return fail(GLIF_EINVAL, "table already carries a different compact G row map (one per table)");
+    }
+    for (int64_t k = 0; k < n; ++k)
+        if (rank[k] >= g_rows) return fail(GLIF_ERANGE, "G row rank >= rows per post");
+    std::vector<int32_t> col_ptr, ph_src;
+    std::vector<uint32_t> ps;
+    int rc;
+    GLIF_HIP(hipDeviceSynchronize());  // weights set on any stream have landed in w_col
+    if ((rc = download(col_ptr, t->col_ptr, static_cast<size_t>(t->n_cols) + 1)) ||
+        (rc = download(ps, t->ps, n)) || (rc = download(ph_src, t->ph_src, n)))
+        return rc;
+    // per column-grouped position k: compact row and column
+    std::vector<int64_t> row(n), col(n);
+    std::vector<int32_t> src(n);
+    std::vector<uint32_t> cps(n);
+    for (int64_t c = 0; c < t->n_cols; ++c)
+        for (int32_t k = col_ptr[c]; k < col_ptr[c + 1]; ++k) col[k] = c;
+    for (int64_t k = 0; k < n; ++k) {
+        const uint32_t post = ps[k] & kLow24;
+        row[k] = static_cast<int64_t>(post) * g_rows + rank[k];
+        cps[k] = post | static_cast<uint32_t>(rank[k]) << 24;
+        src[k] = static_cast<int32_t>(k);
+    }
+    std::vector<uint2> cph_pw(n);
+    for (int64_t k = 0; k < n; ++k) cph_pw[k] = make_uint2(static_cast<uint32_t>(row[ph_src[k]]), 0u);
+    std::vector<int32_t> gs_seg, gs_src;
+    std::vector<uint2> gs_pw;
+    int64_t n_groups = 0, n_gs = 0;
+    build_gs(n, t->n_cols, static_cast<int64_t>(t->n_post) * g_rows, row.data(), col.data(), src.data(), n_groups,
+             n_gs, gs_seg, gs_pw, gs_src);
+    if ((rc = upload(&t->cps, cps.data(), cps.size())) || (rc = upload(&t->cph_pw, cph_pw.data(), cph_pw.size())) ||
+        (n_gs && (rc = upload(&t->cgs_seg, gs_seg.data(), gs_seg.size()))) ||
+        (n_gs && (rc = upload(&t->cgs_pw, gs_pw.data(), gs_pw.size()))) ||
+        (n_gs && (rc = upload(&t->cgs_src, gs_src.data(), gs_src.size()))))
+        return rc;
+    t->n_cgs = n_gs;
+    t->g_rank_host = new uint8_t[std::max<int64_t>(n, 1)];
+    if (n) std::memcpy(t->g_rank_host, rank, n);
+    t->g_rows = g_rows;
+    // the weights the table already holds (later ones arrive through glif_table_set_weights)
+    if (n) {
+        hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(n)), dim3(kBlock), 0, 0, t->cph_pw, t->w_col, t->ph_src, n);
+        GLIF_HIP(hipGetLastError());
+    }
+    if (n_gs) {
+        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(n_gs)), dim3(kBlock), 0, 0, t->cgs_pw, t->w_col, t->cgs_src,
+                           n_gs);
+        GLIF_HIP(hipGetLastError());
+    }
+    GLIF_HIP(hipDeviceSynchronize());
+    return GLIF_OK;
 }
 
 }  // namespace glif
@@ -193,54 +309,15 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
     // theirs (the type-phased order sweeps it once per type; a group's grouped entries come
     // from its own columns), rather than from the reference order
     for (int64_t k = 0; k < n_syn; ++k) ph_src[k] = order_inv[ph_order[k]];
-    // grouped row-sliced order (backward dz walks): a stable counting sort by (G row,
-    // column in group), then by (group, row slice); each (group, slice) segment is padded to
-    // a multiple of kGsPad with copies of its last row marked as column 7 (weight +0.0f)
-    const int64_t n_rows = static_cast<int64_t>(n_types) * n_post;
+    // grouped row-sliced order (backward dz walks) over the type-major rows
     std::vector<int32_t> gs_seg, gs_src;
     std::vector<uint2> gs_pw;
     int64_t n_groups = 0, n_gs = 0;
-    if (n_syn > 0 && n_rows <= static_cast<int64_t>(kGsRowMask) + 1) {
-        n_groups = (n_cols + kGsCols - 1) / kGsCols;
-        std::vector<int64_t> key(n_syn);
-        for (int64_t i = 0; i < n_syn; ++i)
-            key[i] = (static_cast<int64_t>(syn_id[i]) * n_post + post[i]) * kGsCols + col[i] % kGsCols;
-        std::vector<int32_t> ptr1(n_rows * kGsCols + 1), ord1(n_syn);
-        counting_sort(key.data(), nullptr, n_syn, n_rows * kGsCols, ptr1.data(), ord1.data());
-        for (int64_t i = 0; i < n_syn; ++i) {
-            const int64_t row = static_cast<int64_t>(syn_id[i]) * n_post + post[i];
-            key[i] = (col[i] / kGsCols) * kGsSlices + row * kGsSlices / n_rows;
-        }
-        const int64_t n_seg = n_groups * kGsSlices;
-        std::vector<int32_t> ptr2(n_seg + 1), ord2(n_syn);
-        counting_sort(key.data(), ord1.data(), n_syn, n_seg, ptr2.data(), ord2.data());
-        for (int64_t b = 0; b < n_seg; ++b) n_gs += (ptr2[b + 1] - ptr2[b] + kGsPad - 1) / kGsPad * kGsPad;
-        if (n_gs < INT32_MAX) {
-            gs_seg.resize(n_groups * (kGsSlices + 1));
-            gs_pw.resize(n_gs);
-            gs_src.resize(n_gs);
-            int64_t pos = 0;
-            for (int64_t g = 0; g < n_groups; ++g) {
-                for (int p = 0; p < kGsSlices; ++p) {
-                    const int64_t b = g * kGsSlices + p;
-                    gs_seg[g * (kGsSlices + 1) + p] = static_cast<int32_t>(pos);
-                    uint32_t last = 0;
-                    for (int32_t r = ptr2[b]; r < ptr2[b + 1]; ++r, ++pos) {
-                        const int32_t sidx = ord2[r];
-                        last = static_cast<uint32_t>(static_cast<int64_t>(syn_id[sidx]) * n_post + post[sidx]);
-                        gs_pw[pos] = make_uint2(last | static_cast<uint32_t>(col[sidx] % kGsCols) << kGsRowBits, 0u);
-                        gs_src[pos] = order_inv[sidx];
-                    }
-                    for (; pos % kGsPad; ++pos) {
-                        gs_pw[pos] = make_uint2(last | 7u << kGsRowBits, 0u);
-                        gs_src[pos] = -1;
-                    }
-                }
-                gs_seg[g * (kGsSlices + 1) + kGsSlices] = static_cast<int32_t>(pos);
-            }
-        } else {
-            n_groups = n_gs = 0;
-        }
+    {
+        std::vector<int64_t> row(n_syn);
+        for (int64_t i = 0; i < n_syn; ++i) row[i] = static_cast<int64_t>(syn_id[i]) * n_post + post[i];
+        build_gs(n_syn, n_cols, static_cast<int64_t>(n_types) * n_post, row.data(), col, order_inv.data(), n_groups,
+                 n_gs, gs_seg, gs_pw, gs_src);
     }
 
     std::vector<uint32_t> ps(n_syn), pd(n_syn);
@@ -375,6 +452,16 @@ int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
     if (t->n_gs) {
         hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(t->n_gs)), dim3(kBlock), 0, s, t->gs_pw, t->w_col,
                            t->gs_src, t->n_gs);
+        GLIF_HIP(hipGetLastError());
+    }
+    if (t->g_rows && t->n_syn) {  // the compact-row copies of a cell's tables
+        hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(t->n_syn)), dim3(kBlock), 0, s, t->cph_pw, t->w_col,
+                           t->ph_src, t->n_syn);
+        GLIF_HIP(hipGetLastError());
+    }
+    if (t->n_cgs) {
+        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(t->n_cgs)), dim3(kBlock), 0, s, t->cgs_pw, t->w_col,
+                           t->cgs_src, t->n_cgs);
         GLIF_HIP(hipGetLastError());
     }
     if (t->ell_len) {

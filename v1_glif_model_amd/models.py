@@ -130,6 +130,20 @@ class V1Column:
         self.lgn_table.set_weights(self.input_weight_values, force)
         self.bkg_table.set_weights(self.bkg_input_weights, force)
 
+    def g_layout(self):
+        """(rows per neuron, compact) of the backward's per-synapse-type projection: compact
+        when no neuron receives more than three quarters of the synapse types (the
+        reference's class-pair types: 11 of 121 per neuron), each neuron then keeping rows for
+        its own types only."""
+        rows, compact = C.c_int32(), C.c_int32()
+        check(lib().glif_cell_g_layout(self.handle, C.byref(rows), C.byref(compact)))
+        return int(rows.value), bool(compact.value)
+
+    def set_g_layout(self, compact: bool):
+        """Select compact (True, when available) or type-major G rows for the next rollout and
+        backward."""
+        check(lib().glif_cell_set_g_layout(self.handle, int(bool(compact))))
+
     def workspace(self, B: int, T: int) -> torch.Tensor:
         n = int(lib().glif_cell_workspace(self.handle, int(B), int(T)))
         ws = self._ws.get("ws")

@@ -39,7 +39,7 @@ from typing import Optional
 import numpy as np
 
 __all__ = ["SynthConfig", "CONFIGS", "make_network", "make_inputs", "make_rate_targets",
-           "make_cell_types", "make_type_rates", "config", "expand_receptors"]
+           "make_cell_types", "make_type_rates", "config", "expand_receptors", "class_types"]
 
 
 @dataclasses.dataclass(frozen=True)
@@ -281,4 +281,38 @@ def expand_receptors(net):
     out["lgn_input"] = split(net["lgn_input"], False)
     out["bkg_input"] = split(net["bkg_input"], False)
     out["basis"] = np.eye(nb, dtype=np.float32)
+    return out
+
+
+def class_types(net, n_classes: int = 11, seed: int = 5):
+    """The network with synapse types fixed by (presynaptic class, postsynaptic class), the
+    structure of the reference's basis table (`synaptic_data/basis_function_weights.csv`: one
+    row per "<pre>_to_<post>" model over 11 classes, 121 rows, every row feeding every
+    receptor; `load_sparse.py:113-128` maps an edge's model to its syn_id).
+
+    Class 0 is the presynaptic class of the LGN and background inputs (the reference's generic
+    "exc"); the excitatory V1 neurons take classes 1 .. n_classes // 2 and the inhibitory ones
+    the rest, uniformly.  syn_id = pre_class * n_classes + post_class over a dense random basis
+    [n_classes^2, n_basis], so a post neuron receives at most n_classes of the types."""
+    if not 3 <= n_classes <= 16:
+        raise ValueError("n_classes must be in [3, 16] (n_classes^2 uint8 synapse types)")
+    rng = np.random.default_rng(seed)
+    nw = net["network"]
+    N, n_exc = int(nw["n_nodes"]), int(nw["n_exc"])
+    n_cls_exc = n_classes // 2
+    cls = np.empty(N, dtype=np.int64)
+    cls[:n_exc] = rng.integers(1, 1 + n_cls_exc, n_exc)
+    cls[n_exc:] = rng.integers(1 + n_cls_exc, n_classes, N - n_exc)
+    nb = np.asarray(net["basis"]).shape[1]
+
+    def retype(pop, pre_cls):
+        idx = np.asarray(pop["indices"])
+        return dict(pop, syn_ids=(pre_cls(idx[:, 1]) * n_classes + cls[idx[:, 0]]).astype(np.uint8))
+
+    out = dict(net)
+    out["network"] = dict(nw, synapses=retype(nw["synapses"], lambda pre: cls[pre]))
+    out["lgn_input"] = retype(net["lgn_input"], lambda pre: np.zeros_like(pre))
+    out["bkg_input"] = retype(net["bkg_input"], lambda pre: np.zeros_like(pre))
+    out["basis"] = rng.uniform(0.0, 1.0, (n_classes * n_classes, nb)).astype(np.float32)
+    out["neuron_class"] = cls
     return out
