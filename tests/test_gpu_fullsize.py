@@ -14,6 +14,8 @@ against the C oracle on identical seeded inputs.
     step with the sign constraints (within 1e-6 relative given the gradient);
 * config 3 (230k neurons, 69M synapses, B = 1): deterministic forward bit-exact over 500 ms (the
   144 KB-LDS, 1024-lane chunk pull), event counts within the bar;
+* config 2's network with the reference's type structure (121 class-pair types, 4 receptors,
+  5 Hz): compact G rows, deterministic forward bit-exact over 150 ms and BPTT within the bar;
 * config 4 (B = 32, per-batch sinusoidal LGN) at the rate sweep's 5 Hz and 50 Hz weight
   factors: deterministic forward bit-exact over 500 ms, event counts within the bar (5 Hz;
   at 50 Hz the agreement is reported), and a B = 32 BPTT at the 50 Hz factor (one-tick
@@ -274,6 +276,36 @@ def test_config4_bptt_batch32(config4):
     for k in ("rec", "lgn", "bkg"):
         say("config 4 B=32", k, error_summary(g[k], og[k], scale[k]))
         assert np.count_nonzero(og[k]) > 0
+        assert_grads_per_element(g[k], og[k], scale[k], what=k)
+
+
+def test_config2_class_types_compact_rows():
+    """The config-2 network with the reference's type structure (121 types by (pre class, post
+    class) over 11 classes, 4 receptors, dense basis) at the bench's 5 Hz weight factor: the cell
+    keeps 11 compact G rows per neuron; deterministic forward bit-exact over 150 ms and the BPTT
+    (grouped walk over compact rows, their dW passes) per element within the bar."""
+    cfg = dataclasses.replace(sy.config(2), n_basis=4)
+    net = sy.class_types(sy.make_network(cfg, seed=0), n_classes=11)
+    T, B = 150, cfg.batch
+    lgn, bkg = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
+    cell, tbs = _scaled_cell(net, 0.5179)
+    assert cell.g_layout() == (11, True)
+    say("config 2, class types: cell built, compact rows", cell.g_layout())
+    z, v, _ = cell.rollout(lgn, bkg)
+    oc = orc.OracleCell(tbs, **ORC_KW)
+    oz, ov, oref, _ = oc.forward(lgn, bkg)
+    say("config 2, class types:", int(oz.sum()), "spikes, onset", onset(oz))
+    assert oz.sum() > 10000
+    np.testing.assert_array_equal(z.cpu().numpy().astype(np.uint8), oz)
+    np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), ov.view(np.uint32))
+    gz = np.random.default_rng(45).normal(0, 1, oz.shape).astype(np.float32)
+    g = {k: t.cpu().numpy() for k, t in cell.backward(gz=torch.tensor(gz, device="cuda")).items()}
+    del cell
+    say("config 2, class types: GPU BPTT done; oracle")
+    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz)
+    scale = orc.bptt_abs_scale(tbs, lgn, bkg, oz, oref, ov, gz_loss=gz, **ORC_KW)
+    for k in ("rec", "lgn", "bkg"):
+        say("config 2, class types", k, error_summary(g[k], og[k], scale[k]))
         assert_grads_per_element(g[k], og[k], scale[k], what=k)
 
 
