@@ -82,6 +82,37 @@ def test_compact_rows_bptt(B):
     _bptt_check(cell, tb, lgn, bkg, oz, oref, ov, gz, f"B={B}")
 
 
+def test_typed_push_voltages_per_tick():
+    """Event forward with per-type slots (a dense basis: each synapse event is one atomic into
+    its post's type slot, the step folds the slots through the basis): from the oracle's state
+    at every tick, three ticks on, spike trains equal and voltages within 1e-5 relative /
+    1e-6 absolute."""
+    from tests.test_gpu_params import _state_dev
+    from v1_glif_model_amd.models import V1Column
+    cfg = tiny_config(rs=2.0, ins=3.0)
+    net, tb = _class_net(cfg, 81, 5)
+    T, B, K = 40, 3, 3
+    lgn, bkg = sy.make_inputs(cfg, seed=82, seq_len=T, batch=B)
+    cell = V1Column(net, mode="event", **KW)
+    assert cell.g_layout()[1]
+    oc = OracleCell(tb, **OKW)
+    st = oc.zero_state(B)
+    ws = cell.workspace(B, K)
+    worst, spikes = 0.0, 0
+    for t0 in range(T - K):
+        ze, ve, _ = cell.rollout(lgn[t0:t0 + K], bkg[t0:t0 + K], state=_state_dev(cell, st), ws=ws)
+        oz3, ov3, _, _ = oc.forward(lgn[t0:t0 + K], bkg[t0:t0 + K], state=st)
+        np.testing.assert_array_equal(ze.cpu().numpy().astype(np.uint8), oz3)
+        ve = ve.cpu().numpy().astype(np.float64)
+        err = np.abs(ve - ov3)
+        assert np.all(err <= 1e-5 * np.abs(ov3) + 1e-6), (t0, float(err.max()))
+        worst = max(worst, float(err.max()))
+        spikes += int(oz3[0].sum())
+        _, _, _, st = oc.forward(lgn[t0:t0 + 1], bkg[t0:t0 + 1], state=st)
+    assert spikes > 0
+    print("largest per-tick voltage difference", worst)
+
+
 def test_compact_rows_event_mode_and_updated_weights():
     """Event forward, then an ExponentiatedAdam step on all three populations (the compact
     copies of the weights refresh with the others), then a second rollout and BPTT against the

@@ -283,7 +283,9 @@ def test_config2_class_types_compact_rows():
     """The config-2 network with the reference's type structure (121 types by (pre class, post
     class) over 11 classes, 4 receptors, dense basis) at the bench's 5 Hz weight factor: the cell
     keeps 11 compact G rows per neuron; deterministic forward bit-exact over 150 ms and the BPTT
-    (grouped walk over compact rows, their dW passes) per element within the bar."""
+    (grouped walk over compact rows, their dW passes) per element within the bar; the event
+    forward (per-type slots) with the same spike trains for 50 ms from onset and counts within
+    the bar."""
     cfg = dataclasses.replace(sy.config(2), n_basis=4)
     net = sy.class_types(sy.make_network(cfg, seed=0), n_classes=11)
     T, B = 150, cfg.batch
@@ -300,7 +302,17 @@ def test_config2_class_types_compact_rows():
     np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), ov.view(np.uint32))
     gz = np.random.default_rng(45).normal(0, 1, oz.shape).astype(np.float32)
     g = {k: t.cpu().numpy() for k, t in cell.backward(gz=torch.tensor(gz, device="cuda")).items()}
+    # the event forward pushes one atomic per synapse event into the post's type slot and
+    # folds the slots through the basis in the step
+    ze, _, _ = cell.rollout(lgn, bkg, mode="event")
+    ze = ze.cpu().numpy().astype(np.uint8)
     del cell
+    t0 = onset(oz)
+    differ = np.flatnonzero((ze != oz).any(axis=(1, 2)))
+    say("config 2, class types, event: first differing ms", differ[0] if differ.size else None,
+        "count agreement", count_agreement(ze, oz))
+    np.testing.assert_array_equal(ze[:t0 + 50], oz[:t0 + 50])
+    assert count_agreement(ze, oz) >= 0.999
     say("config 2, class types: GPU BPTT done; oracle")
     og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz)
     scale = orc.bptt_abs_scale(tbs, lgn, bkg, oz, oref, ov, gz_loss=gz, **ORC_KW)

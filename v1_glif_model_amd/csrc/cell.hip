@@ -34,7 +34,8 @@ namespace glif {
 // ------------------------------------------------------------------ state ----
 constexpr int kVlossBlocks = 1024;  // blocks of the voltage-penalty reduction
 struct CellWs {
-    float *I;           // [nb][B][N]   pushed rec + LGN currents (event mode)
+    float *I;           // [2][nb][B][N]   pushed rec + LGN currents (event mode), or
+                        // [2][g_rows][B][N] type sums with per-type slots
     float *R, *P;       // [nb][B][N]   psc_rise, psc (receptor-major copies of the state)
     float *A;           // [2][B][N]    asc
     uint64_t *zbits;    // [(T + D)][B][W]   slot t + D holds z_t
@@ -71,12 +72,16 @@ static int win_width(int B) { return 3 * B <= 16 ? 3 : 1; }
 static int n_windows(int T, int Wwin) { return T >= 3 ? (T - 2 + Wwin - 1) / Wwin : 0; }
 static int ring_size(const Cell *c) { return c->D + 6; }
 
+// Current slots per (b, n) of I: the receptors, or in event mode with per-type slots the
+// compact rows when there are more of them.
+static int i_slots(const Cell *c) { return std::max(c->nb, c->push_typed ? c->g_rows : 0); }
+
 static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *bytes) {
     Carver cv(ws, SIZE_MAX);
     CellWs w{};
     const int64_t BN = static_cast<int64_t>(B) * c->N;
     const int64_t nl = c->lgn->n_cols, nk = c->bkg->n_cols;
-    w.I = cv.take<float>(2 * BN * c->nb);   // event mode alternates between the two halves by tick
+    w.I = cv.take<float>(2 * BN * i_slots(c));   // event mode alternates between the two halves by tick
     w.R = cv.take<float>(BN * c->nb);
     w.P = cv.take<float>(BN * c->nb);
     w.A = cv.take<float>(BN * 2);
@@ -233,6 +238,7 @@ struct PushArgs {
     int32_t t, D, N, B, W, nb, n_types, chunks_lgn;
     int32_t d_lo, d_hi;   // delay slots pushed (1-based, inclusive)
     int32_t lgn;          // push the step's LGN events too
+    int32_t typed;        // per-type slots (rec_ps / lgn_ps are then {post | rank} entries)
     const uint64_t *zbits;  // [(T + D)][B][W] spike bits, slot s + D holds z_s
     const int32_t *rec_colptr;
     const uint32_t *rec_ps;
@@ -279,8 +285,12 @@ __device__ inline void push_body(const PushArgs &a, int64_t bid, int64_t nblk) {
                 const int bit = __builtin_ctzll(word);
                 word &= word - 1ull;
                 const int32_t col = wi * 64 + bit + (d - 1) * a.N;
-                push_column<L>(lane_s, a.rec_colptr[col], a.rec_colptr[col + 1], 1u << b, MultOne{}, a.rec_ps,
-                               a.rec_w, basis_lds, a.nb, a.N, 1, BN, a.I);
+                if (a.typed)
+                    push_column_typed<L>(lane_s, a.rec_colptr[col], a.rec_colptr[col + 1], 1u << b, MultOne{},
+                                         a.rec_ps, a.rec_w, a.N, BN, a.I);
+                else
+                    push_column<L>(lane_s, a.rec_colptr[col], a.rec_colptr[col + 1], 1u << b, MultOne{}, a.rec_ps,
+                                   a.rec_w, basis_lds, a.nb, a.N, 1, BN, a.I);
             }
         } else {
             const int64_t v = u - n_words;
@@ -289,8 +299,11 @@ __device__ inline void push_body(const PushArgs &a, int64_t bid, int64_t nblk) {
             const int32_t c = a.lgn_pre[it];
             const int32_t lo = a.lgn_colptr[c] + ch * L * kChunkIters;
             const int32_t hi = min(a.lgn_colptr[c + 1], lo + L * kChunkIters);
-            push_column<L>(lane_s, lo, hi, a.lgn_mask[it], MultOne{}, a.lgn_ps, a.lgn_w, basis_lds,
-                           a.nb, a.N, 1, BN, a.I);
+            if (a.typed)
+                push_column_typed<L>(lane_s, lo, hi, a.lgn_mask[it], MultOne{}, a.lgn_ps, a.lgn_w, a.N, BN, a.I);
+            else
+                push_column<L>(lane_s, lo, hi, a.lgn_mask[it], MultOne{}, a.lgn_ps, a.lgn_w, basis_lds,
+                               a.nb, a.N, 1, BN, a.I);
         }
     }
 }
@@ -343,6 +356,10 @@ struct StepArgs {
     const int32_t *p1_colptr;
     const uint32_t *p1_ps;
     const float *p1_w;
+    // event mode with per-type slots: I holds [gk][B][N] type sums (p1_ps {post | rank});
+    // receptor r's current is sum_q I[q] * basis[gtype[n][q]][r], ascending q.  0: [nb][B][N]
+    int32_t gk;
+    const uint8_t *gtype;
 };
 
 // One GLIF_3 update per thread (b, n), models.py:979-1028 and 1059-1135:
@@ -373,7 +390,22 @@ __device__ inline void step_body(const StepArgs &a, int64_t bid) {
         const int64_t bn = static_cast<int64_t>(b) * k.N + n;
         float Irl[kMaxBasis], Ib[kMaxBasis];
         for (int q = 0; q < nb; ++q) Ib[q] = 0.0f;
-        {
+        if (!DET && a.gk) {
+            // the pushed rec + LGN type sums, folded through the basis (a slot past the
+            // post's types holds +0 and is skipped)
+            for (int q = 0; q < nb; ++q) Irl[q] = 0.0f;
+            const uint8_t *gt = a.gtype + static_cast<int64_t>(n) * a.gk;
+            for (int j = 0; j < a.gk; ++j) {
+                float *Ip = a.I + j * BN + bn;
+                const float x = *Ip;
+                *Ip = 0.0f;
+                const int sj = gt[j];
+                if (sj == 0xFF) continue;
+                const float *bs = basis_lds + sj * nb;
+#pragma unroll
+                for (int q = 0; q < nb; ++q) Irl[q] = Irl[q] + x * bs[q];
+            }
+        } else {
             // the pushed (event) or pulled (deterministic) rec + LGN currents
             for (int q = 0; q < nb; ++q) {
                 float *Ip = a.I + q * BN + bn;
@@ -485,8 +517,12 @@ __device__ inline void step_body(const StepArgs &a, int64_t bid) {
             const int bit = __builtin_ctzll(zw);
             zw &= zw - 1ull;
             const int32_t col = n0 + bit;
-            push_column<kWave>(lane, a.p1_colptr[col], a.p1_colptr[col + 1], 1u << b, MultOne{}, a.p1_ps, a.p1_w,
-                               basis_lds, nb, k.N, 1, BN, a.I_next);
+            if (a.gk)
+                push_column_typed<kWave>(lane, a.p1_colptr[col], a.p1_colptr[col + 1], 1u << b, MultOne{}, a.p1_ps,
+                                         a.p1_w, k.N, BN, a.I_next);
+            else
+                push_column<kWave>(lane, a.p1_colptr[col], a.p1_colptr[col + 1], 1u << b, MultOne{}, a.p1_ps,
+                                   a.p1_w, basis_lds, nb, k.N, 1, BN, a.I_next);
         }
     }
 }
@@ -1107,6 +1143,12 @@ static int plan_g_rows(Cell *c) {
     Table *ts[3] = {c->rec, c->lgn, c->bkg};
     c->g_rows = nt;
     c->g_compact = false;
+    c->push_typed = false;
+    for (int s = 0; s < nt && !c->basis_dense; ++s) {
+        int nz = 0;
+        for (int r = 0; r < c->nb; ++r) nz += c->rec->basis_host[static_cast<size_t>(s) * c->nb + r] != 0.0f;
+        c->basis_dense = nz > 1;
+    }
     if (nt > 255) return GLIF_OK;  // 0xFF marks an unused compact row
     GLIF_HIP(hipDeviceSynchronize());
     std::vector<uint32_t> ps[3];
@@ -1152,6 +1194,7 @@ static int plan_g_rows(Cell *c) {
     GLIF_HIP(hipMemcpy(c->g_type, gtype.data(), gtype.size(), hipMemcpyHostToDevice));
     c->g_rows = c->g_compact_rows = gk;
     c->g_compact = true;
+    c->push_typed = c->basis_dense;
     return GLIF_OK;
 }
 
@@ -1285,7 +1328,10 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                        w.zbits, event ? nullptr : w.zmask,
                        event ? nullptr : w.abits);
     GLIF_HIP(hipGetLastError());
-    if (event && (rc = launch_fill_u32(w.I, 0u, 2 * static_cast<size_t>(B) * c->N * c->nb, s))) return rc;
+    // event push into per-type slots ([gk][B][N] per tick) or receptor currents ([nb][B][N])
+    const bool typed = event && c->push_typed;
+    const int slots = typed ? c->g_rows : c->nb;
+    if (event && (rc = launch_fill_u32(w.I, 0u, 2 * static_cast<size_t>(B) * c->N * slots, s))) return rc;
     const int64_t BNs = static_cast<int64_t>(B) * c->N;
     hipLaunchKernelGGL(k_state_layout, dim3(ceil_div(BNs, kBlock)), dim3(kBlock), 0, s, st->psc_rise, st->psc,
                        st->asc, w.R, w.P, w.A, BNs, c->nb, 1);
@@ -1332,6 +1378,8 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     sa.bkg_ell_len = tb->ell_len;
     sa.n_bkg = static_cast<int32_t>(tb->n_cols);
     sa.basis = tr->basis;
+    sa.gk = typed ? c->g_rows : 0;
+    sa.gtype = c->g_type;
 
     PushArgs pa{};
     pa.D = c->D;
@@ -1345,14 +1393,15 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     pa.lgn = 1;
     pa.zbits = w.zbits;
     pa.W = c->W;
+    pa.typed = typed ? 1 : 0;
     pa.rec_colptr = tr->col_ptr;
-    pa.rec_ps = tr->ps;
+    pa.rec_ps = typed ? tr->cps : tr->ps;
     pa.rec_w = tr->w_col;
     pa.lgn_off = w.lgn_off;
     pa.lgn_pre = w.lgn_pre;
     pa.lgn_mask = w.lgn_mask;
     pa.lgn_colptr = tl->col_ptr;
-    pa.lgn_ps = tl->ps;
+    pa.lgn_ps = typed ? tl->cps : tl->ps;
     pa.lgn_w = tl->w_col;
     pa.basis = tr->basis;
     pa.I = w.I;
@@ -1410,7 +1459,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     // Event mode: tick t's currents accumulate in half t % 2 of I.  One launch per tick runs
     // the step of tick t - 1, whose waves push their spikes' delay-1 events, with the push of
     // tick t's delay-2..D and LGN events (which do not depend on it).
-    float *Ih[2] = {w.I, w.I + static_cast<size_t>(B) * c->N * c->nb};
+    float *Ih[2] = {w.I, w.I + static_cast<size_t>(B) * c->N * slots};
     auto step_args = [&](int t) {
         StepArgs x = sa;
         x.t = t;
@@ -1436,7 +1485,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                 StepArgs x = step_args(t - 1);
                 x.I_next = Ih[t & 1];
                 x.p1_colptr = tr->col_ptr;
-                x.p1_ps = tr->ps;
+                x.p1_ps = typed ? tr->cps : tr->ps;
                 x.p1_w = tr->w_col;
                 ProfScope p(kProfStep, s);
                 launch_step_push(x, static_cast<int>(step_grid.x), early, fused_push_grid, c->nb, lds, s);
@@ -1660,6 +1709,7 @@ int glif_cell_set_g_layout(glif_cell *cc, int32_t compact) {
         return fail(GLIF_EINVAL, "no compact G rows for this cell (some neuron receives > 3/4 of the types)");
     c->g_compact = compact != 0;
     c->g_rows = c->g_compact ? c->g_compact_rows : c->n_types;
+    c->push_typed = c->g_compact && c->basis_dense;
     return GLIF_OK;
 }
 

@@ -140,6 +140,11 @@ struct Cell {
     bool g_compact = false;
     int32_t g_compact_rows = 0;  // compact rows per post the tables carry, 0: none
     uint8_t *g_type = nullptr;  // device [N * g_compact_rows]
+    // event push into per-type slots (with compact rows and a basis with more than one
+    // nonzero receptor in some row): one atomic per synapse event into slot [rank][b][post],
+    // the step folding the slots through the basis, instead of one atomic per receptor
+    bool basis_dense = false;
+    bool push_typed = false;
 };
 
 // Small per-cell constants passed by value to kernels.

@@ -87,6 +87,29 @@ __device__ inline void push_column(int lane_s, int32_t lo, int32_t hi, uint32_t 
     }
 }
 
+// ---- event-driven push of one column into per-type slots ---------------------------
+// As push_column, with one atomic per (synapse, batch entry): (w * mult_b) goes to the
+// synapse's type slot of its post, I[rank * rstride + b * bstride + post] (cps[k] = post |
+// rank << 24, rank = the position of the synapse's type among the types reaching the post);
+// the step then forms each receptor's current as sum over the slots of slot * basis[type][r].
+template <int L, class Mult>
+__device__ inline void push_column_typed(int lane_s, int32_t lo, int32_t hi, uint32_t bmask, Mult mult,
+                                         const uint32_t *__restrict__ cps, const float *__restrict__ w,
+                                         int64_t bstride, int64_t rstride, float *__restrict__ I) {
+    for (int32_t k = lo + lane_s; k < hi; k += L) {
+        const uint32_t p = cps[k];
+        const float wk = w[k];
+        float *base = I + static_cast<int64_t>(p >> 24) * rstride + static_cast<int64_t>(p & kLow24);
+        uint32_t m = bmask;
+        while (m) {
+            const int b = __ffs(m) - 1;
+            m &= m - 1;
+            const float wv = Mult::kOne ? wk : wk * mult(b);
+            if (wv != 0.0f) unsafeAtomicAdd(base + static_cast<int64_t>(b) * bstride, wv);
+        }
+    }
+}
+
 // ---- fused backward of one column (dz and dW) -------------------------------------
 // dz[b] = sum_k w[k] * G[post_k][sid_k][b]   (returned reduced over the sub-wave)
 // dw_col[k] += sum_{b in bmask, ascending} G[post_k][sid_k][b] * mult_b
