@@ -18,6 +18,7 @@ the reference (oracle/) on a bounded prefix of the same workload.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -264,7 +265,12 @@ def bench_op(args):
     from v1_glif_model_amd.ops import SynapseTable
     from v1_glif_model_amd.tables import build_cell_tables
     cfg = sy.config(2)
-    tb = build_cell_tables(sy.make_network(cfg, seed=0))
+    if args.n_basis:
+        cfg = dataclasses.replace(cfg, n_basis=args.n_basis)
+    net = sy.make_network(cfg, seed=0)
+    if args.class_types:
+        net = sy.class_types(net, n_classes=args.class_types)
+    tb = build_cell_tables(net)
     N, D, B, nb = tb.n_neurons, tb.max_delay, 5, tb.n_basis
     t = SynapseTable(np.stack([tb.rec.post, tb.rec.col], -1), tb.rec.syn_id, (N, tb.rec.n_cols), tb.basis,
                      n_delay_slots=D)
@@ -296,7 +302,8 @@ def bench_op(args):
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"config-2 recurrent table: {N} posts, {D} delay slots, {S} synapses, B={B}, "
                                f"z_buf density 0.005 ({events} synapse events per call)",
-                   "neurons": N, "synapses": S, "batch": B},
+                   "neurons": N, "synapses": S, "batch": B, "syn_types": int(tb.basis.shape[0]),
+                   "receptors": int(nb)},
         "us_per_call": {k: round(v, 2) for k, v in out.items()},
         "synaptic_events_per_s": {"fwd_event": round(events / (out["fwd_event"] * 1e-6), 1),
                                   "fwd_deterministic": round(events / (out["fwd_deterministic"] * 1e-6), 1)},

@@ -1395,13 +1395,13 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     pa.W = c->W;
     pa.typed = typed ? 1 : 0;
     pa.rec_colptr = tr->col_ptr;
-    pa.rec_ps = typed ? tr->cps : tr->ps;
+    pa.rec_ps = typed ? tr->cg.ps : tr->ps;
     pa.rec_w = tr->w_col;
     pa.lgn_off = w.lgn_off;
     pa.lgn_pre = w.lgn_pre;
     pa.lgn_mask = w.lgn_mask;
     pa.lgn_colptr = tl->col_ptr;
-    pa.lgn_ps = typed ? tl->cps : tl->ps;
+    pa.lgn_ps = typed ? tl->cg.ps : tl->ps;
     pa.lgn_w = tl->w_col;
     pa.basis = tr->basis;
     pa.I = w.I;
@@ -1485,7 +1485,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                 StepArgs x = step_args(t - 1);
                 x.I_next = Ih[t & 1];
                 x.p1_colptr = tr->col_ptr;
-                x.p1_ps = typed ? tr->cps : tr->ps;
+                x.p1_ps = typed ? tr->cg.ps : tr->ps;
                 x.p1_w = tr->w_col;
                 ProfScope p(kProfStep, s);
                 launch_step_push(x, static_cast<int>(step_grid.x), early, fused_push_grid, c->nb, lds, s);
@@ -1537,7 +1537,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     if ((rc = launch_fill_u32(w.G, 0u, 2 * g_elems, s))) return rc;
     // the grouped row-sliced walk serves 16-float G rows
     const bool cg = c->g_compact;
-    const bool gs = (cg ? tr->n_cgs : tr->n_gs) > 0 && g_row(win_width(B), B) == 16;
+    const bool gs = (cg ? tr->cg.n_gs : tr->n_gs) > 0 && g_row(win_width(B), B) == 16;
     if (dw_rec && (rc = launch_fill_u32(w.dw_rec, 0u, tr->n_syn, s))) return rc;
     if (dw_lgn && (rc = launch_fill_u32(w.dw_lgn, 0u, tl->n_syn, s))) return rc;
     if (dw_bkg && (rc = launch_fill_u32(w.dw_bkg, 0u, tb->n_syn, s))) return rc;
@@ -1577,11 +1577,11 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
 
     // G rows of the {hi | post} entries: syn_id * N + post, or post * g_rows + rank
     const int32_t hm = cg ? 1 : c->N, lm = cg ? c->g_rows : 1;
-    ColArgs ca{tr->n_cols, c->N, c->n_types, 0, tr->ph_ptr, cg ? tr->cph_pw : tr->ph_pw, w.G, 1,
+    ColArgs ca{tr->n_cols, c->N, c->n_types, 0, tr->ph_ptr, cg ? tr->cg.ph_pw : tr->ph_pw, w.G, 1,
                dw_rec ? w.dw_rec : nullptr, nullptr, cg ? 1 : 0};
-    GsArgs ga{tr->n_cols, (tr->n_cols + kGsCols - 1) / kGsCols, 0, cg ? tr->cgs_seg : tr->gs_seg,
-              cg ? tr->cgs_pw : tr->gs_pw, w.G};
-    RecDwArgs da{tr->n_cols, 0, hm, lm, Rg, tr->col_ptr, cg ? tr->cps : tr->ps, w.G, w.dw_rec};
+    GsArgs ga{tr->n_cols, (tr->n_cols + kGsCols - 1) / kGsCols, 0, cg ? tr->cg.gs_seg : tr->gs_seg,
+              cg ? tr->cg.gs_pw : tr->gs_pw, w.G};
+    RecDwArgs da{tr->n_cols, 0, hm, lm, Rg, tr->col_ptr, cg ? tr->cg.ps : tr->ps, w.G, w.dw_rec};
     ActWin act{w.zbits, w.dZ, tr->n_cols, 0, B, c->D, c->W, c->N, ring};
 
     BwdInArgs la{}, ka{};
@@ -1597,7 +1597,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     la.mask = w.lw_mask;
     la.cnt = nullptr;
     la.col_ptr = tl->col_ptr;
-    la.ps = cg ? tl->cps : tl->ps;
+    la.ps = cg ? tl->cg.ps : tl->ps;
     la.dw = w.dw_lgn;
     ka.chunks = chunks_for(tb, kWave);
     ka.n_in = tb->n_cols;
@@ -1606,7 +1606,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     ka.mask = w.kw_mask;
     ka.cnt = w.bkg_cnt;
     ka.col_ptr = tb->col_ptr;
-    ka.ps = cg ? tb->cps : tb->ps;
+    ka.ps = cg ? tb->cg.ps : tb->ps;
     ka.dw = w.dw_bkg;
     const int64_t lgn_units = tl->n_cols * static_cast<int64_t>(la.chunks);
     const int64_t bkg_units = tb->n_cols * static_cast<int64_t>(ka.chunks);

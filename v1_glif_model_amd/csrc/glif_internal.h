@@ -38,6 +38,22 @@ int hip_fail(hipError_t e, const char *what);
         if (e_ != hipSuccess) return hip_fail(e_, #call); \
     } while (0)
 
+// ---- compact G rows of a table ----------------------------------------------
+// The G row of a synapse is post * rows + rank, rank = the position of its syn_id among a
+// per-post set of types (ascending).
+struct CompactRows {
+    int32_t rows = 0;              // rows per post, 0: not built
+    uint8_t *rank_host = nullptr;  // [n_syn] host copy of the ranks, column-grouped order
+    uint32_t *ps = nullptr;        // [n_syn] column-grouped: post | rank << 24
+    uint2 *ph_pw = nullptr;        // [n_syn] type-phased order: {compact row, weight bits}
+    int64_t n_gs = 0;              // grouped row-sliced order over the compact rows (the table's
+    int32_t *gs_seg = nullptr;     // groups of kGsCols columns); 0: not built
+    uint2 *gs_pw = nullptr;
+    int32_t *gs_src = nullptr;
+    uint8_t *gtype = nullptr;      // device [n_post][rows]: syn_id of each rank, 0xFF past the
+                                   // post's types (own rows only; a cell keeps its own)
+};
+
 // ---- device-resident synapse table (one population) -----------------------
 // Column-grouped ("CSC", the reference's pre_ind_table) and post-grouped ("CSR")
 // copies of the same synapses.  Index k runs over the column-grouped order,
@@ -96,23 +112,17 @@ struct Table {
     uint2 *gs_pw = nullptr;       // [n_gs]        {row | column-in-group << kGsRowBits, weight bits}
     int32_t *gs_src = nullptr;    // [n_gs]        column-grouped position of the synapse, -1 for padding
     float *basis_host = nullptr;  // host copy [n_types][n_basis]
-    // compact G rows, set by a cell whose posts each receive few of the synapse types: the G
-    // row of a synapse is post * g_rows + rank, rank = the position of its syn_id among the
-    // types that reach that post from any of the cell's populations (ascending).  The
-    // type-major copies above stay as they are (the op-level entry points use them).
-    // g_rows = 0: not set.
-    int32_t g_rows = 0;
-    uint8_t *g_rank_host = nullptr;  // [n_syn] host copy of the ranks, column-grouped order
-    uint32_t *cps = nullptr;      // [n_syn] column-grouped: post | rank << 24
-    uint2 *cph_pw = nullptr;      // [n_syn] type-phased order: {compact row, weight bits}
-    int64_t n_cgs = 0;            // the grouped row-sliced order over compact rows (n_groups
-    int32_t *cgs_seg = nullptr;   // groups, as gs_*); n_cgs = 0: not built
-    uint2 *cgs_pw = nullptr;
-    int32_t *cgs_src = nullptr;
+    // Compact G rows: a G row per (post, type reaching the post) instead of per (type, post).
+    // cg: set by a cell, over the types reaching each post from any of its three populations;
+    // og: the table's own types per post, built at creation (the op-level backward uses it).
+    // Each is built only when no post receives more than three quarters of the types.  The
+    // type-major copies above stay as they are.
+    CompactRows cg, og;
 };
 
-// Give a table compact G rows (rank: [n_syn] in column-grouped order, each < g_rows).  A table
-// that already has them keeps them if they are the same, else GLIF_EINVAL.  Synchronous.
+// Give a table a cell's compact G rows (Table::cg; rank: [n_syn] in column-grouped order, each
+// < g_rows).  A table that already has them keeps them if they are the same, else GLIF_EINVAL.
+// Synchronous.
 int table_set_g_rows(Table *t, const uint8_t *rank, int32_t g_rows);
 
 // ---- cell ------------------------------------------------------------------

@@ -85,6 +85,32 @@ __global__ void __launch_bounds__(kBlock)
     write_G(G, n, b, Bp, d, basis_lds, n_types, nb, n_post);
 }
 
+// G over a table's own compact rows: G[n * rows + q][b] = sum_r dy[b][n][r] * basis[gtype[n][q]][r]
+// (sequential r as write_G), 0 past the post's types.
+__global__ void __launch_bounds__(kBlock)
+    k_make_G_compact(const float *__restrict__ dy, int32_t B, int32_t n_post, int Bp,
+                     const float *__restrict__ basis, int n_types, int nb, const uint8_t *__restrict__ gtype,
+                     int rows, float *__restrict__ G) {
+    extern __shared__ float basis_lds[];
+    load_basis_lds(basis_lds, basis, n_types * nb);
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gt >= static_cast<int64_t>(B) * n_post) return;
+    const int b = static_cast<int>(gt / n_post);
+    const int64_t n = gt % n_post;
+    float d[kMaxBasis];
+    for (int r = 0; r < nb; ++r) d[r] = dy[gt * nb + r];
+    for (int q = 0; q < rows; ++q) {
+        const int s = gtype[n * rows + q];
+        float e = 0.0f;
+        if (s != 0xFF) {
+            const float *bs = basis_lds + s * nb;
+            e = d[0] * bs[0];
+            for (int r = 1; r < nb; ++r) e = e + d[r] * bs[r];
+        }
+        G[(n * rows + q) * Bp + b] = e;
+    }
+}
+
 // Batch masks and "active in some batch entry" bitmaps of a dense z [B][n_cols] in the
 // row pull's layout: slot plane n_slots - d holds column pre + n_pre * (d - 1) at bit
 // pre (planes of pre_pad = round64(n_pre) bits); one thread per (plane, pre), one wave per
@@ -125,7 +151,7 @@ __global__ void __launch_bounds__(kBlock) k_syn_bwd_gs(GsArgs a, ActDense act) {
 // G[sid][post][b] times the input value (counts) or 1 (spikes).
 struct SynDwArgs {
     int64_t n_cols;
-    int32_t B, n_post, R, counts;
+    int32_t B, hm, lm, R, counts;  // G row of entry p: (p >> 24) * hm + (p & kLow24) * lm
     const float *z;  // [B][n_cols]
     const int32_t *col_ptr;
     const uint32_t *ps;
@@ -176,7 +202,7 @@ __global__ void __launch_bounds__(kBlock) k_syn_bwd_dw(SynDwArgs a) {
             for (int u = 0; u < 4; ++u) {
                 const int32_t k = min(k0 + 16 * u + sl, chi - 1);
                 const uint32_t p = a.ps[k];
-                gp[u] = a.G + (static_cast<int64_t>(p >> 24) * a.n_post + (p & kLow24)) * a.R;
+                gp[u] = a.G + (static_cast<int64_t>(p >> 24) * a.hm + static_cast<int64_t>(p & kLow24) * a.lm) * a.R;
                 d[u] = 0.0f;
             }
             uint32_t mb = mm;
@@ -228,7 +254,9 @@ static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes, bool 
     w.cols = cv.take<int32_t>(t->n_cols);
     w.masks = cv.take<uint32_t>(t->n_cols);
     w.scratch = cv.take<char>(compact_scratch_bytes(1, t->n_cols));
-    if (with_G) w.G = cv.take<float>(static_cast<size_t>(t->n_post) * t->n_types * batch_pad(B));
+    // G: a row per (type, post), or per (post, own type) with the table's compact rows
+    const int rows = t->og.rows ? t->og.rows : t->n_types;
+    if (with_G) w.G = cv.take<float>(static_cast<size_t>(t->n_post) * rows * batch_pad(B));
     if (bytes) *bytes = cv.off;
     return w;
 }
@@ -396,24 +424,33 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     if (!ws || ws_bytes < need) return fail(GLIF_ENOMEM, "workspace too small");
     SynWs w = carve_syn(ws, t, B, nullptr);
     const int Bp = batch_pad(B);
-    if (static_cast<int64_t>(t->n_types) * t->n_post * Bp * 4 >= (int64_t(1) << 32))
-        return fail(GLIF_ERANGE, "n_types * n_post * padded batch * 4 bytes must be < 4 GiB");
+    // the table's own compact rows (post * rows + rank) when it has them, else type-major rows
+    const CompactRows &oc = t->og;
+    const bool cmp = oc.rows > 0;
+    const int rows = cmp ? oc.rows : t->n_types;
+    if (static_cast<int64_t>(rows) * t->n_post * Bp * 4 >= (int64_t(1) << 32))
+        return fail(GLIF_ERANGE, "G rows per post * n_post * padded batch * 4 bytes must be < 4 GiB");
     ProfScope prof(kProfSynBwd, s);
     const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     int rc;
-    if (B < Bp && (rc = launch_fill_u32(w.G, 0u, static_cast<size_t>(t->n_post) * t->n_types * Bp, s)))
+    if (B < Bp && (rc = launch_fill_u32(w.G, 0u, static_cast<size_t>(t->n_post) * rows * Bp, s)))
         return rc;
     const int64_t nI = static_cast<int64_t>(B) * t->n_post;
-    hipLaunchKernelGGL(k_make_G, dim3(ceil_div(nI, kBlock)), dim3(kBlock), lds, s, dy, B, t->n_post, Bp,
-                       t->basis, t->n_types, t->n_basis, w.G);
+    if (cmp)
+        hipLaunchKernelGGL(k_make_G_compact, dim3(ceil_div(nI, kBlock)), dim3(kBlock), lds, s, dy, B, t->n_post, Bp,
+                           t->basis, t->n_types, t->n_basis, oc.gtype, rows, w.G);
+    else
+        hipLaunchKernelGGL(k_make_G, dim3(ceil_div(nI, kBlock)), dim3(kBlock), lds, s, dy, B, t->n_post, Bp,
+                           t->basis, t->n_types, t->n_basis, w.G);
     GLIF_HIP(hipGetLastError());
     // one pass writes every active synapse's dW once, in reference order; the rest stay 0
     if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
-    if (t->n_gs && (Bp == 8 || Bp == 16)) {
+    if ((cmp ? oc.n_gs : t->n_gs) && (Bp == 8 || Bp == 16)) {
         // the grouped row-sliced walk for dz, then the active columns' dW
         ActDense act{z, dz, t->n_cols, counts};
         if (dz) {
-            GsArgs ga{t->n_cols, t->n_groups, B, t->gs_seg, t->gs_pw, w.G};
+            GsArgs ga{t->n_cols, (t->n_cols + kGsCols - 1) / kGsCols, B, cmp ? oc.gs_seg : t->gs_seg,
+                      cmp ? oc.gs_pw : t->gs_pw, w.G};
             const int LG = Bp / 4;
             const dim3 grid(ceil_div(t->n_groups * LG, kBlock));
             if (LG == 2) hipLaunchKernelGGL(k_syn_bwd_gs<2>, grid, dim3(kBlock), 0, s, ga, act);
@@ -421,13 +458,15 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
             GLIF_HIP(hipGetLastError());
         }
         if (dw) {
-            SynDwArgs da{t->n_cols, B, t->n_post, Bp, counts, z, t->col_ptr, t->ps, t->order, w.G, dw};
+            SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->col_ptr,
+                         cmp ? oc.ps : t->ps, t->order, w.G, dw};
             hipLaunchKernelGGL(k_syn_bwd_dw, dim3(ceil_div(t->n_cols, kBlock)), dim3(kBlock), 0, s, da);
             GLIF_HIP(hipGetLastError());
         }
         return GLIF_OK;
     }
-    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, t->ph_pw, w.G, dz ? 1 : 0, dw, t->ph_order};
+    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, cmp ? oc.ph_pw : t->ph_pw, w.G, dz ? 1 : 0, dw,
+               t->ph_order, cmp ? 1 : 0};
     ActDense act{z, dz, t->n_cols, counts};
     const dim3 grid(ceil_div(t->n_cols * (Bp / 4), kBlock));
     switch (Bp / 4) {

@@ -2,6 +2,7 @@
 // orders (pre_ind_table and the preprocessed copies), their upload, the weight-shadow refresh, and shared helpers.
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "glif_internal.h"
@@ -148,11 +149,13 @@ static void free_table(Table *t) {
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
                     t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
                     t->chunk_desc, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src,
-                    t->cps, t->cph_pw, t->cgs_seg, t->cgs_pw, t->cgs_src};
+                    t->cg.ps, t->cg.ph_pw, t->cg.gs_seg, t->cg.gs_pw, t->cg.gs_src, t->cg.gtype,
+                    t->og.ps, t->og.ph_pw, t->og.gs_seg, t->og.gs_pw, t->og.gs_src, t->og.gtype};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete[] t->basis_host;
-    delete[] t->g_rank_host;
+    delete[] t->cg.rank_host;
+    delete[] t->og.rank_host;
     delete t;
 }
 
@@ -163,11 +166,67 @@ static int download(std::vector<T> &dst, const T *src, size_t n) {
     return GLIF_OK;
 }
 
+// Compact rows from host arrays over the column-grouped positions k: col_ptr [n_cols + 1],
+// ps[k] = post | syn_id << 24, ph_src [n_syn] (column-grouped position of each type-phased
+// position) and rank[k] < rows.  Uploads ps / ph_pw / the grouped order into out (weights
+// +0: the caller gathers them from w_col) and keeps a host copy of the ranks.
+static int build_compact(const Table *t, const int32_t *col_ptr, const uint32_t *ps, const int32_t *ph_src,
+                         const uint8_t *rank, int32_t rows, CompactRows &out) {
+    const int64_t n = t->n_syn;
+    std::vector<int64_t> row(n), col(n);
+    std::vector<int32_t> src(n);
+    std::vector<uint32_t> cps(n);
+    for (int64_t c = 0; c < t->n_cols; ++c)
+        for (int32_t k = col_ptr[c]; k < col_ptr[c + 1]; ++k) col[k] = c;
+    for (int64_t k = 0; k < n; ++k) {
+        const uint32_t post = ps[k] & kLow24;
+        row[k] = static_cast<int64_t>(post) * rows + rank[k];
+        cps[k] = post | static_cast<uint32_t>(rank[k]) << 24;
+        src[k] = static_cast<int32_t>(k);
+    }
+    std::vector<uint2> cph_pw(n);
+    for (int64_t k = 0; k < n; ++k) cph_pw[k] = make_uint2(static_cast<uint32_t>(row[ph_src[k]]), 0u);
+    std::vector<int32_t> gs_seg, gs_src;
+    std::vector<uint2> gs_pw;
+    int64_t n_groups = 0, n_gs = 0;
+    build_gs(n, t->n_cols, static_cast<int64_t>(t->n_post) * rows, row.data(), col.data(), src.data(), n_groups,
+             n_gs, gs_seg, gs_pw, gs_src);
+    int rc;
+    if ((rc = upload(&out.ps, cps.data(), cps.size())) || (rc = upload(&out.ph_pw, cph_pw.data(), cph_pw.size())) ||
+        (n_gs && (rc = upload(&out.gs_seg, gs_seg.data(), gs_seg.size()))) ||
+        (n_gs && (rc = upload(&out.gs_pw, gs_pw.data(), gs_pw.size()))) ||
+        (n_gs && (rc = upload(&out.gs_src, gs_src.data(), gs_src.size()))))
+        return rc;
+    out.n_gs = n_gs;
+    out.rank_host = new uint8_t[std::max<int64_t>(n, 1)];
+    if (n) std::memcpy(out.rank_host, rank, n);
+    out.rows = rows;
+    return GLIF_OK;
+}
+
+// the weights of a table's compact copies, gathered from w_col
+static int gather_compact_weights(const Table *t, const CompactRows &c, hipStream_t s) {
+    if (c.rows && t->n_syn) {
+        hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(t->n_syn)), dim3(kBlock), 0, s, c.ph_pw, t->w_col,
+                           t->ph_src, t->n_syn);
+        GLIF_HIP(hipGetLastError());
+    }
+    if (c.n_gs) {
+        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(c.n_gs)), dim3(kBlock), 0, s, c.gs_pw, t->w_col, c.gs_src,
+                           c.n_gs);
+        GLIF_HIP(hipGetLastError());
+    }
+    return GLIF_OK;
+}
+
 int table_set_g_rows(Table *t, const uint8_t *rank, int32_t g_rows) {
     if (g_rows <= 0 || g_rows > 255) return fail(GLIF_EINVAL, "compact G rows per post must be in [1, 255]");
+    // cells created from several threads may share a table
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
     const int64_t n = t->n_syn;
-    if (t->g_rows) {
-        if (t->g_rows == g_rows && (n == 0 || std::memcmp(t->g_rank_host, rank, n) == 0)) return GLIF_OK;
+    if (t->cg.rows) {
+        if (t->cg.rows == g_rows && (n == 0 || std::memcmp(t->cg.rank_host, rank, n) == 0)) return GLIF_OK;
         return fail(GLIF_EINVAL, "table already carries a different compact G row map (one per table)");
     }
     for (int64_t k = 0; k < n; ++k)
@@ -179,46 +238,48 @@ int table_set_g_rows(Table *t, const uint8_t *rank, int32_t g_rows) {
     if ((rc = download(col_ptr, t->col_ptr, static_cast<size_t>(t->n_cols) + 1)) ||
         (rc = download(ps, t->ps, n)) || (rc = download(ph_src, t->ph_src, n)))
         return rc;
-    // per column-grouped position k: compact row and column
-    std::vector<int64_t> row(n), col(n);
-    std::vector<int32_t> src(n);
-    std::vector<uint32_t> cps(n);
-    for (int64_t c = 0; c < t->n_cols; ++c)
-        for (int32_t k = col_ptr[c]; k < col_ptr[c + 1]; ++k) col[k] = c;
-    for (int64_t k = 0; k < n; ++k) {
-        const uint32_t post = ps[k] & kLow24;
-        row[k] = static_cast<int64_t>(post) * g_rows + rank[k];
-        cps[k] = post | static_cast<uint32_t>(rank[k]) << 24;
-        src[k] = static_cast<int32_t>(k);
-    }
-    std::vector<uint2> cph_pw(n);
-    for (int64_t k = 0; k < n; ++k) cph_pw[k] = make_uint2(static_cast<uint32_t>(row[ph_src[k]]), 0u);
-    std::vector<int32_t> gs_seg, gs_src;
-    std::vector<uint2> gs_pw;
-    int64_t n_groups = 0, n_gs = 0;
-    build_gs(n, t->n_cols, static_cast<int64_t>(t->n_post) * g_rows, row.data(), col.data(), src.data(), n_groups,
-             n_gs, gs_seg, gs_pw, gs_src);
-    if ((rc = upload(&t->cps, cps.data(), cps.size())) || (rc = upload(&t->cph_pw, cph_pw.data(), cph_pw.size())) ||
-        (n_gs && (rc = upload(&t->cgs_seg, gs_seg.data(), gs_seg.size()))) ||
-        (n_gs && (rc = upload(&t->cgs_pw, gs_pw.data(), gs_pw.size()))) ||
-        (n_gs && (rc = upload(&t->cgs_src, gs_src.data(), gs_src.size()))))
-        return rc;
-    t->n_cgs = n_gs;
-    t->g_rank_host = new uint8_t[std::max<int64_t>(n, 1)];
-    if (n) std::memcpy(t->g_rank_host, rank, n);
-    t->g_rows = g_rows;
+    if ((rc = build_compact(t, col_ptr.data(), ps.data(), ph_src.data(), rank, g_rows, t->cg))) return rc;
     // the weights the table already holds (later ones arrive through glif_table_set_weights)
-    if (n) {
-        hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(n)), dim3(kBlock), 0, 0, t->cph_pw, t->w_col, t->ph_src, n);
-        GLIF_HIP(hipGetLastError());
-    }
-    if (n_gs) {
-        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(n_gs)), dim3(kBlock), 0, 0, t->cgs_pw, t->w_col, t->cgs_src,
-                           n_gs);
-        GLIF_HIP(hipGetLastError());
-    }
+    if ((rc = gather_compact_weights(t, t->cg, nullptr))) return rc;
     GLIF_HIP(hipDeviceSynchronize());
     return GLIF_OK;
+}
+
+// The table's own compact rows (Table::og) when no post receives more than three quarters of
+// the types: ranks over each post's own types.
+static int build_own_rows(Table *t, const int32_t *col_ptr, const uint32_t *ps, const int32_t *ph_src) {
+    const int nt = t->n_types, words = (nt + 63) / 64;
+    if (nt > 255 || t->n_syn == 0) return GLIF_OK;  // 0xFF marks an unused rank
+    std::vector<uint64_t> seen(static_cast<size_t>(t->n_post) * words, 0ull);
+    for (int64_t k = 0; k < t->n_syn; ++k) {
+        const uint32_t sid = ps[k] >> 24;
+        seen[static_cast<size_t>(ps[k] & kLow24) * words + sid / 64] |= 1ull << (sid % 64);
+    }
+    int gk = 1;
+    for (int32_t n = 0; n < t->n_post; ++n) {
+        int cnt = 0;
+        for (int q = 0; q < words; ++q) cnt += __builtin_popcountll(seen[static_cast<size_t>(n) * words + q]);
+        gk = std::max(gk, cnt);
+    }
+    if (gk * 4 > nt * 3) return GLIF_OK;
+    std::vector<uint8_t> rank(t->n_syn), gtype(static_cast<size_t>(t->n_post) * gk, 0xFF);
+    for (int64_t k = 0; k < t->n_syn; ++k) {
+        const uint32_t sid = ps[k] >> 24;
+        const uint64_t *sn = &seen[static_cast<size_t>(ps[k] & kLow24) * words];
+        int r = 0;
+        for (uint32_t q = 0; q < sid / 64; ++q) r += __builtin_popcountll(sn[q]);
+        r += __builtin_popcountll(sid % 64 ? sn[sid / 64] & ((1ull << (sid % 64)) - 1ull) : 0ull);
+        rank[k] = static_cast<uint8_t>(r);
+    }
+    for (int32_t n = 0; n < t->n_post; ++n) {
+        int q = 0;
+        for (int sid = 0; sid < nt; ++sid)
+            if ((seen[static_cast<size_t>(n) * words + sid / 64] >> (sid % 64)) & 1ull)
+                gtype[static_cast<size_t>(n) * gk + q++] = static_cast<uint8_t>(sid);
+    }
+    int rc;
+    if ((rc = build_compact(t, col_ptr, ps, ph_src, rank.data(), gk, t->og))) return rc;
+    return upload(&t->og.gtype, gtype.data(), gtype.size());
 }
 
 }  // namespace glif
@@ -419,6 +480,10 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         }
         if (n_syn) (void)hipMemset(*wp, 0, n_syn * sizeof(float));
     }
+    if ((rc = build_own_rows(t, col_ptr.data(), ps.data(), ph_src.data()))) {
+        free_table(t);
+        return rc;
+    }
     *out = reinterpret_cast<glif_table *>(t);
     return GLIF_OK;
 }
@@ -454,16 +519,10 @@ int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
                            t->gs_src, t->n_gs);
         GLIF_HIP(hipGetLastError());
     }
-    if (t->g_rows && t->n_syn) {  // the compact-row copies of a cell's tables
-        hipLaunchKernelGGL(k_gather_pair_w, dim3(grid_for(t->n_syn)), dim3(kBlock), 0, s, t->cph_pw, t->w_col,
-                           t->ph_src, t->n_syn);
-        GLIF_HIP(hipGetLastError());
-    }
-    if (t->n_cgs) {
-        hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(t->n_cgs)), dim3(kBlock), 0, s, t->cgs_pw, t->w_col,
-                           t->cgs_src, t->n_cgs);
-        GLIF_HIP(hipGetLastError());
-    }
+    // the compact-row copies (a cell's, the table's own)
+    int rcc = gather_compact_weights(t, t->cg, s);
+    if (!rcc) rcc = gather_compact_weights(t, t->og, s);
+    if (rcc) return rcc;
     if (t->ell_len) {
         const int64_t n_ell = static_cast<int64_t>(t->ell_len) * t->n_post;
         hipLaunchKernelGGL(k_gather_ell_w, dim3(grid_for(n_ell)), dim3(kBlock), 0, s, t->ell_pw, w, t->ell_src,
