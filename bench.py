@@ -423,12 +423,22 @@ def main():
         step()
     torch.cuda.synchronize()
     sc_host = spike_count.cpu().numpy()
-    if not args.forward_only:
-        dominant = "bwd_rec"
-    else:
-        # event mode: one fused launch per tick (the step of t - 1 beside the pushes), timed
-        # as "step"; deterministic mode: the row pull, timed as "push"
-        dominant = "push" if args.mode == "deterministic" else "step"
+    # one more, untimed step with every kernel class timed: the breakdown, and the dominant
+    # class (most time per step), whose launches the timed steps bracket with HIP events.
+    # Event mode's forward is one fused launch per tick (the step of t - 1 beside the pushes,
+    # "step"); deterministic mode's row pull is "push"; "adj" is the adjoint launch with the
+    # previous window's weight gradients and the rest of its dz walk; "bwd_rec" the dz walk
+    # over the columns the next adjoint reads.
+    _lib.prof_enable(list(_lib.PROF_KINDS))
+    step()
+    torch.cuda.synchronize()
+    breakdown = {k: {"ms_per_step": round(v[0], 3), "launches": v[1]} for k, v in _lib.prof_collect().items()}
+    _lib.prof_enable([])
+    dominant = max(breakdown, key=lambda k: breakdown[k]["ms_per_step"])
+    # a class launched once per tick is sampled (about 50 bracketed launches per step): two
+    # event records per launch would cost more host time than the launches themselves
+    stride = max(1, breakdown[dominant]["launches"] // 50)
+    _lib.prof_stride(stride)
     _lib.prof_enable([dominant])
     _lib.prof_collect()
     fwd_ms = bwd_ms = 0.0
@@ -443,12 +453,7 @@ def main():
     wall = time.perf_counter() - t0
     prof = _lib.prof_collect()
     _lib.prof_enable([])
-    # one more, untimed step with every kernel class timed, for the breakdown
-    _lib.prof_enable(list(_lib.PROF_KINDS))
-    step()
-    torch.cuda.synchronize()
-    breakdown = {k: {"ms_per_step": round(v[0], 3), "launches": v[1]} for k, v in _lib.prof_collect().items()}
-    _lib.prof_enable([])
+    _lib.prof_stride(1)
 
     ms_per_step = wall * 1000.0 / args.steps
     value = B * N * T / (ms_per_step / 1000.0)
@@ -464,26 +469,48 @@ def main():
         Rg *= 2
     words = (N + 63) // 64
     tot_ms, launches = prof.get(dominant, (0.0, 0))
+    # the grouped dz walk (16-float G rows) with the weight gradients deferred splits each
+    # window's walk: the columns of delays <= 2 Wwin - 3 (what the next window's adjoint reads,
+    # rounded up to whole waves of 16 four-column groups) in its own launch, the rest in the
+    # next adjoint's launch (libglif's glif_cell_backward)
+    n_cols = D * N
+    n_groups = (n_cols + 3) // 4
+    split = Rg == 16 and not args.forward_only
+    if split:
+        g = (max(0, 2 * Wwin - 3) * N + 3) // 4
+        cols_a = min(n_cols, min(n_groups, (g + 15) // 16 * 16) * 4)
+    else:
+        cols_a = n_cols
+    s_a = int(np.count_nonzero(tb.rec.col < cols_a))
+    windows = max(T - 2, 1) / Wwin
     if dominant == "bwd_rec":
         # per launch = one backward window of Wwin timesteps (the last window may be
-        # shorter; launches = ceil((T-2)/Wwin)): one 8-byte table entry per synapse
-        # (G row + weight) and per-column pointers once, the dz rows of the window's
-        # steps, the G projection read once, spike words, and the dW read-modify-write
-        # of the window's active events (the algorithm's bytes, whichever table layout
-        # the library walks)
-        steps_per_launch = (T - 2) / max(launches / args.steps, 1)
-        if Rg == 16:
-            # the grouped dz walk alone (the window's weight gradients run with the next
-            # window's adjoint): one 8-byte entry per synapse, the per-column pointers, the
-            # dz rows of the window's steps, G read once
-            alg_bytes = (S * 8 + (D * N + 1) * 4 + steps_per_launch * B * D * N * 4 + N * nt * Rg * 4)
-            unit_desc = f"bytes per backward window of {Wwin} timesteps (recurrent dz)"
+        # shorter)
+        steps_per_launch = (T - 2) / max(breakdown[dominant]["launches"], 1)
+        if split:
+            # the first part of the grouped dz walk: one 8-byte table entry per synapse of
+            # its columns, their pointers, the dz rows of the window's steps, G read once
+            alg_bytes = (s_a * 8 + (cols_a + 1) * 4 + steps_per_launch * B * cols_a * 4 + N * nt * Rg * 4)
+            unit_desc = (f"bytes per backward window of {Wwin} timesteps (recurrent dz, the {cols_a} columns "
+                         f"of delays <= {max(0, 2 * Wwin - 3)})")
         else:
             # dz and the dW of the window's active events in one pass
             active = e_rec / max(T, 1) * steps_per_launch
             alg_bytes = (S * 8 + (nt * D * N + 1) * 4 + steps_per_launch * B * D * N * 4 + N * nt * Rg * 4
                          + (steps_per_launch + D) * B * words * 8 + active * 8)
             unit_desc = f"bytes per backward window of {Wwin} timesteps (recurrent dz + dW)"
+    elif dominant == "adj":
+        # per launch = one backward window: the adjoint's state stream per (b, n) and tick
+        # (D dz values, saved voltage, refractory bit; gV, gP, gR read and written once per
+        # launch), its G rows written; the previous window's recurrent and LGN dW (per active
+        # synapse event: 4-byte entry, the dW read and written, one G element) and the rest of
+        # its dz walk (8-byte entries of the other columns, their pointers and dz rows)
+        rows = cell.g_layout()[0]
+        act_ev = (e_rec + e_lgn) / max(T, 1) * Wwin
+        alg_bytes = (Wwin * B * N * (D * 4 + 4) + Wwin * B * words * 8 + 2 * B * N * (1 + 2 * nb) * 4
+                     + N * rows * Rg * 4 + act_ev * 16
+                     + (S - s_a) * 8 + (n_cols - cols_a + 1) * 4 + Wwin * B * (n_cols - cols_a) * 4)
+        unit_desc = f"bytes per backward window of {Wwin} timesteps (adjoint + previous window's dW and dz rest)"
     elif dominant == "step":
         # per launch = one tick: the GLIF_3 step's state stream per (b, n) -- reads I, R, P
         # (nb floats each), A (2 floats), v, r (int16); writes I (cleared), R, P, A, v, r and
@@ -507,7 +534,8 @@ def main():
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic.get("bytes_per_launch") if traffic else None,
                 "algorithmic_bytes_per_launch": int(alg_bytes), "basis": unit_desc,
-                "avg_launch_us": round(avg_ms * 1000.0, 2), "launches_timed": launches}
+                "avg_launch_us": round(avg_ms * 1000.0, 2), "launches_timed": launches,
+                "launch_sampling": f"every {stride} of the kernel's launches" if stride > 1 else "every launch"}
     if traffic and avg_ms > 0:
         # the measured L2 <-> memory-fabric bytes (FETCH_SIZE + WRITE_SIZE: HBM and
         # Infinity Cache) over the same live launch time

@@ -272,11 +272,13 @@ int glif_sample_poisson(float lam, float exp_neg_lam, int64_t n, uint64_t seed, 
  * 4 bwd_lgn, 5 bwd_bkg, 6 syn_fwd, 7 syn_bwd.  In the cell's event mode "step" is the
  * one launch per tick that runs the step beside that tick's pushes and "push" only the
  * push of tick 0; in deterministic mode "push" is the row pull.  "adj" includes the
- * previous window's weight-gradient passes that share its launch.  While bit k of `mask` is set, every
- * launch of class k is bracketed by two HIP events on its stream.
+ * previous window's weight-gradient passes and the rest of its dz walk, which share its launch.
+ * While bit k of `mask` is set, every launch of class k (every `every`-th, glif_prof_stride,
+ * counted from glif_prof_enable; default 1) is bracketed by two HIP events on its stream.
  * glif_prof_collect waits for the recorded events and returns, per class, the
- * summed elapsed milliseconds and the number of launches since the last collect. */
+ * summed elapsed milliseconds and the number of bracketed launches since the last collect. */
 int glif_prof_enable(uint32_t mask);
+int glif_prof_stride(int32_t every);
 int glif_prof_collect(double *total_ms, int64_t *count, int32_t n);
 const char *glif_prof_name(int32_t kind);
 

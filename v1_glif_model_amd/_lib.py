@@ -73,6 +73,7 @@ SIGNATURES = {
     "glif_sample_bernoulli": (C.c_int, [vp, i64, C.c_uint64, C.c_uint64, vp, vp]),
     "glif_sample_poisson": (C.c_int, [C.c_float, C.c_float, i64, C.c_uint64, C.c_uint64, vp, vp]),
     "glif_prof_enable": (C.c_int, [C.c_uint32]),
+    "glif_prof_stride": (C.c_int, [i32]),
     "glif_prof_collect": (C.c_int, [vp, vp, i32]),
     "glif_prof_name": (C.c_char_p, [i32]),
 }
@@ -138,6 +139,11 @@ def prof_enable(kinds):
     for k in kinds:
         mask |= 1 << PROF_KINDS.index(k)
     check(lib().glif_prof_enable(mask))
+
+
+def prof_stride(every: int):
+    """Bracket only every `every`-th launch of an enabled class (1: all)."""
+    check(lib().glif_prof_stride(int(every)))
 
 
 def prof_collect():

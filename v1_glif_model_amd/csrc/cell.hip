@@ -12,9 +12,10 @@
 //                 background and does the same update.
 // Backward, in windows of Wwin reverse ticks t0, t0-1, .. (lagged adjoint, k_adj):
 //   k_adj         per tick t: gz_t -> gV_t -> gP_{t-1} -> gR_{t-2} -> G_{t-2}
-//   k_bwd_rec_gs  dz of the window's steps t0-2, t0-3, .. over every recurrent
-//                 column, one pass over the grouped row-sliced table per window (16-float
-//                 G rows), then k_bwd_rec_dw: dW of the window's active columns;
+//   k_bwd_rec_gs  dz of the window's steps t0-2, t0-3, .. over the recurrent columns
+//                 of delays <= 2 Wwin - 3, one pass over the grouped row-sliced table
+//                 (16-float G rows); the other columns' dz and the dW of the window's
+//                 active columns run in the next window's adjoint launch (k_adj_dw);
 //                 other row lengths: k_bwd_rec, dz and dW in one type-phased pass
 //   k_bwd_in      dW of the LGN / background events of the window's steps
 // A window is legal because dz_s depends only on dz_{>= s+3}: a spike reaches the
@@ -875,7 +876,7 @@ __global__ void __launch_bounds__(kBlock) k_bwd_rec(ColArgs a, ActWin act) {
 
 __global__ void __launch_bounds__(kBlock) k_bwd_rec_gs(GsArgs a, ActWin act) {
     __shared__ float stage[kBlock / kWave * kGsStage];
-    bwd_groups<4>(a, act, stage);
+    bwd_groups<4>(a, act, stage, blockIdx.x);
 }
 
 // dW of one window's active recurrent columns next to the grouped walk (which computes
@@ -1020,43 +1021,44 @@ __device__ inline void bwd_in_body(const BwdInArgs &a, int64_t bid, int64_t nblk
 static void launch_bwd_rec(const ColArgs &ca, int R, const ActWin &act, hipStream_t s) {
     const int LG = R / 4;
     const dim3 grid(ceil_div(ca.n_cols * LG, kBlock));
-    if (LG == 1) hipLaunchKernelGGL(k_bwd_rec<1>, grid, dim3(kBlock), 0, s, ca, act);
-    else if (LG == 2) hipLaunchKernelGGL(k_bwd_rec<2>, grid, dim3(kBlock), 0, s, ca, act);
-    else if (LG == 4) hipLaunchKernelGGL(k_bwd_rec<4>, grid, dim3(kBlock), 0, s, ca, act);
-    else hipLaunchKernelGGL(k_bwd_rec<8>, grid, dim3(kBlock), 0, s, ca, act);
+    if (LG == 1) GLIF_PROF_LAUNCH(k_bwd_rec<1>, grid, dim3(kBlock), 0, s, ca, act);
+    else if (LG == 2) GLIF_PROF_LAUNCH(k_bwd_rec<2>, grid, dim3(kBlock), 0, s, ca, act);
+    else if (LG == 4) GLIF_PROF_LAUNCH(k_bwd_rec<4>, grid, dim3(kBlock), 0, s, ca, act);
+    else GLIF_PROF_LAUNCH(k_bwd_rec<8>, grid, dim3(kBlock), 0, s, ca, act);
 }
 
-__global__ void __launch_bounds__(kBlock) k_bwd_rec_dw(RecDwArgs a, ActWin act) { rec_dw_body(a, act, blockIdx.x); }
 
 template <bool COUNTS>
 __global__ void __launch_bounds__(kBlock) k_bwd_in(BwdInArgs a) {
     bwd_in_body<COUNTS>(a, blockIdx.x, gridDim.x);
 }
 
-// The recurrent dW pass and the LGN dW of one window in one launch: blocks [0, rec_blocks)
-// run the first, the rest the second.  Both are chains of dependent loads with little
-// traffic, so sharing the machine overlaps their latencies.
-__global__ void __launch_bounds__(kBlock) k_bwd_dw_rec_lgn(RecDwArgs a, ActWin act, BwdInArgs la, int rec_blocks) {
-    if (static_cast<int>(blockIdx.x) < rec_blocks)
-        rec_dw_body(a, act, blockIdx.x);
-    else
-        bwd_in_body<false>(la, blockIdx.x - rec_blocks, gridDim.x - rec_blocks);
-}
-
-// The adjoint of window j (blocks [0, adj_blocks), writing G buffer j % 2) with the weight
-// gradients of window j - 1 (the rest: the recurrent dW pass, then the LGN dW, reading G
-// buffer (j - 1) % 2): the adjoint streams state through HBM while the dW passes are chains
+// The adjoint of window j (blocks [0, adj_blocks) after the walk's, writing G buffer j % 2)
+// with the weight gradients of window j - 1 (the rest: the recurrent dW pass, then the LGN
+// dW, reading G buffer (j - 1) % 2): the adjoint streams state through HBM while the dW passes are chains
 // of dependent loads, and one launch keeps the dW work out of window j's dz walk.
+// With a split dz walk, also the second part of window j - 1's walk (the columns of delays
+// above what window j's adjoint reads, blocks [0, walk_blocks), first since they run longest):
+// the adjoint of tick t reads dz of tick t + d at delay d only, so window j's adjoint needs
+// window j - 1's dz of delays <= 2 W - 3, and the rest of that walk can share its launch.
 struct DwPrev {
     RecDwArgs da;
     ActWin act;
     BwdInArgs la;
     int32_t rec_blocks, lgn_blocks;
+    GsArgs gb;          // the walk's remaining groups (window j - 1)
+    int32_t walk_blocks;
 };
 
 template <int NB>
 __global__ void __launch_bounds__(kBlock) k_adj_dw(AdjArgs a, int adj_blocks, DwPrev p) {
-    const int64_t bid = blockIdx.x;
+    int64_t bid = blockIdx.x;
+    if (bid < p.walk_blocks) {
+        extern __shared__ float lds_f[];  // kBlock / kWave * kGsStage floats of the launch's LDS
+        bwd_groups<4>(p.gb, p.act, lds_f, bid);
+        return;
+    }
+    bid -= p.walk_blocks;
     if (bid < adj_blocks) {
         adj_body<NB>(a, bid);
     } else if (bid < adj_blocks + p.rec_blocks) {
@@ -1069,9 +1071,9 @@ __global__ void __launch_bounds__(kBlock) k_adj_dw(AdjArgs a, int adj_blocks, Dw
 static void launch_bwd_in(const BwdInArgs &ia, int64_t max_units, hipStream_t s) {
     const dim3 grid(grid_subwaves(max_units, kWave));
     if (ia.cnt)
-        hipLaunchKernelGGL(k_bwd_in<true>, grid, dim3(kBlock), 0, s, ia);
+        GLIF_PROF_LAUNCH(k_bwd_in<true>, grid, dim3(kBlock), 0, s, ia);
     else
-        hipLaunchKernelGGL(k_bwd_in<false>, grid, dim3(kBlock), 0, s, ia);
+        GLIF_PROF_LAUNCH(k_bwd_in<false>, grid, dim3(kBlock), 0, s, ia);
 }
 
 static void launch_step_push(const StepArgs &sa, int step_blocks, const PushArgs &pa, int push_blocks, int nb,
@@ -1079,7 +1081,7 @@ static void launch_step_push(const StepArgs &sa, int step_blocks, const PushArgs
     const dim3 grid(step_blocks + push_blocks);
     switch (nb) {
 #define GLIF_STEP_PUSH(NB) \
-    case NB: hipLaunchKernelGGL((k_step_push<NB>), grid, dim3(kBlock), lds, s, sa, step_blocks, pa); break;
+    case NB: GLIF_PROF_LAUNCH((k_step_push<NB>), grid, dim3(kBlock), lds, s, sa, step_blocks, pa); break;
         GLIF_STEP_PUSH(1) GLIF_STEP_PUSH(2) GLIF_STEP_PUSH(3) GLIF_STEP_PUSH(4) GLIF_STEP_PUSH(5)
         GLIF_STEP_PUSH(6) GLIF_STEP_PUSH(7) GLIF_STEP_PUSH(8)
 #undef GLIF_STEP_PUSH
@@ -1091,7 +1093,7 @@ template <bool DET>
 static void launch_step(const StepArgs &sa, int nb, dim3 grid, size_t lds, hipStream_t s) {
     switch (nb) {
 #define GLIF_STEP(NB) \
-    case NB: hipLaunchKernelGGL((k_step<DET, NB>), grid, dim3(kBlock), lds, s, sa); break;
+    case NB: GLIF_PROF_LAUNCH((k_step<DET, NB>), grid, dim3(kBlock), lds, s, sa); break;
         GLIF_STEP(1) GLIF_STEP(2) GLIF_STEP(3) GLIF_STEP(4) GLIF_STEP(5) GLIF_STEP(6) GLIF_STEP(7) GLIF_STEP(8)
 #undef GLIF_STEP
         default: break;
@@ -1115,17 +1117,20 @@ static size_t adj_stage_lds(const CellConst &k, int R, int tc) {
     return sizeof(float) * (static_cast<size_t>(k.n_types) * k.nb + static_cast<size_t>(tc) * nr * R);
 }
 
-// prev: the weight-gradient passes of the previous window to run in the same launch, or null
-static void launch_adj(const AdjArgs &aa, int nb, hipStream_t s, const DwPrev *prev = nullptr) {
+// prev: the weight-gradient passes (and the rest of the dz walk) of the previous window to run
+// in the same launch, or null; with_adj false: those alone (after the last window)
+static void launch_adj(const AdjArgs &aa, int nb, hipStream_t s, const DwPrev *prev = nullptr,
+                       bool with_adj = true) {
     const CellConst &k = aa.k;
-    const size_t use = adj_stage_lds(k, aa.R, aa.tc);
-    const int adj_blocks = ceil_div(k.N, kBlock / k.B);
-    const dim3 grid(adj_blocks + (prev ? prev->rec_blocks + prev->lgn_blocks : 0));
+    size_t use = with_adj ? adj_stage_lds(k, aa.R, aa.tc) : 0;
+    if (prev && prev->walk_blocks) use = std::max(use, sizeof(float) * (kBlock / kWave) * kGsStage);
+    const int adj_blocks = with_adj ? ceil_div(k.N, kBlock / k.B) : 0;
+    const dim3 grid(adj_blocks + (prev ? prev->walk_blocks + prev->rec_blocks + prev->lgn_blocks : 0));
     switch (nb) {
 #define GLIF_ADJ(NB)                                                                                   \
     case NB:                                                                                           \
-        if (prev) hipLaunchKernelGGL((k_adj_dw<NB>), grid, dim3(kBlock), use, s, aa, adj_blocks, *prev); \
-        else hipLaunchKernelGGL((k_adj<NB>), grid, dim3(kBlock), use, s, aa);                           \
+        if (prev) GLIF_PROF_LAUNCH((k_adj_dw<NB>), grid, dim3(kBlock), use, s, aa, adj_blocks, *prev); \
+        else GLIF_PROF_LAUNCH((k_adj<NB>), grid, dim3(kBlock), use, s, aa);                           \
         break;
         GLIF_ADJ(1) GLIF_ADJ(2) GLIF_ADJ(3) GLIF_ADJ(4) GLIF_ADJ(5) GLIF_ADJ(6) GLIF_ADJ(7) GLIF_ADJ(8)
 #undef GLIF_ADJ
@@ -1478,8 +1483,8 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
             early.I = Ih[t & 1];
             if (t == 0) {
                 // tick 0: every delay slot (the initial history) and the LGN inputs
-                ProfScope p(kProfPush, s);
-                hipLaunchKernelGGL(k_push, dim3(push_grid), dim3(kBlock), lds, s, early);
+                ProfScope p(kProfPush, s, true);
+                GLIF_PROF_LAUNCH(k_push, dim3(push_grid), dim3(kBlock), lds, s, early);
             } else {
                 early.d_lo = 2;   // d_hi = D; nothing recurrent when D = 1
                 StepArgs x = step_args(t - 1);
@@ -1487,20 +1492,20 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                 x.p1_colptr = tr->col_ptr;
                 x.p1_ps = typed ? tr->cg.ps : tr->ps;
                 x.p1_w = tr->w_col;
-                ProfScope p(kProfStep, s);
+                ProfScope p(kProfStep, s, true);
                 launch_step_push(x, static_cast<int>(step_grid.x), early, fused_push_grid, c->nb, lds, s);
             }
             if (t == T - 1) {
-                ProfScope p(kProfStep, s);
+                ProfScope p(kProfStep, s, true);
                 launch_step<false>(step_args(t), c->nb, step_grid, lds, s);
             }
         } else {
             pl.t = t;
             {
-                ProfScope p(kProfPush, s);
+                ProfScope p(kProfPush, s, true);
                 launch_pull(pl, lds, s);
             }
-            ProfScope p(kProfStep, s);
+            ProfScope p(kProfStep, s, true);
             launch_step<true>(sa, c->nb, step_grid, lds, s);
         }
     }
@@ -1613,10 +1618,20 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
 
     // With the grouped walk, the weight-gradient passes of window j (recurrent, then LGN)
     // run in window j + 1's adjoint launch (k_adj_dw); windows alternate between two G
-    // buffers so that launch reads one while the adjoint writes the other.
+    // buffers so that launch reads one while the adjoint writes the other.  The dz walk of
+    // window j covers the columns of delays <= 2 W - 3 (the ones window j + 1's adjoint reads,
+    // groups [0, g_split)) before that launch and the rest inside it.
     const bool defer = gs && dw_rec;
     DwPrev prev{};
     bool have_prev = false;
+    const int64_t n_groups = (tr->n_cols + kGsCols - 1) / kGsCols;
+    int64_t g_split = n_groups;
+    if (defer) {
+        const int64_t d_need = std::max(0, 2 * Wwin - 3);
+        constexpr int64_t wave_groups = kWave / 4;  // g_lo of a range: whole waves of groups
+        const int64_t g = (d_need * c->N + kGsCols - 1) / kGsCols;
+        g_split = std::min(n_groups, (g + wave_groups - 1) / wave_groups * wave_groups);
+    }
     int j = 0;
     for (int t0 = T - 1; t0 >= 2; t0 -= Wwin, ++j) {
         const int nw = std::min(Wwin, t0 - 1);
@@ -1627,7 +1642,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         aa.t0 = t0;
         aa.nw = nw;
         {
-            ProfScope p(kProfAdj, s);
+            ProfScope p(kProfAdj, s, true);
             launch_adj(aa, c->nb, s, have_prev ? &prev : nullptr);
         }
         ca.n_elem = ga.n_elem = da.n_elem = nw * B;
@@ -1635,11 +1650,15 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         la.j = j;
         la.s0 = s0;
         {
-            ProfScope p(kProfBwdRec, s);
-            if (gs)
-                hipLaunchKernelGGL(k_bwd_rec_gs, dim3(ceil_div(ga.n_groups * 4, kBlock)), dim3(kBlock), 0, s, ga, act);
-            else
+            ProfScope p(kProfBwdRec, s, true);
+            if (gs) {
+                GsArgs g1 = ga;
+                g1.g_hi = g_split;
+                if (g_split > 0)
+                    GLIF_PROF_LAUNCH(k_bwd_rec_gs, dim3(ceil_div(g_split * 4, kBlock)), dim3(kBlock), 0, s, g1, act);
+            } else {
                 launch_bwd_rec(ca, Rg, act, s);
+            }
         }
         if (defer) {
             prev.da = da;
@@ -1647,25 +1666,24 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
             prev.la = la;
             prev.rec_blocks = ceil_div(tr->n_cols, kBlock);
             prev.lgn_blocks = dw_lgn ? grid_subwaves(lgn_units, kWave) : 0;
+            prev.gb = ga;
+            prev.gb.g_lo = g_split;
+            prev.walk_blocks = g_split < n_groups ? ceil_div((n_groups - g_split) * 4, kBlock) : 0;
             have_prev = true;
         } else if (dw_lgn) {
-            ProfScope p(kProfBwdLgn, s);
+            ProfScope p(kProfBwdLgn, s, true);
             launch_bwd_in(la, lgn_units, s);
         }
         if (dw_bkg) {
             ka.j = j;
             ka.s0 = s0;
-            ProfScope p(kProfBwdBkg, s);
+            ProfScope p(kProfBwdBkg, s, true);
             launch_bwd_in(ka, bkg_units, s);
         }
     }
-    if (have_prev) {  // the last window's weight gradients
-        ProfScope p(kProfAdj, s);
-        if (prev.lgn_blocks)
-            hipLaunchKernelGGL(k_bwd_dw_rec_lgn, dim3(prev.rec_blocks + prev.lgn_blocks), dim3(kBlock), 0, s, prev.da,
-                               prev.act, prev.la, prev.rec_blocks);
-        else
-            hipLaunchKernelGGL(k_bwd_rec_dw, dim3(prev.rec_blocks), dim3(kBlock), 0, s, prev.da, prev.act);
+    if (have_prev) {  // the last window's weight gradients and the rest of its dz walk
+        ProfScope p(kProfAdj, s, true);
+        launch_adj(aa, c->nb, s, &prev, false);
     }
     GLIF_HIP(hipGetLastError());
     if (dw_rec && (rc = launch_gather_f32(dw_rec, w.dw_rec, gs ? tr->order_inv : tr->ph_inv, tr->n_syn, s))) return rc;

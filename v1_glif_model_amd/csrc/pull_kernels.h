@@ -7,6 +7,7 @@
 #include <algorithm>
 
 #include "glif_internal.h"
+#include "prof.h"
 #include "syn_kernels.h"
 
 namespace glif {
@@ -405,9 +406,9 @@ static const void *chunk_kernel(int G) {
 template <int BLOCK>
 static void launch_chunks(int G, dim3 grid, size_t lb, hipStream_t s, const PullArgs &pa) {
     switch (G) {
-        case 1: hipLaunchKernelGGL((k_pull_chunks<1, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
-        case 2: hipLaunchKernelGGL((k_pull_chunks<2, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
-        default: hipLaunchKernelGGL((k_pull_chunks<4, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
+        case 1: GLIF_PROF_LAUNCH((k_pull_chunks<1, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
+        case 2: GLIF_PROF_LAUNCH((k_pull_chunks<2, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
+        default: GLIF_PROF_LAUNCH((k_pull_chunks<4, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
     }
 }
 
@@ -448,10 +449,10 @@ static void launch_pull(const PullArgs &pa, size_t lds, hipStream_t s) {
     const int G = (pa.B * pa.nb + 31) / 32;
     const dim3 grid(ceil_div(static_cast<int64_t>(pa.N) * 32, kBlock));
     switch (G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8) {
-        case 1: hipLaunchKernelGGL(k_pull<1>, grid, dim3(kBlock), lds, s, pa); break;
-        case 2: hipLaunchKernelGGL(k_pull<2>, grid, dim3(kBlock), lds, s, pa); break;
-        case 4: hipLaunchKernelGGL(k_pull<4>, grid, dim3(kBlock), lds, s, pa); break;
-        default: hipLaunchKernelGGL(k_pull<8>, grid, dim3(kBlock), lds, s, pa); break;
+        case 1: GLIF_PROF_LAUNCH(k_pull<1>, grid, dim3(kBlock), lds, s, pa); break;
+        case 2: GLIF_PROF_LAUNCH(k_pull<2>, grid, dim3(kBlock), lds, s, pa); break;
+        case 4: GLIF_PROF_LAUNCH(k_pull<4>, grid, dim3(kBlock), lds, s, pa); break;
+        default: GLIF_PROF_LAUNCH(k_pull<8>, grid, dim3(kBlock), lds, s, pa); break;
     }
 }
 

@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(kBlock) k_syn_bwd_cols(ColArgs a, ActDense act
 template <int LG>
 __global__ void __launch_bounds__(kBlock) k_syn_bwd_gs(GsArgs a, ActDense act) {
     __shared__ float stage[kBlock / kWave * kGsStage];
-    bwd_groups<LG>(a, act, stage);
+    bwd_groups<LG>(a, act, stage, blockIdx.x);
 }
 
 // dW of the active columns (z[b][c] > 0) next to the grouped dz walk: a wave per 64

@@ -334,6 +334,9 @@ struct GsArgs {
     const int32_t *seg;   // [n_groups * (kGsSlices + 1)]
     const uint2 *pw;      // {row | column-in-group << kGsRowBits, weight bits}
     const float *G;       // [rows][4 LG], < 4 GiB
+    // the groups walked: [g_lo, g_hi), g_hi = 0 for every group from g_lo; g_lo a multiple of
+    // the groups of a wave (kWave / LG)
+    int64_t g_lo = 0, g_hi = 0;
 };
 
 // value of lane `src` of this lane's quad (DPP quad_perm broadcast)
@@ -365,12 +368,12 @@ constexpr int kGsStage = 16 * (16 * kGsCols + 1) > 8 * (32 * kGsCols + 1) ? 16 *
 // of 8 entries is 8 / LG entries per lane (one or two 16-byte loads).  stage: kGsStage floats
 // of LDS per wave of the block.
 template <int LG, class Act>
-__device__ inline void bwd_groups(const GsArgs &a, const Act &act, float *stage) {
+__device__ inline void bwd_groups(const GsArgs &a, const Act &act, float *stage, int64_t bid) {
     constexpr int R = 4 * LG, EPL = 8 / LG, CW = (kWave / LG) * kGsCols;
     const int q = threadIdx.x % LG;
-    const int64_t g = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / LG;
+    const int64_t g = a.g_lo + (bid * blockDim.x + threadIdx.x) / LG;
     // a group past the end walks nothing but still takes part in the staging below
-    const bool own = g < a.n_groups;
+    const bool own = g < (a.g_hi ? a.g_hi : a.n_groups);
     const char *Gb = reinterpret_cast<const char *>(a.G) + static_cast<uint32_t>(q) * 16u;
     float acc[kGsCols][4];
 #pragma unroll
@@ -425,10 +428,11 @@ __device__ inline void bwd_groups(const GsArgs &a, const Act &act, float *stage)
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int64_t cw0 = (g - gl) * kGsCols;
+    const int64_t c_end = a.g_hi ? min(a.n_cols, a.g_hi * kGsCols) : a.n_cols;
 #pragma unroll
     for (int cc = lane; cc < CW; cc += kWave) {
         const int64_t c = cw0 + cc;
-        if (c < a.n_cols) {
+        if (c < c_end) {
             const typename Act::Col ci = act.col(c);
             for (int e = 0; e < a.n_elem; ++e) *act.out(ci, e) = st[e * (CW + 1) + cc];
         }
