@@ -399,8 +399,8 @@ def main():
     timings = []
 
     def step():
-        for s, z0 in zip(state, zero):
-            s.copy_(z0)
+        for s in state:      # every batch starts from the zero state
+            s.zero_()
         spike_count.zero_()
         cell.refresh_weights(force=True)
         fwd_ev[0].record()
