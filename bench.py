@@ -426,7 +426,9 @@ def main():
     # one more, untimed step with every kernel class timed: the breakdown, and the dominant
     # class (most time per step), whose launches the timed steps bracket with HIP events.
     # Event mode's forward is one fused launch per tick (the step of t - 1 beside the pushes,
-    # "step"); deterministic mode's row pull is "push"; "adj" is the adjoint launch with the
+    # "step"), and so is deterministic mode's (the row pull of t beside the step of t, whose R
+    # takes the currents of t - 1; "step"; where the pull and the step run as two launches the
+    # row pull is "push"); "adj" is the adjoint launch with the
     # previous window's weight gradients and the rest of its dz walk; "bwd_rec" the dz walk
     # over the columns the next adjoint reads.
     _lib.prof_enable(list(_lib.PROF_KINDS))
@@ -511,6 +513,18 @@ def main():
                      + N * rows * Rg * 4 + act_ev * 16
                      + (S - s_a) * 8 + (n_cols - cols_a + 1) * 4 + Wwin * B * (n_cols - cols_a) * 4)
         unit_desc = f"bytes per backward window of {Wwin} timesteps (adjoint + previous window's dW and dz rest)"
+    elif dominant == "step" and args.mode == "deterministic":
+        # per launch = one tick: the row pull (every recurrent and LGN entry's bitmap index,
+        # 4 bytes; the row pointers; each active entry's batch mask, weight and type, 9 bytes;
+        # the rec and LGN currents written) beside the GLIF_3 step's state stream per (b, n)
+        # -- reads the previous tick's pulled I and I2, R, P (nb floats each), A (2 floats),
+        # v, r (int16); writes R, P, A, v, r and the saved voltage -- the per-neuron constants
+        # (7 floats) and the background rows (8 bytes per synapse)
+        active = (e_rec + e_lgn) / max(T, 1)
+        per_bn = (4 * nb * 4 + 14) + (2 * nb * 4 + 18)
+        alg_bytes = ((S + tb.lgn.n_syn) * 4 + 2 * (N + 1) * 4 + active * 9 + 2 * nb * B * N * 4
+                     + B * N * per_bn + N * 28 + tb.bkg.n_syn * 8)
+        unit_desc = "bytes per forward timestep (deterministic row pull beside the GLIF_3 step)"
     elif dominant == "step":
         # per launch = one tick: the GLIF_3 step's state stream per (b, n) -- reads I, R, P
         # (nb floats each), A (2 floats), v, r (int16); writes I (cleared), R, P, A, v, r and
@@ -529,7 +543,8 @@ def main():
         unit_desc = "bytes per forward timestep (deterministic row pull)"
     avg_ms = tot_ms / max(launches, 1)
     achieved = alg_bytes / (avg_ms / 1000.0) / 1e9 if avg_ms > 0 else 0.0
-    traffic = load_traffic(dominant)
+    # measured traffic per kernel class (deterministic mode's fused launch has its own)
+    traffic = load_traffic("pull_step" if (dominant == "step" and args.mode == "deterministic") else dominant)
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic.get("bytes_per_launch") if traffic else None,

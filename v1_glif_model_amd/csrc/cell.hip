@@ -8,8 +8,10 @@
 //                 k_step(t)   background pull, GLIF_3 update, spike bits (wave
 //                             ballots); I is re-zeroed after reading.
 //   deterministic: the row pull (pull_kernels.h) sums rec and LGN per post row in
-//                 the reference's accumulation order, then k_step(t) adds the
-//                 background and does the same update.
+//                 the reference's accumulation order and k_step adds the background
+//                 and does the same update; with the resident chunk pull both run in
+//                 one launch per tick (k_pull_step: the pull of t beside the step of
+//                 t, whose R takes the currents of t - 1).
 // Backward, in windows of Wwin reverse ticks t0, t0-1, .. (lagged adjoint, k_adj):
 //   k_adj         per tick t: gz_t -> gV_t -> gP_{t-1} -> gR_{t-2} -> G_{t-2}
 //   k_bwd_rec_gs  dz of the window's steps t0-2, t0-3, .. over the recurrent columns
@@ -45,7 +47,7 @@ struct CellWs {
     uint32_t *lmask;    // [T][n_lgn]        bit b: LGN input x_t[b][pre] > 0
     uint64_t *abits;    // [(T + D)][W]      bit n: z_t[b][n] for some b (slot t + D)
     uint64_t *lbits;    // [T][Wl]           bit pre: x_t[b][pre] > 0 for some b
-    float *I2;          // [nb][B][N]   LGN currents (deterministic chunk pull)
+    float *I2;          // [2][nb][B][N]   LGN currents (deterministic chunk pull)
     float *vsave;       // [T][B][N]
     int64_t *lgn_off;   // [T + 1]           per-step LGN (column, batch-mask) lists
     int32_t *lgn_pre;   // [T * n_lgn]
@@ -92,7 +94,7 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.lmask = cv.take<uint32_t>(static_cast<size_t>(T) * nl);
     w.abits = cv.take<uint64_t>(static_cast<size_t>(T + c->D) * c->W);
     w.lbits = cv.take<uint64_t>(static_cast<size_t>(T) * ((nl + 63) / 64));
-    w.I2 = cv.take<float>(BN * c->nb);
+    w.I2 = cv.take<float>(2 * BN * c->nb);  // deterministic pull beside the step: two halves
     w.vsave = cv.take<float>(static_cast<size_t>(T) * BN);
     w.lgn_off = cv.take<int64_t>(T + 1);
     w.lgn_pre = cv.take<int32_t>(static_cast<size_t>(T) * nl);
@@ -361,7 +363,101 @@ struct StepArgs {
     // receptor r's current is sum_q I[q] * basis[gtype[n][q]][r], ascending q.  0: [nb][B][N]
     int32_t gk;
     const uint8_t *gtype;
+    // deterministic pull beside the step (lag = 1): R takes tick t - 1's currents (I, I2
+    // and bkg_x point at that tick; none at t = 0), P the R of tick t - 1 so updated
+    int32_t lag;
 };
+
+// The input of R for (b, n) at one tick, (I_rec + I_lgn) + I_bkg, times lr_scale
+// (models.py:896-931, 979-990): the pushed (event, [nb][B][N] or per-type slots, cleared
+// after reading) or pulled (deterministic) rec + LGN currents, plus the background, every
+// synapse of the row times its Poisson count.
+template <bool DET, int NB>
+__device__ inline void step_inputs(const StepArgs &a, const float *basis_lds, int n, int b, int64_t bn,
+                                   float (&in)[kMaxBasis]) {
+    const CellConst &k = a.k;
+    constexpr int nb = NB;
+    const int64_t BN = static_cast<int64_t>(k.B) * k.N;
+    float Irl[kMaxBasis], Ib[kMaxBasis];
+    for (int q = 0; q < nb; ++q) Ib[q] = 0.0f;
+    if (!DET && a.gk) {
+        // the pushed rec + LGN type sums, folded through the basis (a slot past the
+        // post's types holds +0 and is skipped)
+        for (int q = 0; q < nb; ++q) Irl[q] = 0.0f;
+        const uint8_t *gt = a.gtype + static_cast<int64_t>(n) * a.gk;
+        for (int j = 0; j < a.gk; ++j) {
+            float *Ip = a.I + j * BN + bn;
+            const float x = *Ip;
+            *Ip = 0.0f;
+            const int sj = gt[j];
+            if (sj == 0xFF) continue;
+            const float *bs = basis_lds + sj * nb;
+#pragma unroll
+            for (int q = 0; q < nb; ++q) Irl[q] = Irl[q] + x * bs[q];
+        }
+    } else {
+        // the pushed (event) or pulled (deterministic) rec + LGN currents
+        for (int q = 0; q < nb; ++q) {
+            float *Ip = a.I + q * BN + bn;
+            Irl[q] = *Ip;
+            if (DET && a.I2) Irl[q] = Irl[q] + a.I2[q * BN + bn];
+            if (!DET) *Ip = 0.0f;
+        }
+    }
+    // background: every synapse of the row, weight times the Poisson count.  A zero
+    // count adds +/-0, which leaves a sum started at +0 unchanged, so the
+    // branch-free loop equals the reference's event-only sum bit for bit.
+    const uint8_t *xb = a.bkg_x + static_cast<int64_t>(b) * a.n_bkg;
+    if (a.bkg_ell) {
+        // ELL rows: entry j of every post in one coalesced 8-byte load; the padding
+        // ({pre 0, w +0}) adds +0, which leaves the sum unchanged
+        for (int32_t jb = 0; jb < a.bkg_ell_len; jb += 8) {
+            uint2 e[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                e[u] = jb + u < a.bkg_ell_len ? a.bkg_ell[static_cast<int64_t>(jb + u) * k.N + n] : make_uint2(0u, 0u);
+            float cnt[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cnt[u] = static_cast<float>(xb[e[u].x & kLow24]);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (jb + u >= a.bkg_ell_len) break;
+                const float wv = __uint_as_float(e[u].y) * cnt[u];
+                const float *bs = basis_lds + (e[u].x >> 24) * nb;
+#pragma unroll
+                for (int r = 0; r < nb; ++r) Ib[r] = Ib[r] + wv * bs[r];
+            }
+        }
+    } else {
+        // 8 synapses at a time: their table entries, then their counts, are loaded
+        // together before the (in-order) accumulation
+        const int32_t j0 = a.bkg_row[n], j1 = a.bkg_row[n + 1];
+        for (int32_t jb = j0; jb < j1; jb += 8) {
+            uint32_t pd[8];
+            float wj[8];
+            int sj[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const bool ok = jb + u < j1;
+                pd[u] = ok ? a.bkg_pd[jb + u] : 0u;
+                wj[u] = ok ? a.bkg_w[jb + u] : 0.0f;
+                sj[u] = ok ? a.bkg_sid[jb + u] : 0;
+            }
+            float cnt[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cnt[u] = (jb + u < j1) ? static_cast<float>(xb[pd[u] & kLow24]) : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (jb + u >= j1) break;
+                const float wv = wj[u] * cnt[u];
+                const float *bs = basis_lds + sj[u] * nb;
+#pragma unroll
+                for (int r = 0; r < nb; ++r) Ib[r] = Ib[r] + wv * bs[r];
+            }
+        }
+    }
+    for (int q = 0; q < nb; ++q) in[q] = (Irl[q] + Ib[q]) * k.lr;
+}
 
 // One GLIF_3 update per thread (b, n), models.py:979-1028 and 1059-1135:
 //   I      = ((I_rec + I_lgn) + I_bkg) * lr_scale
@@ -370,6 +466,8 @@ struct StepArgs {
 //   V'     = (decay * (V * (1 - vgd) + V * vgd) + cf * c) - z_prev
 //   r'     = max(r + z_prev * tref - 1, 0); hard reset: V' = 0 while r' > 0
 //   z      = r' > 0 ? 0 : (V' - 1 > 0)
+// V', r' and z take the old P and A only, so tick t's currents can arrive one launch late
+// (a.lag): R is then brought to tick t - 1 here and P' takes that R.
 template <bool DET, int NB>
 __device__ inline void step_body(const StepArgs &a, int64_t bid) {
     extern __shared__ float basis_lds[];
@@ -389,85 +487,9 @@ __device__ inline void step_body(const StepArgs &a, int64_t bid) {
     if (n < k.N) {
         const int64_t BN = static_cast<int64_t>(k.B) * k.N;
         const int64_t bn = static_cast<int64_t>(b) * k.N + n;
-        float Irl[kMaxBasis], Ib[kMaxBasis];
-        for (int q = 0; q < nb; ++q) Ib[q] = 0.0f;
-        if (!DET && a.gk) {
-            // the pushed rec + LGN type sums, folded through the basis (a slot past the
-            // post's types holds +0 and is skipped)
-            for (int q = 0; q < nb; ++q) Irl[q] = 0.0f;
-            const uint8_t *gt = a.gtype + static_cast<int64_t>(n) * a.gk;
-            for (int j = 0; j < a.gk; ++j) {
-                float *Ip = a.I + j * BN + bn;
-                const float x = *Ip;
-                *Ip = 0.0f;
-                const int sj = gt[j];
-                if (sj == 0xFF) continue;
-                const float *bs = basis_lds + sj * nb;
-#pragma unroll
-                for (int q = 0; q < nb; ++q) Irl[q] = Irl[q] + x * bs[q];
-            }
-        } else {
-            // the pushed (event) or pulled (deterministic) rec + LGN currents
-            for (int q = 0; q < nb; ++q) {
-                float *Ip = a.I + q * BN + bn;
-                Irl[q] = *Ip;
-                if (DET && a.I2) Irl[q] = Irl[q] + a.I2[q * BN + bn];
-                if (!DET) *Ip = 0.0f;
-            }
-        }
-        // background: every synapse of the row, weight times the Poisson count.  A zero
-        // count adds +/-0, which leaves a sum started at +0 unchanged, so the
-        // branch-free loop equals the reference's event-only sum bit for bit.
-        const uint8_t *xb = a.bkg_x + static_cast<int64_t>(b) * a.n_bkg;
-        if (a.bkg_ell) {
-            // ELL rows: entry j of every post in one coalesced 8-byte load; the padding
-            // ({pre 0, w +0}) adds +0, which leaves the sum unchanged
-            for (int32_t jb = 0; jb < a.bkg_ell_len; jb += 8) {
-                uint2 e[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    e[u] = jb + u < a.bkg_ell_len ? a.bkg_ell[static_cast<int64_t>(jb + u) * k.N + n] : make_uint2(0u, 0u);
-                float cnt[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) cnt[u] = static_cast<float>(xb[e[u].x & kLow24]);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    if (jb + u >= a.bkg_ell_len) break;
-                    const float wv = __uint_as_float(e[u].y) * cnt[u];
-                    const float *bs = basis_lds + (e[u].x >> 24) * nb;
-#pragma unroll
-                    for (int r = 0; r < nb; ++r) Ib[r] = Ib[r] + wv * bs[r];
-                }
-            }
-        } else {
-            // 8 synapses at a time: their table entries, then their counts, are loaded
-            // together before the (in-order) accumulation
-            const int32_t j0 = a.bkg_row[n], j1 = a.bkg_row[n + 1];
-            for (int32_t jb = j0; jb < j1; jb += 8) {
-                uint32_t pd[8];
-                float wj[8];
-                int sj[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const bool ok = jb + u < j1;
-                    pd[u] = ok ? a.bkg_pd[jb + u] : 0u;
-                    wj[u] = ok ? a.bkg_w[jb + u] : 0.0f;
-                    sj[u] = ok ? a.bkg_sid[jb + u] : 0;
-                }
-                float cnt[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) cnt[u] = (jb + u < j1) ? static_cast<float>(xb[pd[u] & kLow24]) : 0.0f;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    if (jb + u >= j1) break;
-                    const float wv = wj[u] * cnt[u];
-                    const float *bs = basis_lds + sj[u] * nb;
-#pragma unroll
-                    for (int r = 0; r < nb; ++r) Ib[r] = Ib[r] + wv * bs[r];
-                }
-            }
-        }
-
+        const bool upd = !a.lag || t > 0;  // with the lag, R of tick -1 is the state
+        float in[kMaxBasis];
+        if (upd) step_inputs<DET, NB>(a, basis_lds, n, b, bn, in);
         const float zp = zbit(a.zbits, t - 1 + k.D, b, k.B, k.W, n) ? 1.0f : 0.0f;
         float Pold[kMaxBasis];
         for (int q = 0; q < nb; ++q) Pold[q] = a.P[q * BN + bn];
@@ -476,11 +498,11 @@ __device__ inline void step_body(const StepArgs &a, int64_t bid) {
         const float A0 = a.A[bn], A1 = a.A[BN + bn];
         const float c1 = sumP + (A0 + A1);
         for (int q = 0; q < nb; ++q) {
-            const float in = (Irl[q] + Ib[q]) * k.lr;
             float *Rq = a.R + q * BN + bn;
             const float Rold = *Rq;
-            *Rq = Rold * k.sd[q] + in * k.p0[q];
-            a.P[q * BN + bn] = Pold[q] * k.sd[q] + k.dtsd[q] * Rold;
+            const float Rnew = upd ? Rold * k.sd[q] + in[q] * k.p0[q] : Rold;
+            if (upd) *Rq = Rnew;
+            a.P[q * BN + bn] = Pold[q] * k.sd[q] + k.dtsd[q] * (a.lag ? Rnew : Rold);
         }
         a.A[bn] = a.ad[2 * n] * A0 + zp * a.amp[2 * n];
         a.A[BN + bn] = a.ad[2 * n + 1] * A1 + zp * a.amp[2 * n + 1];
@@ -531,6 +553,36 @@ __device__ inline void step_body(const StepArgs &a, int64_t bid) {
 template <bool DET, int NB>
 __global__ void __launch_bounds__(kBlock) k_step(StepArgs a) {
     step_body<DET, NB>(a, blockIdx.x);
+}
+
+// Deterministic mode: the row pull of tick t (the first pull_blocks workgroups, resident,
+// into one half of the double-buffered currents) beside the step of tick t with R one tick
+// late (the other workgroups, reading the other half).  The pull streams the tables and is
+// bound by its chains of dependent loads and ordered adds, the step streams the state, and
+// one launch overlaps them.
+template <int NB>
+__global__ void __launch_bounds__(kPullBlock) k_pull_step(PullArgs pa, int pull_blocks, StepArgs sa) {
+    if (static_cast<int>(blockIdx.x) < pull_blocks) pull_chunks_body<1>(pa, blockIdx.x, pull_blocks);
+    else step_body<true, NB>(sa, blockIdx.x - pull_blocks);
+}
+
+// After the lagged loop: R of the last tick from its currents and background.
+template <int NB>
+__global__ void __launch_bounds__(kBlock) k_r_last(StepArgs a) {
+    extern __shared__ float basis_lds[];
+    const CellConst &k = a.k;
+    load_basis_lds(basis_lds, a.basis, k.n_types * k.nb);
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gt >= static_cast<int64_t>(k.B) * k.Np) return;
+    const int b = static_cast<int>(gt / k.Np), n = static_cast<int>(gt % k.Np);
+    if (n >= k.N) return;
+    const int64_t BN = static_cast<int64_t>(k.B) * k.N, bn = static_cast<int64_t>(b) * k.N + n;
+    float in[kMaxBasis];
+    step_inputs<true, NB>(a, basis_lds, n, b, bn, in);
+    for (int q = 0; q < NB; ++q) {
+        float *Rq = a.R + q * BN + bn;
+        *Rq = *Rq * k.sd[q] + in[q] * k.p0[q];
+    }
 }
 
 // Event mode: the push of tick t's events that do not depend on the step of tick t - 1
@@ -1089,6 +1141,71 @@ static void launch_step_push(const StepArgs &sa, int step_blocks, const PushArgs
     }
 }
 
+// Pull workgroups of the fused deterministic launch: all the workgroups that stay resident
+// but a quarter of one per CU, so that the step's workgroups start beside the pull's (the
+// pull walks a fixed share of the chunks per workgroup and its workgroups come first);
+// config 2, 3 resident per CU: 2.75 per CU gave 56.3 us per tick, 2: 58.7, 2.5: 57.4, 3
+// (the step behind the pull): 57.4, 1.5: 72.3, the step's workgroups first: 64.4.  0 when
+// the pull is not the resident chunk form or only one workgroup fits a CU (then pull and
+// step run as two launches).
+static const void *pull_step_kernel(int nb) {
+    switch (nb) {
+        case 1: return reinterpret_cast<const void *>(&k_pull_step<1>);
+        case 2: return reinterpret_cast<const void *>(&k_pull_step<2>);
+        case 3: return reinterpret_cast<const void *>(&k_pull_step<3>);
+        case 4: return reinterpret_cast<const void *>(&k_pull_step<4>);
+        case 5: return reinterpret_cast<const void *>(&k_pull_step<5>);
+        case 6: return reinterpret_cast<const void *>(&k_pull_step<6>);
+        case 7: return reinterpret_cast<const void *>(&k_pull_step<7>);
+        default: return reinterpret_cast<const void *>(&k_pull_step<8>);
+    }
+}
+
+static int fused_pull_blocks(const PullArgs &pl, int nb) {
+    if (!pull_chunked(pl) || nb < 1 || nb > kMaxBasis) return 0;
+    const DevShape &ds = dev_shape();
+    const size_t lb = chunk_lds_bytes(pl);
+    if (ds.lds_per_cu / lb < 2) return 0;
+    static int cache_pc[64][kMaxBasis + 1];
+    static size_t cache_lb[64][kMaxBasis + 1];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int per_cu = cache_pc[dev][nb];
+    if (per_cu < 1 || cache_lb[dev][nb] != lb) {
+        const void *fn = pull_step_kernel(nb);
+        if (lb > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lb));
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPullBlock, lb) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        cache_pc[dev][nb] = per_cu;
+        cache_lb[dev][nb] = lb;
+    }
+    return per_cu < 2 ? 0 : ds.n_cu * per_cu - ds.n_cu / 4;
+}
+
+static void launch_pull_step(const PullArgs &pa, int pull_blocks, const StepArgs &sa, int step_blocks, int nb,
+                             size_t lds, hipStream_t s) {
+    const dim3 grid(pull_blocks + step_blocks);
+    switch (nb) {
+#define GLIF_PULL_STEP(NB) \
+    case NB: GLIF_PROF_LAUNCH((k_pull_step<NB>), grid, dim3(kPullBlock), lds, s, pa, pull_blocks, sa); break;
+        GLIF_PULL_STEP(1) GLIF_PULL_STEP(2) GLIF_PULL_STEP(3) GLIF_PULL_STEP(4) GLIF_PULL_STEP(5)
+        GLIF_PULL_STEP(6) GLIF_PULL_STEP(7) GLIF_PULL_STEP(8)
+#undef GLIF_PULL_STEP
+        default: break;
+    }
+}
+
+static void launch_r_last(const StepArgs &sa, int nb, dim3 grid, size_t lds, hipStream_t s) {
+    switch (nb) {
+#define GLIF_R_LAST(NB) \
+    case NB: hipLaunchKernelGGL((k_r_last<NB>), grid, dim3(kBlock), lds, s, sa); break;
+        GLIF_R_LAST(1) GLIF_R_LAST(2) GLIF_R_LAST(3) GLIF_R_LAST(4) GLIF_R_LAST(5) GLIF_R_LAST(6) GLIF_R_LAST(7)
+        GLIF_R_LAST(8)
+#undef GLIF_R_LAST
+        default: break;
+    }
+}
+
 template <bool DET>
 static void launch_step(const StepArgs &sa, int nb, dim3 grid, size_t lds, hipStream_t s) {
     switch (nb) {
@@ -1465,6 +1582,11 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     // the step of tick t - 1, whose waves push their spikes' delay-1 events, with the push of
     // tick t's delay-2..D and LGN events (which do not depend on it).
     float *Ih[2] = {w.I, w.I + static_cast<size_t>(B) * c->N * slots};
+    // Deterministic mode: one launch per tick runs the row pull of tick t (into half t % 2 of
+    // I and I2) beside the step of tick t, whose R takes the currents of tick t - 1.
+    float *I2h[2] = {w.I2, w.I2 + BNs * c->nb};
+    const int pull_fused = event ? 0 : fused_pull_blocks(pl, c->nb);
+    const int fused_step_blocks = static_cast<int>(ceil_div(static_cast<int64_t>(B) * c->Np, kPullBlock));
     auto step_args = [&](int t) {
         StepArgs x = sa;
         x.t = t;
@@ -1499,6 +1621,17 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                 ProfScope p(kProfStep, s, true);
                 launch_step<false>(step_args(t), c->nb, step_grid, lds, s);
             }
+        } else if (pull_fused) {
+            pl.t = t;
+            pl.I = Ih[t & 1];
+            pl.I2 = I2h[t & 1];
+            StepArgs x = sa;
+            x.lag = 1;
+            x.I = Ih[(t + 1) & 1];
+            x.I2 = I2h[(t + 1) & 1];
+            x.bkg_x = bkg + static_cast<int64_t>(t > 0 ? t - 1 : 0) * B * tb->n_cols;
+            ProfScope p(kProfStep, s, true);
+            launch_pull_step(pl, pull_fused, x, fused_step_blocks, c->nb, chunk_lds_bytes(pl), s);
         } else {
             pl.t = t;
             {
@@ -1508,6 +1641,16 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
             ProfScope p(kProfStep, s, true);
             launch_step<true>(sa, c->nb, step_grid, lds, s);
         }
+    }
+    if (pull_fused) {
+        // R of the last tick
+        StepArgs x = sa;
+        x.t = T;
+        x.lag = 1;
+        x.I = Ih[(T - 1) & 1];
+        x.I2 = I2h[(T - 1) & 1];
+        x.bkg_x = bkg + static_cast<int64_t>(T - 1) * B * tb->n_cols;
+        launch_r_last(x, c->nb, step_grid, lds, s);
     }
     GLIF_HIP(hipGetLastError());
     hipLaunchKernelGGL(k_state_layout, dim3(ceil_div(BNs, kBlock)), dim3(kBlock), 0, s, st->psc_rise, st->psc,

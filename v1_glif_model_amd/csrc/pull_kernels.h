@@ -290,8 +290,10 @@ __device__ inline void copy_to_lds(uint64_t *dst, const uint64_t *src, int n) {
     }
 }
 
-template <int G, int BLOCK>
-__global__ void __launch_bounds__(BLOCK) k_pull_chunks(PullArgs a) {
+// The chunk walk of workgroup bid of nblocks (the whole grid of k_pull_chunks, or the
+// first block range of a launch that runs other work beside it).
+template <int G>
+__device__ inline void pull_chunks_body(const PullArgs &a, int32_t bid, int32_t nblocks) {
     extern __shared__ float lds_f[];
     float *basis_lds = lds_f;
     const int nbasis = a.n_types * a.nb;
@@ -315,8 +317,8 @@ __global__ void __launch_bounds__(BLOCK) k_pull_chunks(PullArgs a) {
     }
     // wave index made explicitly uniform: chunk indices, descriptors and loop bounds live
     // in scalar registers
-    const int32_t waves = static_cast<int32_t>(gridDim.x * (blockDim.x / kWave));
-    const int32_t wave0 = static_cast<int32_t>(blockIdx.x * (blockDim.x / kWave)) +
+    const int32_t waves = static_cast<int32_t>(nblocks * (blockDim.x / kWave));
+    const int32_t wave0 = static_cast<int32_t>(bid * (blockDim.x / kWave)) +
                           __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
     const int32_t n_all = a.rec_chunks + a.lgn_chunks;
 
@@ -355,6 +357,11 @@ __global__ void __launch_bounds__(BLOCK) k_pull_chunks(PullArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) e[u] = en[u];
     }
+}
+
+template <int G, int BLOCK>
+__global__ void __launch_bounds__(BLOCK) k_pull_chunks(PullArgs a) {
+    pull_chunks_body<G>(a, blockIdx.x, gridDim.x);
 }
 
 static size_t chunk_lds_bytes(const PullArgs &pa) {
