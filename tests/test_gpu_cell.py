@@ -115,6 +115,33 @@ def test_event_forward_delays_and_split_rollout(D, B):
         assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
 
 
+@pytest.mark.parametrize("D,B", [(1, 2), (4, 3)])
+def test_deterministic_split_rollout_bit_exact(D, B):
+    """Deterministic mode, one launch per tick with R updated a tick late: a rollout split in
+    two (the second part starts from carried R, P and spikes in the history) equals the
+    oracle's one-piece rollout bit for bit in spikes, voltages and both final states, so the
+    last tick's R update and the first tick's (none: R of tick -1 is the state) are exact."""
+    cfg = tiny_config(rs=2.0, ins=3.0, delays=D)
+    tn = network(cfg, seed=12, dense_basis=True)
+    T, T1 = 40, 30
+    lgn, bkg = _inputs(cfg, T, B, seed=13)
+    oc = _oracle(tn[1], **ORC_KW)
+    oz, ov, _, ost = oc.forward(lgn, bkg)
+    _, _, _, ost1 = oc.forward(lgn[:T1], bkg[:T1])
+    assert oz[T1 - D:T1].sum() > 0   # the split point carries spikes in its history
+    cell = _cell(tn, "deterministic", **CELL_KW)
+    z1, v1, state = cell.rollout(lgn[:T1], bkg[:T1], state=cell.zero_state(B))
+    mid = [s.clone() for s in state]
+    z2, v2, st = cell.rollout(lgn[T1:], bkg[T1:], state=state)
+    np.testing.assert_array_equal(torch.cat([z1, z2]).cpu().numpy().astype(np.uint8), oz)
+    np.testing.assert_array_equal(torch.cat([v1, v2]).cpu().numpy().view(np.uint32), ov.view(np.uint32))
+    for got, exp in ((mid, ost1), (st, ost)):
+        np.testing.assert_array_equal(got[0].cpu().numpy(), exp["zbuf"])
+        np.testing.assert_array_equal(got[2].cpu().numpy().astype(np.int32), exp["r"])
+        for i, k in ((1, "v"), (3, "asc"), (4, "psc_rise"), (5, "psc")):
+            np.testing.assert_array_equal(got[i].cpu().numpy().view(np.uint32), exp[k].view(np.uint32), err_msg=k)
+
+
 @pytest.mark.parametrize("pseudo_gauss,hard_reset", [(True, False), (False, False), (True, True)])
 def test_backward_matches_oracle(pseudo_gauss, hard_reset):
     cfg = tiny_config(rs=2.0, ins=1.0)
