@@ -1166,19 +1166,7 @@ static int fused_pull_blocks(const PullArgs &pl, int nb) {
     const DevShape &ds = dev_shape();
     const size_t lb = chunk_lds_bytes(pl);
     if (ds.lds_per_cu / lb < 2) return 0;
-    static int cache_pc[64][kMaxBasis + 1];
-    static size_t cache_lb[64][kMaxBasis + 1];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    int per_cu = cache_pc[dev][nb];
-    if (per_cu < 1 || cache_lb[dev][nb] != lb) {
-        const void *fn = pull_step_kernel(nb);
-        if (lb > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lb));
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPullBlock, lb) != hipSuccess || per_cu < 1)
-            per_cu = 1;
-        cache_pc[dev][nb] = per_cu;
-        cache_lb[dev][nb] = lb;
-    }
+    const int per_cu = resident_per_cu(pull_step_kernel(nb), kPullBlock, lb);
     return per_cu < 2 ? 0 : ds.n_cu * per_cu - ds.n_cu / 4;
 }
 

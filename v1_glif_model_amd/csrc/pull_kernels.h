@@ -5,6 +5,8 @@
 #pragma once
 
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "glif_internal.h"
 #include "prof.h"
@@ -373,10 +375,18 @@ struct DevShape {
     size_t lds_per_block = 0, lds_per_cu = 0;
 };
 
+// Launch-shape caches below are shared by every host thread: their lookups and fills hold
+// this lock (a fill queries the runtime once per device and key).
+static std::mutex &shape_mutex() {
+    static std::mutex mu;
+    return mu;
+}
+
 static const DevShape &dev_shape() {
     static DevShape d[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    std::lock_guard<std::mutex> lock(shape_mutex());
     if (d[dev].n_cu == 0) {
         int v = 0;
         DevShape x;
@@ -401,6 +411,29 @@ static bool pull_chunked(const PullArgs &pa) {
     // passes and the half-wave row pull (two rows per wave) was measured faster
     return fits && pa.rec_pidx && (pa.lgn_chunks == 0 || pa.lgn_pidx) && lb <= ds.lds_per_block &&
            pa.B * pa.nb <= kWave;
+}
+
+// Resident workgroups per CU of kernel fn with workgroups of `block` lanes and lb bytes of
+// dynamic LDS on the current device (at least 1).
+static int resident_per_cu(const void *fn, int block, size_t lb) {
+    struct Entry {
+        int dev;
+        const void *fn;
+        int block;
+        size_t lb;
+        int per_cu;
+    };
+    static std::vector<Entry> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    std::lock_guard<std::mutex> lock(shape_mutex());
+    for (const Entry &e : cache)
+        if (e.dev == dev && e.fn == fn && e.block == block && e.lb == lb) return e.per_cu;
+    if (lb > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lb));
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, lb) != hipSuccess || per_cu < 1) per_cu = 1;
+    cache.push_back(Entry{dev, fn, block, lb, per_cu});
+    return per_cu;
 }
 
 template <int BLOCK>
@@ -429,22 +462,7 @@ static bool launch_pull_chunks(const PullArgs &pa, hipStream_t s) {
     const int G = (pa.B * pa.nb + kWave - 1) / kWave;
     const bool wide = ds.lds_per_cu / lb < 2;
     const void *fn = wide ? chunk_kernel<2 * kPullBlock>(G) : chunk_kernel<kPullBlock>(G);
-    // resident workgroups per CU, per device, kernel and LDS size
-    static int cache_pc[64][6];
-    static size_t cache_lb[64][6];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    const int gi = (G == 1 ? 0 : G == 2 ? 1 : 2) + (wide ? 3 : 0);
-    int per_cu = cache_pc[dev][gi];
-    if (per_cu < 1 || cache_lb[dev][gi] != lb) {
-        if (lb > 65536) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lb));
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, wide ? 2 * kPullBlock : kPullBlock, lb) !=
-                hipSuccess ||
-            per_cu < 1)
-            per_cu = 1;
-        cache_pc[dev][gi] = per_cu;
-        cache_lb[dev][gi] = lb;
-    }
+    const int per_cu = resident_per_cu(fn, wide ? 2 * kPullBlock : kPullBlock, lb);
     const dim3 grid(ds.n_cu * per_cu);
     if (wide) launch_chunks<2 * kPullBlock>(G, grid, lb, s, pa);
     else launch_chunks<kPullBlock>(G, grid, lb, s, pa);
