@@ -5,7 +5,8 @@ arithmetic and launch shapes depend on: neuron counts around the 64-lane wave (1
 130, 200), delay slots 1-9, receptors 1-8, synapse types 1-20 (dense basis), batch 1-32
 (every G row length and backward window width), sparse tables with empty columns, and both
 surrogates; cases 4 and 5 receive few of their types per neuron, so they run with compact G rows
-(grouped walk at B = 3, type-phased at B = 7) and the event push into per-type slots.  Per case,
+(grouped walk at B = 3, type-phased at B = 7) and the event push into per-type slots; the last
+case fills all 64 accumulator lanes of the deterministic chunk pull (B = 8, nb = 8).  Per case,
 against the C oracle on the same inputs:
 
 * deterministic forward: spikes, voltages and the final state bit-exact;
@@ -40,6 +41,7 @@ CASES = [
     (65, 4, 2, 1, 4, 17, 14, 20, 3, False, 400.0),
     (64, 6, 6, 4, 9, 32, 12, 25, 4, True, 150.0),
     (200, 10, 1, 5, 5, 9, 16, 60, 5, False, 60.0),
+    (130, 5, 3, 8, 8, 8, 16, 20, 4, True, 30.0),   # B * nb = 64: every lane of the chunk pull adds
 ]
 
 
