@@ -1519,8 +1519,9 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     pa.basis = tr->basis;
     pa.I = w.I;
     // Push grids (blocks of 256 that stride over the events): 2048 where a push runs alone,
-    // 1024 beside the step in the fused launch, which fills the rest of the chip.
-    const int push_grid = 2048, fused_push_grid = 1024;
+    // 768 beside the step in the fused launch, which fills the rest of the chip (config 2:
+    // 38.4 us per tick; 384: 40.8, 512: 39.3, 640: 38.5, 1024: 39.4, 1280: 39.5).
+    const int push_grid = 2048, fused_push_grid = 768;
     const dim3 step_grid(ceil_div(static_cast<int64_t>(B) * c->Np, kBlock));
 
     PullArgs pl{};
