@@ -436,22 +436,6 @@ static int resident_per_cu(const void *fn, int block, size_t lb) {
     return per_cu;
 }
 
-template <int BLOCK>
-static const void *chunk_kernel(int G) {
-    return G == 1 ? reinterpret_cast<const void *>(&k_pull_chunks<1, BLOCK>)
-           : G == 2 ? reinterpret_cast<const void *>(&k_pull_chunks<2, BLOCK>)
-                    : reinterpret_cast<const void *>(&k_pull_chunks<4, BLOCK>);
-}
-
-template <int BLOCK>
-static void launch_chunks(int G, dim3 grid, size_t lb, hipStream_t s, const PullArgs &pa) {
-    switch (G) {
-        case 1: GLIF_PROF_LAUNCH((k_pull_chunks<1, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
-        case 2: GLIF_PROF_LAUNCH((k_pull_chunks<2, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
-        default: GLIF_PROF_LAUNCH((k_pull_chunks<4, BLOCK>), grid, dim3(BLOCK), lb, s, pa); break;
-    }
-}
-
 // The resident chunk kernel, when pull_chunked(pa); false (nothing launched) otherwise.
 // Workgroups of kPullBlock lanes, as many as stay resident; when the bitmaps leave room
 // for only one workgroup per CU, workgroups of 2 * kPullBlock lanes instead.
@@ -459,13 +443,14 @@ static bool launch_pull_chunks(const PullArgs &pa, hipStream_t s) {
     if (!pull_chunked(pa)) return false;
     const DevShape &ds = dev_shape();
     const size_t lb = chunk_lds_bytes(pa);
-    const int G = (pa.B * pa.nb + kWave - 1) / kWave;
+    // pull_chunked: B * nb <= 64, one accumulator slot per lane (G = 1)
     const bool wide = ds.lds_per_cu / lb < 2;
-    const void *fn = wide ? chunk_kernel<2 * kPullBlock>(G) : chunk_kernel<kPullBlock>(G);
+    const void *fn = wide ? reinterpret_cast<const void *>(&k_pull_chunks<1, 2 * kPullBlock>)
+                          : reinterpret_cast<const void *>(&k_pull_chunks<1, kPullBlock>);
     const int per_cu = resident_per_cu(fn, wide ? 2 * kPullBlock : kPullBlock, lb);
     const dim3 grid(ds.n_cu * per_cu);
-    if (wide) launch_chunks<2 * kPullBlock>(G, grid, lb, s, pa);
-    else launch_chunks<kPullBlock>(G, grid, lb, s, pa);
+    if (wide) GLIF_PROF_LAUNCH((k_pull_chunks<1, 2 * kPullBlock>), grid, dim3(2 * kPullBlock), lb, s, pa);
+    else GLIF_PROF_LAUNCH((k_pull_chunks<1, kPullBlock>), grid, dim3(kPullBlock), lb, s, pa);
     return true;
 }
 
