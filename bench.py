@@ -398,10 +398,11 @@ def main():
     fwd_ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     timings = []
 
+    zero_each_step = [*state, spike_count]
+
     def step():
-        for s in state:      # every batch starts from the zero state
-            s.zero_()
-        spike_count.zero_()
+        # every batch starts from the zero state (one multi-tensor fill)
+        torch._foreach_zero_(zero_each_step)
         cell.refresh_weights(force=True)
         fwd_ev[0].record()
         cell.rollout(lgn, bkg, state=state, record_z=False, record_v=False, spike_count=spike_count,
