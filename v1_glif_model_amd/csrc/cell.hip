@@ -1,17 +1,22 @@
 // The GLIF_3 cell over T steps (V1Column.call, models.py:1059-1135) and its BPTT.
 //
 // Forward, per step t (one stream, no host round trip):
+//   LGN (B <= 8): k_lgn_rows computes the LGN currents of 64 ticks at a time, per post
+//                 row in the reference's order, into a ring of current slots ahead of
+//                 the ticks that read them (with more batch entries, or the per-type
+//                 push, the LGN events are pushed or pulled per tick as below);
 //   event mode:   k_push(t)   the spike words of steps t-1..t-D (set bits = columns of
-//                             the recurrent table) and the step's LGN (column,
-//                             batch-mask) list are streamed through the column-grouped
-//                             tables and added into I with fp32 atomics;
+//                             the recurrent table), and without the LGN ring the step's
+//                             LGN (column, batch-mask) list, are streamed through the
+//                             column-grouped tables and added into I with fp32 atomics;
 //                 k_step(t)   background pull, GLIF_3 update, spike bits (wave
-//                             ballots); I is re-zeroed after reading.
-//   deterministic: the row pull (pull_kernels.h) sums rec and LGN per post row in
-//                 the reference's accumulation order and k_step adds the background
-//                 and does the same update; with the resident chunk pull both run in
-//                 one launch per tick (k_pull_step: the pull of t beside the step of
-//                 t, whose R takes the currents of t - 1).
+//                             ballots); I is re-zeroed after reading (not with the
+//                             LGN ring, which the next LGN segment rewrites).
+//   deterministic: the row pull (pull_kernels.h) sums rec (and without the LGN ring,
+//                 LGN) per post row in the reference's accumulation order and k_step
+//                 adds the LGN and background currents and does the same update; with
+//                 the resident chunk pull both run in one launch per tick (k_pull_step:
+//                 the pull of t beside the step of t, whose R takes the currents of t - 1).
 // Backward, in windows of Wwin reverse ticks t0, t0-1, .. (lagged adjoint, k_adj):
 //   k_adj         per tick t: gz_t -> gV_t -> gP_{t-1} -> gR_{t-2} -> G_{t-2}
 //   k_bwd_rec_gs  dz of the window's steps t0-2, t0-3, .. over the recurrent columns
@@ -48,6 +53,9 @@ struct CellWs {
     uint64_t *abits;    // [(T + D)][W]      bit n: z_t[b][n] for some b (slot t + D)
     uint64_t *lbits;    // [T][Wl]           bit pre: x_t[b][pre] > 0 for some b
     float *I2;          // [2][nb][B][N]   LGN currents (deterministic chunk pull)
+    float *IL;          // [kLgnRing][nb][B][N]  LGN currents computed ahead of the loop (B <= 8):
+                        // the event push adds onto them, the deterministic step adds them
+    uint8_t *lgnT;      // [ceil(T / 64)][n_lgn][64]  LGN batch masks by input, then tick
     float *vsave;       // [T][B][N]
     int64_t *lgn_off;   // [T + 1]           per-step LGN (column, batch-mask) lists
     int32_t *lgn_pre;   // [T * n_lgn]
@@ -69,6 +77,23 @@ struct CellWs {
     float *dw_rec;      // column-grouped order with the grouped walk, else type-phased
     float *dw_lgn, *dw_bkg;  // column-grouped order
 };
+
+// ------------------------------------------------- LGN currents ahead of the loop ----
+// The LGN inputs of a rollout are known before its first tick, so their currents are
+// computed in segments of kLgnSeg ticks ahead of the T loop instead of being pushed with
+// atomics (event mode) or pulled row by row inside it (deterministic mode).  Each
+// segment's currents land in a ring of kLgnRing current slots [nb][B][N], which the
+// event push then adds the recurrent events to, or which the deterministic step adds to
+// the pulled recurrent currents.  Ring safety: the segment of ticks [64s, 64s + 64) is
+// computed right before tick 64s's launch and overwrites the slots of ticks up to
+// 64s - 3, whose last reader (the step of that tick) ran in launch 64s - 2 at the latest.
+constexpr int kLgnSeg = 64;
+constexpr int kLgnRing = kLgnSeg + 2;
+constexpr int kLgnPosts = 8;     // posts (waves) per k_lgn_rows workgroup
+constexpr int kLgnMaxBatch = 8;  // the tick-major masks hold one byte per (input, tick)
+
+// Whether this cell computes its LGN currents ahead of the loop at batch size B.
+static bool lgn_ahead(const Cell *c, int B) { return B <= kLgnMaxBatch && c->lgn->n_cols > 0; }
 
 // Backward window width (reverse ticks per table pass) and G row length.
 static int win_width(int B) { return 3 * B <= 16 ? 3 : 1; }
@@ -95,6 +120,10 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.abits = cv.take<uint64_t>(static_cast<size_t>(T + c->D) * c->W);
     w.lbits = cv.take<uint64_t>(static_cast<size_t>(T) * ((nl + 63) / 64));
     w.I2 = cv.take<float>(2 * BN * c->nb);  // deterministic pull beside the step: two halves
+    if (lgn_ahead(c, B)) {
+        w.IL = cv.take<float>(static_cast<size_t>(kLgnRing) * BN * c->nb);
+        w.lgnT = cv.take<uint8_t>(static_cast<size_t>((T + kLgnSeg - 1) / kLgnSeg) * nl * kLgnSeg);
+    }
     w.vsave = cv.take<float>(static_cast<size_t>(T) * BN);
     w.lgn_off = cv.take<int64_t>(T + 1);
     w.lgn_pre = cv.take<int32_t>(static_cast<size_t>(T) * nl);
@@ -197,6 +226,178 @@ __global__ void __launch_bounds__(kBlock)
     if ((threadIdx.x & (kWave - 1)) == 0) lbits[t * Wl + (pre >> 6)] = bits;
 }
 
+// lgnT[(seg * n_in + pre) * 64 + k] = batch mask of the LGN inputs x[64 seg + k][b][pre] > 0
+// (0 past T).  Workgroup: one segment x 64 inputs; the masks are composed with reads
+// coalesced over the inputs and leave, through an LDS transpose, as contiguous 64-byte rows.
+__global__ void __launch_bounds__(kBlock)
+    k_lgn_tmask(const uint8_t *__restrict__ x, int T, int B, int32_t n_in, uint8_t *__restrict__ lgnT) {
+    __shared__ uint32_t tile[64][17];  // [input][4 ticks per word], padded against bank conflicts
+    const int seg = blockIdx.y;
+    const int32_t pre0 = blockIdx.x * 64;
+    const int lane = threadIdx.x & 63, wq = threadIdx.x >> 6;  // wq: 4 waves
+    const int32_t pre = pre0 + lane;
+    for (int kw = wq; kw < 16; kw += 4) {
+        uint32_t word = 0;
+        for (int j = 0; j < 4; ++j) {
+            const int t = seg * kLgnSeg + 4 * kw + j;
+            uint32_t m = 0;
+            if (pre < n_in && t < T)
+                for (int b = 0; b < B; ++b)
+                    if (x[(static_cast<int64_t>(t) * B + b) * n_in + pre] > 0) m |= 1u << b;
+            word |= m << (8 * j);
+        }
+        tile[lane][kw] = word;
+    }
+    __syncthreads();
+    uint32_t *out = reinterpret_cast<uint32_t *>(lgnT + (static_cast<int64_t>(seg) * n_in + pre0) * kLgnSeg);
+    for (int i = threadIdx.x; i < 64 * 16; i += blockDim.x) {
+        const int p = i >> 4, kw = i & 15;
+        if (pre0 + p < n_in) out[i] = tile[p][kw];
+    }
+}
+
+struct LgnRowArgs {
+    int32_t seg, T, N, B, nb, n_types, n_in;
+    const int32_t *row;   // post-grouped LGN table: row pointers,
+    const uint32_t *pd;   // pre | (delay - 1) << 24,
+    const uint8_t *sid;   // synapse type,
+    const float *w;       // weight, in ascending (column, synapse id) order per row
+    const uint8_t *lgnT;  // tick-major batch masks (k_lgn_tmask)
+    const float *basis;   // [n_types][nb]
+    float *ring;          // kLgnRing slots of [nb][B][N]
+};
+
+// One wave per post, lane k = tick 64 seg + k: the row's entries are wave-uniform, each
+// lane tests its tick's batch mask of the entry's input (one coalesced 64-byte load per
+// entry) and adds w * basis[type][r] into its (b, r) accumulators in entry order from +0
+// -- per (tick, b, post, r) the reference's order over the LGN events, the same sum the
+// deterministic row pull forms.  Zero products are skipped (adding +/-0 to a sum started
+// at +0 never changes it), so only the receptors the type's basis feeds are visited.  The
+// workgroup's 8 posts then write each (b, r) plane through LDS as 32-byte runs.
+template <int NB, int BB>
+__global__ void __launch_bounds__(kLgnPosts * kWave) k_lgn_rows(LgnRowArgs a) {
+    __shared__ float tile[2][kLgnSeg][kLgnPosts + 1];
+    extern __shared__ float basis_lds[];  // [n_types][nb], then the per-type receptor masks
+    uint32_t *nz_lds = reinterpret_cast<uint32_t *>(basis_lds + a.n_types * NB);
+    load_basis_lds(basis_lds, a.basis, a.n_types * NB);
+    for (int s = threadIdx.x; s < a.n_types; s += blockDim.x) {
+        uint32_t m = 0;
+        for (int q = 0; q < NB; ++q)
+            if (a.basis[s * NB + q] != 0.0f) m |= 1u << q;
+        nz_lds[s] = m;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    // XCD-aware order: workgroups go to the 8 XCDs round robin (blockIdx % 8), so group g of
+    // consecutive posts is given to workgroup (g % per) * 8 + g / per: neighbouring groups,
+    // whose 32-byte output runs share 128-byte lines, are written through the same L2
+    const int32_t per = static_cast<int32_t>(gridDim.x) / 8;
+    const int32_t grp = static_cast<int32_t>(blockIdx.x % 8) * per + static_cast<int32_t>(blockIdx.x / 8);
+    const int32_t n = grp * kLgnPosts + wv;
+    float acc[BB][NB];
+#pragma unroll
+    for (int b = 0; b < BB; ++b)
+#pragma unroll
+        for (int q = 0; q < NB; ++q) acc[b][q] = 0.0f;
+    if (n < a.N) {
+        const uint8_t *mt = a.lgnT + static_cast<int64_t>(a.seg) * a.n_in * kLgnSeg + lane;
+        const int32_t j0 = a.row[n], j1 = a.row[n + 1];
+        // Up to 64 entries at a time: lane l loads entry jb + l (input, type, weight; three
+        // coalesced loads, indices clamped to the row's last entry), and the walk reads them
+        // back with lane reads.  The batch masks of 8 entries are loaded together, the next 8
+        // before this 8 are processed.
+        for (int32_t jb = j0; jb < j1; jb += kWave) {
+            const int cnt = min(j1 - jb, kWave);
+            const int32_t jl = min(jb + lane, j1 - 1);
+            const int pre_l = static_cast<int>(a.pd[jl] & kLow24);
+            const int sid_l = a.sid[jl];
+            const float w_l = a.w[jl];
+            // entry jb + l's products w * basis[type][r] and the receptors its type feeds
+            const int nz_l = static_cast<int>(nz_lds[sid_l]);
+            int v_l[NB];
+#pragma unroll
+            for (int q = 0; q < NB; ++q) v_l[q] = __float_as_int(w_l * basis_lds[sid_l * NB + q]);
+            uint32_t m[8];
+            auto fetch = [&](int ub) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    m[u] = mt[static_cast<int64_t>(__builtin_amdgcn_readlane(pre_l, ub + u)) * kLgnSeg];
+            };
+            fetch(0);
+            for (int ub = 0; ub < cnt; ub += 8) {
+                uint32_t mc[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) mc[u] = m[u];
+                if (ub + 8 < cnt) fetch(ub + 8);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (ub + u >= cnt) break;
+                    if (__ballot(mc[u] != 0u) == 0ull) continue;
+                    const uint32_t nz = static_cast<uint32_t>(__builtin_amdgcn_readlane(nz_l, ub + u));
+                    bool hit[BB];
+#pragma unroll
+                    for (int b = 0; b < BB; ++b) hit[b] = (mc[u] >> b) & 1u;
+#pragma unroll
+                    for (int q = 0; q < NB; ++q) {
+                        if (!((nz >> q) & 1u)) continue;
+                        const float v = __int_as_float(__builtin_amdgcn_readlane(v_l[q], ub + u));
+#pragma unroll
+                        for (int b = 0; b < BB; ++b)
+                            if (hit[b]) acc[b][q] = acc[b][q] + v;
+                    }
+                }
+            }
+        }
+    }
+    // every wave takes part in the write-out (barriers), live or not
+    const int64_t BN = static_cast<int64_t>(a.B) * a.N;
+    const int kt = threadIdx.x / kLgnPosts, p = threadIdx.x % kLgnPosts;
+    const int t = a.seg * kLgnSeg + kt;
+    const int32_t np = grp * kLgnPosts + p;
+    float *slot = a.ring + static_cast<int64_t>(t % kLgnRing) * NB * BN;
+    int buf = 0;
+#pragma unroll
+    for (int b = 0; b < BB; ++b) {
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+            tile[buf][lane][wv] = acc[b][q];
+            __syncthreads();
+            if (t < a.T && np < a.N) slot[q * BN + static_cast<int64_t>(b) * a.N + np] = tile[buf][kt][p];
+            buf ^= 1;
+        }
+    }
+}
+
+template <int NB>
+static void launch_lgn_rows_nb(const LgnRowArgs &la, dim3 grid, size_t lds, hipStream_t s) {
+    switch (la.B) {
+#define GLIF_LGN_ROWS(BB) \
+    case BB: GLIF_PROF_LAUNCH((k_lgn_rows<NB, BB>), grid, dim3(kLgnPosts * kWave), lds, s, la); break;
+        GLIF_LGN_ROWS(1) GLIF_LGN_ROWS(2) GLIF_LGN_ROWS(3) GLIF_LGN_ROWS(4) GLIF_LGN_ROWS(5)
+        GLIF_LGN_ROWS(6) GLIF_LGN_ROWS(7) GLIF_LGN_ROWS(8)
+#undef GLIF_LGN_ROWS
+        default: break;
+    }
+}
+
+static void launch_lgn_rows(const LgnRowArgs &la, hipStream_t s) {
+    // a multiple of 8 workgroups (the XCD-aware order); groups past the last post idle
+    const dim3 grid(static_cast<unsigned>(8 * ceil_div(static_cast<int64_t>(la.N), 8 * kLgnPosts)));
+    const size_t lds = sizeof(float) * la.n_types * (la.nb + 1);
+    switch (la.nb) {
+        case 1: launch_lgn_rows_nb<1>(la, grid, lds, s); break;
+        case 2: launch_lgn_rows_nb<2>(la, grid, lds, s); break;
+        case 3: launch_lgn_rows_nb<3>(la, grid, lds, s); break;
+        case 4: launch_lgn_rows_nb<4>(la, grid, lds, s); break;
+        case 5: launch_lgn_rows_nb<5>(la, grid, lds, s); break;
+        case 6: launch_lgn_rows_nb<6>(la, grid, lds, s); break;
+        case 7: launch_lgn_rows_nb<7>(la, grid, lds, s); break;
+        case 8: launch_lgn_rows_nb<8>(la, grid, lds, s); break;
+        default: break;
+    }
+}
+
 // z_buf out = [z_{T-1}, ..., z_{T-D}].
 __global__ void __launch_bounds__(kBlock)
     k_write_zbuf(float *__restrict__ z_buf, CellConst k, int T, const uint64_t *__restrict__ zbits) {
@@ -270,7 +471,7 @@ __device__ inline void push_body(const PushArgs &a, int64_t bid, int64_t nblk) {
     load_basis_lds(basis_lds, a.basis, a.n_types * a.nb);
     const int64_t BW = static_cast<int64_t>(a.B) * a.W;
     const int64_t n_words = a.d_hi >= a.d_lo ? static_cast<int64_t>(a.d_hi - a.d_lo + 1) * BW : 0;
-    const int64_t l0 = a.lgn_off[a.t], n_lgn = a.lgn ? a.lgn_off[a.t + 1] - l0 : 0;
+    const int64_t l0 = a.lgn ? a.lgn_off[a.t] : 0, n_lgn = a.lgn ? a.lgn_off[a.t + 1] - l0 : 0;
     const int64_t units = n_words + n_lgn * a.chunks_lgn;
     const int lane_s = threadIdx.x % L;
     const int64_t n_subs = nblk * blockDim.x / L;
@@ -366,6 +567,9 @@ struct StepArgs {
     // deterministic pull beside the step (lag = 1): R takes tick t - 1's currents (I, I2
     // and bkg_x point at that tick; none at t = 0), P the R of tick t - 1 so updated
     int32_t lag;
+    // event mode: I is a slot of the LGN ring, which the LGN pass rewrites before its next
+    // use, so the step leaves it as it is (0: the step clears I after reading it)
+    int32_t keep_I;
 };
 
 // The input of R for (b, n) at one tick, (I_rec + I_lgn) + I_bkg, times lr_scale
@@ -401,7 +605,7 @@ __device__ inline void step_inputs(const StepArgs &a, const float *basis_lds, in
             float *Ip = a.I + q * BN + bn;
             Irl[q] = *Ip;
             if (DET && a.I2) Irl[q] = Irl[q] + a.I2[q * BN + bn];
-            if (!DET) *Ip = 0.0f;
+            if (!DET && !a.keep_I) *Ip = 0.0f;
         }
     }
     // background: every synapse of the row, weight times the Poisson count.  A zero
@@ -1418,10 +1622,36 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     const bool event = mode == GLIF_MODE_EVENT;
     const Table *tr = c->rec, *tl = c->lgn, *tb = c->bkg;
     int rc;
+    // event push into per-type slots ([gk][B][N] per tick) or receptor currents ([nb][B][N])
+    const bool typed = event && c->push_typed;
+    // LGN currents computed ahead of the loop, segment by segment, into the LGN ring (the
+    // per-type push keeps pushing its LGN events into the type slots)
+    const bool ahead = lgn_ahead(c, B) && !typed;
 
     // input lists (LGN push in the forward, LGN / background dW in the backward)
-    if ((rc = build_batch_mask_lists(lgn, T, B, tl->n_cols, w.lgn_off, w.lgn_pre, w.lgn_mask, w.scratch, s)))
+    if (event && !ahead &&
+        (rc = build_batch_mask_lists(lgn, T, B, tl->n_cols, w.lgn_off, w.lgn_pre, w.lgn_mask, w.scratch, s)))
         return rc;
+    const int nseg = (T + kLgnSeg - 1) / kLgnSeg;
+    if (ahead) {
+        hipLaunchKernelGGL(k_lgn_tmask, dim3(ceil_div(tl->n_cols, 64), nseg), dim3(kBlock), 0, s, lgn, T, B,
+                           static_cast<int32_t>(tl->n_cols), w.lgnT);
+        GLIF_HIP(hipGetLastError());
+    }
+    LgnRowArgs la{};
+    la.T = T;
+    la.N = c->N;
+    la.B = B;
+    la.nb = c->nb;
+    la.n_types = c->n_types;
+    la.n_in = static_cast<int32_t>(tl->n_cols);
+    la.row = tl->row_ptr;
+    la.pd = tl->pd;
+    la.sid = tl->sid_row;
+    la.w = tl->w_row;
+    la.lgnT = w.lgnT;
+    la.basis = tr->basis;
+    la.ring = w.IL;
     const int Wwin = win_width(B), nwin = n_windows(T, Wwin);
     if (nwin > 0) {
         if ((rc = build_window_mask_lists(lgn, T, B, tl->n_cols, Wwin, nwin, w.lw_off, w.lw_pre, w.lw_mask,
@@ -1441,10 +1671,8 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                        w.zbits, event ? nullptr : w.zmask,
                        event ? nullptr : w.abits);
     GLIF_HIP(hipGetLastError());
-    // event push into per-type slots ([gk][B][N] per tick) or receptor currents ([nb][B][N])
-    const bool typed = event && c->push_typed;
     const int slots = typed ? c->g_rows : c->nb;
-    if (event && (rc = launch_fill_u32(w.I, 0u, 2 * static_cast<size_t>(B) * c->N * slots, s))) return rc;
+    if (event && !ahead && (rc = launch_fill_u32(w.I, 0u, 2 * static_cast<size_t>(B) * c->N * slots, s))) return rc;
     const int64_t BNs = static_cast<int64_t>(B) * c->N;
     hipLaunchKernelGGL(k_state_layout, dim3(ceil_div(BNs, kBlock)), dim3(kBlock), 0, s, st->psc_rise, st->psc,
                        st->asc, w.R, w.P, w.A, BNs, c->nb, 1);
@@ -1493,6 +1721,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     sa.basis = tr->basis;
     sa.gk = typed ? c->g_rows : 0;
     sa.gtype = c->g_type;
+    sa.keep_I = event && ahead;
 
     PushArgs pa{};
     pa.D = c->D;
@@ -1503,7 +1732,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     pa.chunks_lgn = chunks_for(tl, kWave);
     pa.d_lo = 1;
     pa.d_hi = c->D;
-    pa.lgn = 1;
+    pa.lgn = ahead ? 0 : 1;
     pa.zbits = w.zbits;
     pa.W = c->W;
     pa.typed = typed ? 1 : 0;
@@ -1560,8 +1789,14 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         pl.rec_cdesc = tr->chunk_desc;
         pl.lgn_cdesc = tl->chunk_desc;
         pl.I2 = w.I2;
+        if (ahead) {
+            // the pull sums the recurrent rows only; the step adds the LGN ring's currents
+            pl.lgn_chunks = 0;
+            pl.lgn_row = nullptr;
+            pl.Wl = 0;
+        }
         // the step adds the chunk form's LGN currents (I2); k_pull writes rec + lgn to I
-        sa.I2 = pull_chunked(pl) ? w.I2 : nullptr;
+        sa.I2 = ahead ? w.IL : pull_chunked(pl) ? w.I2 : nullptr;
         const int64_t n_lm = static_cast<int64_t>(T) * pl.Wl * 64;
         if (n_lm > 0) {
             hipLaunchKernelGGL(k_lgn_mask, dim3(ceil_div(n_lm, kBlock)), dim3(kBlock), 0, s, lgn, T, B,
@@ -1577,12 +1812,17 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     // Deterministic mode: one launch per tick runs the row pull of tick t (into half t % 2 of
     // I and I2) beside the step of tick t, whose R takes the currents of tick t - 1.
     float *I2h[2] = {w.I2, w.I2 + BNs * c->nb};
+    // With the LGN ring, tick t's currents start in ring slot t % kLgnRing (event mode: the
+    // push adds onto them; deterministic mode: the step adds them to the pulled ones).
+    auto ring_slot = [&](int t) { return w.IL + static_cast<size_t>(t % kLgnRing) * BNs * c->nb; };
+    auto cur = [&](int t) { return event && ahead ? ring_slot(t) : Ih[t & 1]; };
+    auto lgn_cur = [&](int t) { return ahead ? ring_slot(t) : I2h[t & 1]; };
     const int pull_fused = event ? 0 : fused_pull_blocks(pl, c->nb);
     const int fused_step_blocks = static_cast<int>(ceil_div(static_cast<int64_t>(B) * c->Np, kPullBlock));
     auto step_args = [&](int t) {
         StepArgs x = sa;
         x.t = t;
-        x.I = Ih[t & 1];
+        x.I = cur(t);
         x.lgn_x = lgn + static_cast<int64_t>(t) * B * tl->n_cols;
         x.bkg_x = bkg + static_cast<int64_t>(t) * B * tb->n_cols;
         return x;
@@ -1591,10 +1831,15 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         sa.t = t;
         sa.lgn_x = lgn + static_cast<int64_t>(t) * B * tl->n_cols;
         sa.bkg_x = bkg + static_cast<int64_t>(t) * B * tb->n_cols;
+        if (ahead && t % kLgnSeg == 0) {
+            la.seg = t / kLgnSeg;
+            ProfScope p(kProfPush, s, true);
+            launch_lgn_rows(la, s);
+        }
         if (event) {
             PushArgs early = pa;
             early.t = t;
-            early.I = Ih[t & 1];
+            early.I = cur(t);
             if (t == 0) {
                 // tick 0: every delay slot (the initial history) and the LGN inputs
                 ProfScope p(kProfPush, s, true);
@@ -1602,7 +1847,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
             } else {
                 early.d_lo = 2;   // d_hi = D; nothing recurrent when D = 1
                 StepArgs x = step_args(t - 1);
-                x.I_next = Ih[t & 1];
+                x.I_next = cur(t);
                 x.p1_colptr = tr->col_ptr;
                 x.p1_ps = typed ? tr->cg.ps : tr->ps;
                 x.p1_w = tr->w_col;
@@ -1620,7 +1865,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
             StepArgs x = sa;
             x.lag = 1;
             x.I = Ih[(t + 1) & 1];
-            x.I2 = I2h[(t + 1) & 1];
+            x.I2 = ahead || sa.I2 ? lgn_cur(t > 0 ? t - 1 : 0) : nullptr;  // not read at t = 0
             x.bkg_x = bkg + static_cast<int64_t>(t > 0 ? t - 1 : 0) * B * tb->n_cols;
             ProfScope p(kProfStep, s, true);
             launch_pull_step(pl, pull_fused, x, fused_step_blocks, c->nb, chunk_lds_bytes(pl), s);
@@ -1630,8 +1875,10 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                 ProfScope p(kProfPush, s, true);
                 launch_pull(pl, lds, s);
             }
+            StepArgs x = sa;
+            if (ahead) x.I2 = ring_slot(t);
             ProfScope p(kProfStep, s, true);
-            launch_step<true>(sa, c->nb, step_grid, lds, s);
+            launch_step<true>(x, c->nb, step_grid, lds, s);
         }
     }
     if (pull_fused) {
@@ -1640,7 +1887,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         x.t = T;
         x.lag = 1;
         x.I = Ih[(T - 1) & 1];
-        x.I2 = I2h[(T - 1) & 1];
+        x.I2 = ahead || sa.I2 ? lgn_cur(T - 1) : nullptr;
         x.bkg_x = bkg + static_cast<int64_t>(T - 1) * B * tb->n_cols;
         launch_r_last(x, c->nb, step_grid, lds, s);
     }

@@ -118,14 +118,17 @@ __global__ void __launch_bounds__(kBlock) k_pull(PullArgs a) {
 #pragma unroll
     for (int g = 0; g < G; ++g) ar[g] = al[g] = 0.0f;
     pull_row<G, true>(a, basis_lds, lane32, half, live ? a.rec_row[n] : 0, live ? a.rec_row[n + 1] : 0, ar);
-    pull_row<G, false>(a, basis_lds, lane32, half, live ? a.lgn_row[n] : 0, live ? a.lgn_row[n + 1] : 0, al);
+    // lgn_row null: the LGN currents come from elsewhere (the cell's LGN ring) and I
+    // holds the recurrent sum alone
+    const bool lgn = a.lgn_row != nullptr;
+    if (lgn) pull_row<G, false>(a, basis_lds, lane32, half, live ? a.lgn_row[n] : 0, live ? a.lgn_row[n + 1] : 0, al);
     if (!live) return;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const int ai = lane32 + 32 * g;
         if (ai < a.B * a.nb) {
             const int b = ai / a.nb, r = ai - b * a.nb;
-            a.I[r * a.os_r + b * a.os_b + n * a.os_n] = ar[g] + al[g];
+            a.I[r * a.os_r + b * a.os_b + n * a.os_n] = lgn ? ar[g] + al[g] : ar[g];
         }
     }
 }
