@@ -429,7 +429,8 @@ def main():
     # Event mode's forward is one fused launch per tick (the step of t - 1 beside the pushes,
     # "step"), and so is deterministic mode's (the row pull of t beside the step of t, whose R
     # takes the currents of t - 1; "step"; where the pull and the step run as two launches the
-    # row pull is "push"); "adj" is the adjoint launch with the
+    # row pull is "push"); "lgn" computes 64 ticks of LGN currents ahead of the loop (batch
+    # sizes up to 8); "adj" is the adjoint launch with the
     # previous window's weight gradients and the rest of its dz walk; "bwd_rec" the dz walk
     # over the columns the next adjoint reads.
     _lib.prof_enable(list(_lib.PROF_KINDS))
@@ -471,6 +472,11 @@ def main():
     while Rg < Wwin * B:
         Rg *= 2
     words = (N + 63) // 64
+    # LGN currents computed ahead of the loop (the "lgn" class ran): the tick's launch then
+    # pushes or pulls the recurrent events only, and in event mode the step leaves the
+    # current slot to the next LGN pass instead of clearing it
+    lgn_ahead = breakdown.get("lgn", {}).get("launches", 0) > 0
+    e_in = 0.0 if lgn_ahead else e_lgn
     tot_ms, launches = prof.get(dominant, (0.0, 0))
     # the grouped dz walk (16-float G rows) with the weight gradients deferred splits each
     # window's walk: the columns of delays <= 2 Wwin - 3 (what the next window's adjoint reads,
@@ -509,38 +515,49 @@ def main():
         # synapse event: 4-byte entry, the dW read and written, one G element) and the rest of
         # its dz walk (8-byte entries of the other columns, their pointers and dz rows)
         rows = cell.g_layout()[0]
-        act_ev = (e_rec + e_lgn) / max(T, 1) * Wwin
+        act_ev = (e_rec + e_lgn) / max(T, 1) * Wwin   # the backward's dW covers both
         alg_bytes = (Wwin * B * N * (D * 4 + 4) + Wwin * B * words * 8 + 2 * B * N * (1 + 2 * nb) * 4
                      + N * rows * Rg * 4 + act_ev * 16
                      + (S - s_a) * 8 + (n_cols - cols_a + 1) * 4 + Wwin * B * (n_cols - cols_a) * 4)
         unit_desc = f"bytes per backward window of {Wwin} timesteps (adjoint + previous window's dW and dz rest)"
     elif dominant == "step" and args.mode == "deterministic":
-        # per launch = one tick: the row pull (every recurrent and LGN entry's bitmap index,
-        # 4 bytes; the row pointers; each active entry's batch mask, weight and type, 9 bytes;
-        # the rec and LGN currents written) beside the GLIF_3 step's state stream per (b, n)
-        # -- reads the previous tick's pulled I and I2, R, P (nb floats each), A (2 floats),
-        # v, r (int16); writes R, P, A, v, r and the saved voltage -- the per-neuron constants
+        # per launch = one tick: the row pull (every recurrent entry's bitmap index, and the
+        # LGN ones when their currents are not computed ahead, 4 bytes; the row pointers; each
+        # active entry's batch mask, weight and type, 9 bytes; the currents written) beside the
+        # GLIF_3 step's state stream per (b, n) -- reads the previous tick's pulled I and its
+        # LGN currents (I2 or the LGN ring's slot), R, P (nb floats each), A (2 floats), v, r
+        # (int16); writes R, P, A, v, r and the saved voltage -- the per-neuron constants
         # (7 floats) and the background rows (8 bytes per synapse)
-        active = (e_rec + e_lgn) / max(T, 1)
+        active = (e_rec + e_in) / max(T, 1)
+        tables = 1 if lgn_ahead else 2
         per_bn = (4 * nb * 4 + 14) + (2 * nb * 4 + 18)
-        alg_bytes = ((S + tb.lgn.n_syn) * 4 + 2 * (N + 1) * 4 + active * 9 + 2 * nb * B * N * 4
-                     + B * N * per_bn + N * 28 + tb.bkg.n_syn * 8)
+        alg_bytes = ((S + (0 if lgn_ahead else tb.lgn.n_syn)) * 4 + tables * (N + 1) * 4 + active * 9
+                     + tables * nb * B * N * 4 + B * N * per_bn + N * 28 + tb.bkg.n_syn * 8)
         unit_desc = "bytes per forward timestep (deterministic row pull beside the GLIF_3 step)"
     elif dominant == "step":
         # per launch = one tick: the GLIF_3 step's state stream per (b, n) -- reads I, R, P
-        # (nb floats each), A (2 floats), v, r (int16); writes I (cleared), R, P, A, v, r and
-        # the saved voltage -- the per-neuron constants (7 floats), the background rows (8 bytes
-        # per synapse), and the tick's pushed events (8-byte entry + one 4-byte atomic each)
-        active = (e_rec + e_lgn) / max(T, 1)
-        per_bn = (3 * nb * 4 + 14) + (3 * nb * 4 + 18)
+        # (nb floats each), A (2 floats), v, r (int16); writes R, P, A, v, r, the saved voltage
+        # and, without the LGN ring, I (cleared) -- the per-neuron constants (7 floats), the
+        # background rows (8 bytes per synapse), and the tick's pushed events (8-byte entry +
+        # one 4-byte atomic each; the LGN events too when their currents are not computed ahead)
+        active = (e_rec + e_in) / max(T, 1)
+        per_bn = (3 * nb * 4 + 14) + ((2 if lgn_ahead else 3) * nb * 4 + 18)
         alg_bytes = B * N * per_bn + N * 28 + tb.bkg.n_syn * 8 + active * 12
         unit_desc = "bytes per forward timestep (GLIF_3 step + the tick's pushed events)"
+    elif dominant == "lgn":
+        # per launch = 64 ticks of LGN currents: every LGN entry (input, weight, type: 9
+        # bytes), the row pointers, the segment's tick masks per (input, batch entry), 8 bytes,
+        # and the 64 current slots written ([nb][B][N] floats each)
+        alg_bytes = (tb.lgn.n_syn * 9 + (N + 1) * 4 + tb.lgn.n_cols * B * 8 + 64 * nb * B * N * 4)
+        unit_desc = "bytes per 64-tick segment of LGN currents"
     else:
-        # per launch = one timestep's row pull: every recurrent and LGN entry's bitmap index
-        # (4 bytes), the row pointers, each active entry's batch mask, weight and type (9
-        # bytes), and the currents written (rec and LGN halves)
-        active = (e_rec + e_lgn) / max(T, 1)
-        alg_bytes = ((S + tb.lgn.n_syn) * 4 + 2 * (N + 1) * 4 + active * 9 + 2 * nb * B * N * 4)
+        # per launch = one timestep's row pull: every recurrent entry's bitmap index, and the
+        # LGN ones when their currents are not computed ahead (4 bytes), the row pointers, each
+        # active entry's batch mask, weight and type (9 bytes), and the currents written
+        active = (e_rec + e_in) / max(T, 1)
+        tables = 1 if lgn_ahead else 2
+        alg_bytes = ((S + (0 if lgn_ahead else tb.lgn.n_syn)) * 4 + tables * (N + 1) * 4 + active * 9
+                     + tables * nb * B * N * 4)
         unit_desc = "bytes per forward timestep (deterministic row pull)"
     avg_ms = tot_ms / max(launches, 1)
     achieved = alg_bytes / (avg_ms / 1000.0) / 1e9 if avg_ms > 0 else 0.0

@@ -269,9 +269,11 @@ int glif_sample_poisson(float lam, float exp_neg_lam, int64_t n, uint64_t seed, 
 /* ------------------------------------------------------------ profiling ------
  * No reference counterpart (the reference times whole steps with time(),
  * callbacks.py:1442-1449).  Kernel classes: 0 push, 1 step, 2 adj, 3 bwd_rec,
- * 4 bwd_lgn, 5 bwd_bkg, 6 syn_fwd, 7 syn_bwd.  In the cell's event mode "step" is the
- * one launch per tick that runs the step beside that tick's pushes and "push" only the
- * push of tick 0; in deterministic mode "push" is the row pull.  "adj" includes the
+ * 4 bwd_lgn, 5 bwd_bkg, 6 syn_fwd, 7 syn_bwd, 8 lgn.  In the cell's event mode "step" is
+ * the one launch per tick that runs the step beside that tick's pushes and "push" only the
+ * push of tick 0; in deterministic mode "push" is the row pull where it runs as a launch
+ * of its own.  "lgn" is the pass that computes 64 ticks of LGN currents ahead of the loop
+ * (batch sizes up to 8).  "adj" includes the
  * previous window's weight-gradient passes and the rest of its dz walk, which share its launch.
  * While bit k of `mask` is set, every launch of class k (every `every`-th, glif_prof_stride,
  * counted from glif_prof_enable; default 1) is bracketed by two HIP events on its stream.

@@ -78,7 +78,7 @@ SIGNATURES = {
     "glif_prof_name": (C.c_char_p, [i32]),
 }
 
-PROF_KINDS = ("push", "step", "adj", "bwd_rec", "bwd_lgn", "bwd_bkg", "syn_fwd", "syn_bwd")
+PROF_KINDS = ("push", "step", "adj", "bwd_rec", "bwd_lgn", "bwd_bkg", "syn_fwd", "syn_bwd", "lgn")
 
 
 class GlifError(RuntimeError):

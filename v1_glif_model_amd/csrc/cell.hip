@@ -55,7 +55,7 @@ struct CellWs {
     float *I2;          // [2][nb][B][N]   LGN currents (deterministic chunk pull)
     float *IL;          // [kLgnRing][nb][B][N]  LGN currents computed ahead of the loop (B <= 8):
                         // the event push adds onto them, the deterministic step adds them
-    uint8_t *lgnT;      // [ceil(T / 64)][n_lgn][64]  LGN batch masks by input, then tick
+    uint64_t *lgnT;     // [ceil(T / 64)][n_lgn][B]  LGN tick masks (bit k: tick 64 seg + k)
     float *vsave;       // [T][B][N]
     int64_t *lgn_off;   // [T + 1]           per-step LGN (column, batch-mask) lists
     int32_t *lgn_pre;   // [T * n_lgn]
@@ -122,7 +122,7 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.I2 = cv.take<float>(2 * BN * c->nb);  // deterministic pull beside the step: two halves
     if (lgn_ahead(c, B)) {
         w.IL = cv.take<float>(static_cast<size_t>(kLgnRing) * BN * c->nb);
-        w.lgnT = cv.take<uint8_t>(static_cast<size_t>((T + kLgnSeg - 1) / kLgnSeg) * nl * kLgnSeg);
+        w.lgnT = cv.take<uint64_t>(static_cast<size_t>((T + kLgnSeg - 1) / kLgnSeg) * nl * B);
     }
     w.vsave = cv.take<float>(static_cast<size_t>(T) * BN);
     w.lgn_off = cv.take<int64_t>(T + 1);
@@ -226,34 +226,23 @@ __global__ void __launch_bounds__(kBlock)
     if ((threadIdx.x & (kWave - 1)) == 0) lbits[t * Wl + (pre >> 6)] = bits;
 }
 
-// lgnT[(seg * n_in + pre) * 64 + k] = batch mask of the LGN inputs x[64 seg + k][b][pre] > 0
-// (0 past T).  Workgroup: one segment x 64 inputs; the masks are composed with reads
-// coalesced over the inputs and leave, through an LDS transpose, as contiguous 64-byte rows.
+// lgnT[(seg * n_in + pre) * B + b] = tick mask of input pre in batch entry b over segment seg:
+// bit k = x[64 seg + k][b][pre] > 0 (0 past T).  Thread per (b, pre), reads coalesced over
+// the inputs.
 __global__ void __launch_bounds__(kBlock)
-    k_lgn_tmask(const uint8_t *__restrict__ x, int T, int B, int32_t n_in, uint8_t *__restrict__ lgnT) {
-    __shared__ uint32_t tile[64][17];  // [input][4 ticks per word], padded against bank conflicts
+    k_lgn_tmask(const uint8_t *__restrict__ x, int T, int B, int32_t n_in, uint64_t *__restrict__ lgnT) {
     const int seg = blockIdx.y;
-    const int32_t pre0 = blockIdx.x * 64;
-    const int lane = threadIdx.x & 63, wq = threadIdx.x >> 6;  // wq: 4 waves
-    const int32_t pre = pre0 + lane;
-    for (int kw = wq; kw < 16; kw += 4) {
-        uint32_t word = 0;
-        for (int j = 0; j < 4; ++j) {
-            const int t = seg * kLgnSeg + 4 * kw + j;
-            uint32_t m = 0;
-            if (pre < n_in && t < T)
-                for (int b = 0; b < B; ++b)
-                    if (x[(static_cast<int64_t>(t) * B + b) * n_in + pre] > 0) m |= 1u << b;
-            word |= m << (8 * j);
-        }
-        tile[lane][kw] = word;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(B) * n_in) return;
+    const int b = static_cast<int>(i / n_in);
+    const int32_t pre = static_cast<int32_t>(i - static_cast<int64_t>(b) * n_in);
+    const int k_end = min(kLgnSeg, T - seg * kLgnSeg);
+    uint64_t m = 0;
+    for (int k = 0; k < k_end; ++k) {
+        const int64_t t = static_cast<int64_t>(seg) * kLgnSeg + k;
+        if (x[(t * B + b) * n_in + pre] > 0) m |= 1ull << k;
     }
-    __syncthreads();
-    uint32_t *out = reinterpret_cast<uint32_t *>(lgnT + (static_cast<int64_t>(seg) * n_in + pre0) * kLgnSeg);
-    for (int i = threadIdx.x; i < 64 * 16; i += blockDim.x) {
-        const int p = i >> 4, kw = i & 15;
-        if (pre0 + p < n_in) out[i] = tile[p][kw];
-    }
+    lgnT[(static_cast<int64_t>(seg) * n_in + pre) * B + b] = m;
 }
 
 struct LgnRowArgs {
@@ -262,14 +251,14 @@ struct LgnRowArgs {
     const uint32_t *pd;   // pre | (delay - 1) << 24,
     const uint8_t *sid;   // synapse type,
     const float *w;       // weight, in ascending (column, synapse id) order per row
-    const uint8_t *lgnT;  // tick-major batch masks (k_lgn_tmask)
+    const uint64_t *lgnT; // tick masks per (input, batch entry) (k_lgn_tmask)
     const float *basis;   // [n_types][nb]
     float *ring;          // kLgnRing slots of [nb][B][N]
 };
 
-// One wave per post, lane k = tick 64 seg + k: the row's entries are wave-uniform, each
-// lane tests its tick's batch mask of the entry's input (one coalesced 64-byte load per
-// entry) and adds w * basis[type][r] into its (b, r) accumulators in entry order from +0
+// One wave per post, lane k = tick 64 seg + k: the row's entries are wave-uniform, and the
+// 64-tick mask of the entry's input in batch entry b selects the lanes that add
+// w * basis[type][r] into their (b, r) accumulators, in entry order from +0
 // -- per (tick, b, post, r) the reference's order over the LGN events, the same sum the
 // deterministic row pull forms.  Zero products are skipped (adding +/-0 to a sum started
 // at +0 never changes it), so only the receptors the type's basis feeds are visited.  The
@@ -301,50 +290,47 @@ __global__ void __launch_bounds__(kLgnPosts * kWave) k_lgn_rows(LgnRowArgs a) {
 #pragma unroll
         for (int q = 0; q < NB; ++q) acc[b][q] = 0.0f;
     if (n < a.N) {
-        const uint8_t *mt = a.lgnT + static_cast<int64_t>(a.seg) * a.n_in * kLgnSeg + lane;
+        const uint64_t *tm = a.lgnT + static_cast<int64_t>(a.seg) * a.n_in * BB;
         const int32_t j0 = a.row[n], j1 = a.row[n + 1];
         // Up to 64 entries at a time: lane l loads entry jb + l (input, type, weight; three
-        // coalesced loads, indices clamped to the row's last entry), and the walk reads them
-        // back with lane reads.  The batch masks of 8 entries are loaded together, the next 8
-        // before this 8 are processed.
+        // coalesced loads, indices clamped to the row's last entry), forms its products
+        // w * basis[type][r] and the receptors its type feeds; the walk reads them back with
+        // lane reads.  Per entry the BB tick masks of its input are scalar loads (4 entries'
+        // at a time), and each mask is the lane mask of that batch entry's adds.
         for (int32_t jb = j0; jb < j1; jb += kWave) {
             const int cnt = min(j1 - jb, kWave);
             const int32_t jl = min(jb + lane, j1 - 1);
             const int pre_l = static_cast<int>(a.pd[jl] & kLow24);
             const int sid_l = a.sid[jl];
             const float w_l = a.w[jl];
-            // entry jb + l's products w * basis[type][r] and the receptors its type feeds
             const int nz_l = static_cast<int>(nz_lds[sid_l]);
             int v_l[NB];
 #pragma unroll
             for (int q = 0; q < NB; ++q) v_l[q] = __float_as_int(w_l * basis_lds[sid_l * NB + q]);
-            uint32_t m[8];
-            auto fetch = [&](int ub) {
+            for (int ub = 0; ub < cnt; ub += 4) {
+                uint64_t M[4][BB];
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    m[u] = mt[static_cast<int64_t>(__builtin_amdgcn_readlane(pre_l, ub + u)) * kLgnSeg];
-            };
-            fetch(0);
-            for (int ub = 0; ub < cnt; ub += 8) {
-                uint32_t mc[8];
+                for (int u = 0; u < 4; ++u) {
+                    const int pre = __builtin_amdgcn_readlane(pre_l, min(ub + u, kWave - 1));
 #pragma unroll
-                for (int u = 0; u < 8; ++u) mc[u] = m[u];
-                if (ub + 8 < cnt) fetch(ub + 8);
+                    for (int b = 0; b < BB; ++b) M[u][b] = tm[static_cast<int64_t>(pre) * BB + b];
+                }
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
+                for (int u = 0; u < 4; ++u) {
                     if (ub + u >= cnt) break;
-                    if (__ballot(mc[u] != 0u) == 0ull) continue;
-                    const uint32_t nz = static_cast<uint32_t>(__builtin_amdgcn_readlane(nz_l, ub + u));
-                    bool hit[BB];
+                    uint64_t any = 0;
 #pragma unroll
-                    for (int b = 0; b < BB; ++b) hit[b] = (mc[u] >> b) & 1u;
+                    for (int b = 0; b < BB; ++b) any |= M[u][b];
+                    if (any == 0ull) continue;
+                    const uint32_t nz = static_cast<uint32_t>(__builtin_amdgcn_readlane(nz_l, ub + u));
 #pragma unroll
                     for (int q = 0; q < NB; ++q) {
                         if (!((nz >> q) & 1u)) continue;
                         const float v = __int_as_float(__builtin_amdgcn_readlane(v_l[q], ub + u));
 #pragma unroll
                         for (int b = 0; b < BB; ++b)
-                            if (hit[b]) acc[b][q] = acc[b][q] + v;
+                            if (M[u][b] != 0ull && __builtin_amdgcn_inverse_ballot_w64(M[u][b]))
+                                acc[b][q] = acc[b][q] + v;
                     }
                 }
             }
@@ -1634,8 +1620,8 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         return rc;
     const int nseg = (T + kLgnSeg - 1) / kLgnSeg;
     if (ahead) {
-        hipLaunchKernelGGL(k_lgn_tmask, dim3(ceil_div(tl->n_cols, 64), nseg), dim3(kBlock), 0, s, lgn, T, B,
-                           static_cast<int32_t>(tl->n_cols), w.lgnT);
+        hipLaunchKernelGGL(k_lgn_tmask, dim3(ceil_div(static_cast<int64_t>(B) * tl->n_cols, kBlock), nseg),
+                           dim3(kBlock), 0, s, lgn, T, B, static_cast<int32_t>(tl->n_cols), w.lgnT);
         GLIF_HIP(hipGetLastError());
     }
     LgnRowArgs la{};
@@ -1833,7 +1819,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         sa.bkg_x = bkg + static_cast<int64_t>(t) * B * tb->n_cols;
         if (ahead && t % kLgnSeg == 0) {
             la.seg = t / kLgnSeg;
-            ProfScope p(kProfPush, s, true);
+            ProfScope p(kProfLgn, s, true);
             launch_lgn_rows(la, s);
         }
         if (event) {

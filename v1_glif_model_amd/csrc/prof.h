@@ -15,6 +15,7 @@ enum ProfKind {
     kProfBwdBkg,
     kProfSynFwd,
     kProfSynBwd,
+    kProfLgn,
     kProfKinds
 };
 

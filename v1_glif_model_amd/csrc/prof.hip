@@ -38,7 +38,7 @@ hipEvent_t get_event() {
 }  // namespace
 
 const char *const kProfNames[kProfKinds] = {"push", "step", "adj", "bwd_rec", "bwd_lgn", "bwd_bkg",
-                                            "syn_fwd", "syn_bwd"};
+                                            "syn_fwd", "syn_bwd", "lgn"};
 
 namespace {
 thread_local hipEvent_t t_pend_a = nullptr, t_pend_b = nullptr;  // a one-launch scope's pair
