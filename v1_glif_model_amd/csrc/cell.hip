@@ -1,10 +1,10 @@
 // The GLIF_3 cell over T steps (V1Column.call, models.py:1059-1135) and its BPTT.
 //
 // Forward, per step t (one stream, no host round trip):
-//   LGN (B <= 8): k_lgn_rows computes the LGN currents of 64 ticks at a time, per post
-//                 row in the reference's order, into a ring of current slots ahead of
-//                 the ticks that read them (with more batch entries, or the per-type
-//                 push, the LGN events are pushed or pulled per tick as below);
+//   LGN (B <= 8; event mode from B = 3 and without per-type slots): k_lgn_rows computes
+//                 the LGN currents of 64 ticks at a time, per post row in the reference's
+//                 order, into a ring of current slots ahead of the ticks that read them
+//                 (otherwise the LGN events are pushed or pulled per tick as below);
 //   event mode:   k_push(t)   the spike words of steps t-1..t-D (set bits = columns of
 //                             the recurrent table), and without the LGN ring the step's
 //                             LGN (column, batch-mask) list, are streamed through the
@@ -90,7 +90,8 @@ struct CellWs {
 constexpr int kLgnSeg = 64;
 constexpr int kLgnRing = kLgnSeg + 2;
 constexpr int kLgnPosts = 8;     // posts (waves) per k_lgn_rows workgroup
-constexpr int kLgnMaxBatch = 8;  // the tick-major masks hold one byte per (input, tick)
+constexpr int kLgnMaxBatch = 8;      // batch accumulators per lane of k_lgn_rows
+constexpr int kLgnEventMinBatch = 3; // event mode computes LGN ahead from this batch size up
 
 // Whether this cell computes its LGN currents ahead of the loop at batch size B.
 static bool lgn_ahead(const Cell *c, int B) { return B <= kLgnMaxBatch && c->lgn->n_cols > 0; }
@@ -585,6 +586,7 @@ __device__ inline void step_inputs(const StepArgs &a, const float *basis_lds, in
 #pragma unroll
             for (int q = 0; q < nb; ++q) Irl[q] = Irl[q] + x * bs[q];
         }
+
     } else {
         // the pushed (event) or pulled (deterministic) rec + LGN currents
         for (int q = 0; q < nb; ++q) {
@@ -1610,9 +1612,14 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     int rc;
     // event push into per-type slots ([gk][B][N] per tick) or receptor currents ([nb][B][N])
     const bool typed = event && c->push_typed;
-    // LGN currents computed ahead of the loop, segment by segment, into the LGN ring (the
-    // per-type push keeps pushing its LGN events into the type slots)
-    const bool ahead = lgn_ahead(c, B) && !typed;
+    // LGN currents computed ahead of the loop, segment by segment, into the LGN ring: in event
+    // mode the ring's slots are the current buffer the push adds to, in deterministic mode the
+    // step adds them to the pulled recurrent currents.  Event mode keeps pushing the LGN
+    // events where that was measured cheaper: below kLgnEventMinBatch batch entries (config 3
+    // at B = 1: 16.96 against 15.88 ms per rollout) and with per-type slots, whose single LGN
+    // atomic per event the launch hides (class-pair types: 61.2 against 59.8 ms per step)
+    const bool ahead = lgn_ahead(c, B) && (!event || (!typed && B >= kLgnEventMinBatch));
+    const bool ring_is_I = event && ahead;
 
     // input lists (LGN push in the forward, LGN / background dW in the backward)
     if (event && !ahead &&
@@ -1658,7 +1665,8 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
                        event ? nullptr : w.abits);
     GLIF_HIP(hipGetLastError());
     const int slots = typed ? c->g_rows : c->nb;
-    if (event && !ahead && (rc = launch_fill_u32(w.I, 0u, 2 * static_cast<size_t>(B) * c->N * slots, s))) return rc;
+    if (event && !ring_is_I && (rc = launch_fill_u32(w.I, 0u, 2 * static_cast<size_t>(B) * c->N * slots, s)))
+        return rc;
     const int64_t BNs = static_cast<int64_t>(B) * c->N;
     hipLaunchKernelGGL(k_state_layout, dim3(ceil_div(BNs, kBlock)), dim3(kBlock), 0, s, st->psc_rise, st->psc,
                        st->asc, w.R, w.P, w.A, BNs, c->nb, 1);
@@ -1707,7 +1715,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     sa.basis = tr->basis;
     sa.gk = typed ? c->g_rows : 0;
     sa.gtype = c->g_type;
-    sa.keep_I = event && ahead;
+    sa.keep_I = ring_is_I;
 
     PushArgs pa{};
     pa.D = c->D;
@@ -1801,7 +1809,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     // With the LGN ring, tick t's currents start in ring slot t % kLgnRing (event mode: the
     // push adds onto them; deterministic mode: the step adds them to the pulled ones).
     auto ring_slot = [&](int t) { return w.IL + static_cast<size_t>(t % kLgnRing) * BNs * c->nb; };
-    auto cur = [&](int t) { return event && ahead ? ring_slot(t) : Ih[t & 1]; };
+    auto cur = [&](int t) { return ring_is_I ? ring_slot(t) : Ih[t & 1]; };
     auto lgn_cur = [&](int t) { return ahead ? ring_slot(t) : I2h[t & 1]; };
     const int pull_fused = event ? 0 : fused_pull_blocks(pl, c->nb);
     const int fused_step_blocks = static_cast<int>(ceil_div(static_cast<int64_t>(B) * c->Np, kPullBlock));
