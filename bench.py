@@ -403,7 +403,9 @@ def main():
     def step():
         # every batch starts from the zero state (one multi-tensor fill)
         torch._foreach_zero_(zero_each_step)
-        cell.refresh_weights(force=True)
+        # the weight copies of the tables the last update changed (the optimizer bumps its
+        # variables' versions; the background weights are not trained here)
+        cell.refresh_weights()
         fwd_ev[0].record()
         cell.rollout(lgn, bkg, state=state, record_z=False, record_v=False, spike_count=spike_count,
                      ws=ws)

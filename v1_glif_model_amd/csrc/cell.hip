@@ -2062,8 +2062,10 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         launch_adj(aa, c->nb, s, &prev, false);
     }
     GLIF_HIP(hipGetLastError());
-    if (dw_rec && (rc = launch_gather_f32(dw_rec, w.dw_rec, gs ? tr->order_inv : tr->ph_inv, tr->n_syn, s))) return rc;
-    if (dw_lgn && (rc = launch_gather_f32(dw_lgn, w.dw_lgn, tl->order_inv, tl->n_syn, s))) return rc;
+    if (dw_rec && (rc = gs ? launch_perm_gather(dw_rec, w.dw_rec, tr->order_inv, tr->pinv, tr->n_syn, s)
+                           : launch_gather_f32(dw_rec, w.dw_rec, tr->ph_inv, tr->n_syn, s)))
+        return rc;
+    if (dw_lgn && (rc = launch_perm_gather(dw_lgn, w.dw_lgn, tl->order_inv, tl->pinv, tl->n_syn, s))) return rc;
     if (dw_bkg && (rc = launch_gather_f32(dw_bkg, w.dw_bkg, tb->order_inv, tb->n_syn, s))) return rc;
     return GLIF_OK;
 }

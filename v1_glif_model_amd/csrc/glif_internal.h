@@ -58,6 +58,23 @@ struct CompactRows {
 // Column-grouped ("CSC", the reference's pre_ind_table) and post-grouped ("CSR")
 // copies of the same synapses.  Index k runs over the column-grouped order,
 // j over the post-grouped order.
+// Two-pass plan of a large permutation gather dst[k] = src[P[k]] whose indices are far
+// apart (a CSR <-> CSC reordering).  Destinations form superblocks of 64K, sources chunks of
+// 64K.  Pass 1 (k_perm_runs) copies each chunk's sources into the superblocks they go to: one
+// workgroup per (chunk, superblock) run, the run written contiguously, the chunk's 256 KB read
+// from cache.  Pass 2 (k_perm_local) places every destination from its superblock's 256 KB of
+// staging.  Both passes stream their offsets and stay inside 256 KB windows, where one gather
+// over the whole array misses the cache on nearly every element.
+constexpr int kPermShift = 16;  // superblock / chunk size 1 << 16
+constexpr int64_t kPermMinSyn = int64_t(1) << 20;  // tables from this size get the plans
+struct PermPlan {
+    int32_t n_runs = 0;        // workgroups of pass 1 (XCD-aware order, padded with empty runs)
+    int4 *runs = nullptr;      // {first staging position, length, first source of the chunk, 0}
+    uint16_t *off1 = nullptr;  // [n] per staging position: source - first source of its chunk
+    uint16_t *off2 = nullptr;  // [n] per destination: staging position - superblock start
+    float *mid = nullptr;      // [n] staging (the plan's own: gathers with one plan do not overlap)
+};
+
 struct Table {
     int64_t n_syn = 0;
     int32_t n_post = 0;
@@ -118,6 +135,10 @@ struct Table {
     // Each is built only when no post receives more than three quarters of the types.  The
     // type-major copies above stay as they are.
     CompactRows cg, og;
+    // two-pass plans (tables of at least kPermMinSyn synapses): the column-grouped weight copy
+    // (P = order) and weight gradients from the column-grouped order back to the reference
+    // order (P = order_inv)
+    PermPlan pcol, pinv;
 };
 
 // Give a table a cell's compact G rows (Table::cg; rank: [n_syn] in column-grouped order, each
@@ -184,6 +205,9 @@ struct Carver {
 // ---- launch helpers (defined in the .hip files) ----------------------------
 int launch_fill_u32(void *p, uint32_t value, size_t n, hipStream_t s);
 int launch_gather_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s);
+// dst[k] = src[idx[k]] through the plan when it is built, else one gather
+int launch_perm_gather(float *dst, const float *src, const int32_t *idx, const PermPlan &plan, int64_t n,
+                       hipStream_t s);
 
 inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
 

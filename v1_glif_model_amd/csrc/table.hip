@@ -38,6 +38,29 @@ __global__ void k_gather_f32(float *__restrict__ dst, const float *__restrict__ 
     for (; i < n; i += stride) dst[i] = src[idx[i]];
 }
 
+// Pass 1 of a permutation plan: workgroup = one (chunk, superblock) run, staged contiguously.
+__global__ void __launch_bounds__(kBlock)
+    k_perm_runs(const float *__restrict__ src, float *__restrict__ mid, const int4 *__restrict__ runs,
+                const uint16_t *__restrict__ off1) {
+    const int4 r = runs[blockIdx.x];
+    for (int i = threadIdx.x; i < r.y; i += blockDim.x) {
+        const int32_t m = r.x + i;
+        mid[m] = src[static_cast<int64_t>(r.z) + off1[m]];
+    }
+}
+
+// Pass 2: dst[k] from the staging of k's superblock.  Workgroups go to the 8 XCDs round robin
+// (blockIdx % 8); XCD x takes the x-th eighth of the destinations, so each superblock's
+// staging is read through one L2.
+__global__ void __launch_bounds__(kBlock)
+    k_perm_local(const float *__restrict__ mid, float *__restrict__ dst, const uint16_t *__restrict__ off2,
+                 int64_t n) {
+    const int64_t per = gridDim.x / 8;
+    const int64_t lb = static_cast<int64_t>(blockIdx.x % 8) * per + blockIdx.x / 8;
+    const int64_t k = lb * blockDim.x + threadIdx.x;
+    if (k < n) dst[k] = mid[((k >> kPermShift) << kPermShift) + off2[k]];
+}
+
 __global__ void k_gather_pair_w(uint2 *__restrict__ dst, const float *__restrict__ src,
                                 const int32_t *__restrict__ idx, int64_t n) {
     int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -69,6 +92,18 @@ int launch_fill_u32(void *p, uint32_t value, size_t n, hipStream_t s) {
 int launch_gather_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s) {
     if (n == 0) return GLIF_OK;
     hipLaunchKernelGGL(k_gather_f32, dim3(grid_for(n)), dim3(kBlock), 0, s, dst, src, idx, n);
+    GLIF_HIP(hipGetLastError());
+    return GLIF_OK;
+}
+
+int launch_perm_gather(float *dst, const float *src, const int32_t *idx, const PermPlan &plan, int64_t n,
+                       hipStream_t s) {
+    if (!plan.runs) return launch_gather_f32(dst, src, idx, n, s);
+    hipLaunchKernelGGL(k_perm_runs, dim3(plan.n_runs), dim3(kBlock), 0, s, src, plan.mid, plan.runs, plan.off1);
+    GLIF_HIP(hipGetLastError());
+    const int64_t blocks = 8 * ((n + 8 * kBlock - 1) / (8 * kBlock));
+    hipLaunchKernelGGL(k_perm_local, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, plan.mid, dst, plan.off2,
+                       n);
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;
 }
@@ -144,8 +179,64 @@ static bool build_gs(int64_t n, int64_t n_cols, int64_t n_rows, const int64_t *r
     return true;
 }
 
+static void free_plan(PermPlan &pp) {
+    void *ptrs[] = {pp.runs, pp.off1, pp.off2, pp.mid};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    pp = PermPlan{};
+}
+
+// The two-pass plan of dst[k] = src[P[k]], k < n (P a permutation of 0..n-1).  Staging
+// position of source j: in the superblock of its destination, after the sources j' < j that go
+// there, so each (chunk, superblock) pair's sources are one contiguous run.
+static int build_perm_plan(PermPlan *pp, const int32_t *P, int64_t n) {
+    constexpr int64_t kSB = int64_t(1) << kPermShift;
+    const int64_t nsb = (n + kSB - 1) / kSB;
+    std::vector<int32_t> Pinv(n), mpos(n), fill(nsb, 0), snap(nsb);
+    for (int64_t k = 0; k < n; ++k) Pinv[P[k]] = static_cast<int32_t>(k);
+    std::vector<uint16_t> off1(n), off2(n);
+    std::vector<int4> by_xcd[8];
+    for (int64_t c = 0; c * kSB < n; ++c) {
+        std::copy(fill.begin(), fill.end(), snap.begin());
+        const int64_t j1 = std::min(n, (c + 1) * kSB);
+        for (int64_t j = c * kSB; j < j1; ++j) {
+            const int64_t sb = Pinv[j] >> kPermShift;
+            const int64_t m = sb * kSB + fill[sb]++;
+            mpos[j] = static_cast<int32_t>(m);
+            off1[m] = static_cast<uint16_t>(j - c * kSB);
+        }
+        for (int64_t sb = 0; sb < nsb; ++sb)
+            if (fill[sb] > snap[sb])
+                by_xcd[c % 8].push_back(make_int4(static_cast<int32_t>(sb * kSB + snap[sb]), fill[sb] - snap[sb],
+                                                  static_cast<int32_t>(c * kSB), 0));
+    }
+    for (int64_t k = 0; k < n; ++k) off2[k] = static_cast<uint16_t>(mpos[P[k]] - ((k >> kPermShift) << kPermShift));
+    // block b runs on XCD b % 8: XCD x takes the runs of chunks x, x + 8, .., so a chunk's 256 KB
+    // of sources is read through one L2
+    size_t slots = 0;
+    for (auto &v : by_xcd) slots = std::max(slots, v.size());
+    std::vector<int4> runs(8 * slots, make_int4(0, 0, 0, 0));
+    for (int x = 0; x < 8; ++x)
+        for (size_t i = 0; i < by_xcd[x].size(); ++i) runs[i * 8 + x] = by_xcd[x][i];
+    int rc;
+    if ((rc = upload(&pp->runs, runs.data(), runs.size())) || (rc = upload(&pp->off1, off1.data(), off1.size())) ||
+        (rc = upload(&pp->off2, off2.data(), off2.size()))) {
+        free_plan(*pp);
+        return rc;
+    }
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&pp->mid), n * sizeof(float));
+    if (e != hipSuccess) {
+        free_plan(*pp);
+        return hip_fail(e, "hipMalloc(permutation staging)");
+    }
+    pp->n_runs = static_cast<int32_t>(runs.size());
+    return GLIF_OK;
+}
+
 static void free_table(Table *t) {
     if (!t) return;
+    free_plan(t->pcol);
+    free_plan(t->pinv);
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
                     t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
                     t->chunk_desc, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src,
@@ -484,6 +575,13 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         free_table(t);
         return rc;
     }
+    // two-pass plans of the two reorderings done every training step (config 2's recurrent
+    // table: 305 us each as one gather)
+    if (n_syn >= kPermMinSyn && ((rc = build_perm_plan(&t->pcol, order.data(), n_syn)) ||
+                                 (rc = build_perm_plan(&t->pinv, order_inv.data(), n_syn)))) {
+        free_table(t);
+        return rc;
+    }
     *out = reinterpret_cast<glif_table *>(t);
     return GLIF_OK;
 }
@@ -506,7 +604,7 @@ int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
     if (!tt || !w) return fail(GLIF_EINVAL, "NULL argument");
     Table *t = reinterpret_cast<Table *>(tt);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    int rc = launch_gather_f32(t->w_col, w, t->order, t->n_syn, s);
+    int rc = launch_perm_gather(t->w_col, w, t->order, t->pcol, t->n_syn, s);
     if (rc) return rc;
     // the type-phased and grouped copies from w_col (near-sequential reads)
     if (t->n_syn) {
