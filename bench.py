@@ -501,9 +501,13 @@ def main():
         if split:
             # the first part of the grouped dz walk: one 8-byte table entry per synapse of
             # its columns, their pointers, the dz rows of the window's steps, G read once
-            alg_bytes = (s_a * 8 + (cols_a + 1) * 4 + steps_per_launch * B * cols_a * 4 + N * nt * Rg * 4)
-            unit_desc = (f"bytes per backward window of {Wwin} timesteps (recurrent dz, the {cols_a} columns "
-                         f"of delays <= {max(0, 2 * Wwin - 3)})")
+            # + the window's recurrent and LGN dW behind it (per active synapse event: 4-byte
+            # entry, the dW read and written, one G element)
+            act_ev = (e_rec + e_lgn) / max(T, 1) * steps_per_launch
+            alg_bytes = (s_a * 8 + (cols_a + 1) * 4 + steps_per_launch * B * cols_a * 4 + N * nt * Rg * 4
+                         + act_ev * 16)
+            unit_desc = (f"bytes per backward window of {Wwin} timesteps (recurrent dz over the {cols_a} columns "
+                         f"of delays <= {max(0, 2 * Wwin - 3)}, and the window's dW)")
         else:
             # dz and the dW of the window's active events in one pass
             active = e_rec / max(T, 1) * steps_per_launch
@@ -513,15 +517,13 @@ def main():
     elif dominant == "adj":
         # per launch = one backward window: the adjoint's state stream per (b, n) and tick
         # (D dz values, saved voltage, refractory bit; gV, gP, gR read and written once per
-        # launch), its G rows written; the previous window's recurrent and LGN dW (per active
-        # synapse event: 4-byte entry, the dW read and written, one G element) and the rest of
-        # its dz walk (8-byte entries of the other columns, their pointers and dz rows)
+        # launch), its G rows written, and the rest of the previous window's dz walk (8-byte
+        # entries of the other columns, their pointers and dz rows)
         rows = cell.g_layout()[0]
-        act_ev = (e_rec + e_lgn) / max(T, 1) * Wwin   # the backward's dW covers both
         alg_bytes = (Wwin * B * N * (D * 4 + 4) + Wwin * B * words * 8 + 2 * B * N * (1 + 2 * nb) * 4
-                     + N * rows * Rg * 4 + act_ev * 16
+                     + N * rows * Rg * 4
                      + (S - s_a) * 8 + (n_cols - cols_a + 1) * 4 + Wwin * B * (n_cols - cols_a) * 4)
-        unit_desc = f"bytes per backward window of {Wwin} timesteps (adjoint + previous window's dW and dz rest)"
+        unit_desc = f"bytes per backward window of {Wwin} timesteps (adjoint + previous window's dz rest)"
     elif dominant == "step" and args.mode == "deterministic":
         # per launch = one tick: the row pull (every recurrent entry's bitmap index, and the
         # LGN ones when their currents are not computed ahead, 4 bytes; the row pointers; each
