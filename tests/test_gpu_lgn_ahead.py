@@ -1,7 +1,8 @@
 """GPU parity of the LGN currents computed ahead of the T loop.
 
 For batch sizes up to 8 the cell computes the LGN currents of 64 ticks at a time (k_lgn_rows)
-into a ring of 66 current slots, right before the first of those ticks; the deterministic step
+into a ring of 130 current slots, the first segment before the loop and each later one on the
+cell's side stream beside the previous segment's ticks; the deterministic step
 adds a slot to the pulled recurrent currents, the event push (from batch 3) adds the recurrent
 events onto it.  These tests run rollouts long enough to cross segment boundaries and wrap the
 ring (T = 64, 65 and 200: segments of 64, 1 and 8 ticks at the end), at batch sizes on both sides

@@ -84,17 +84,54 @@ struct CellWs {
 // atomics (event mode) or pulled row by row inside it (deterministic mode).  Each
 // segment's currents land in a ring of kLgnRing current slots [nb][B][N], which the
 // event push then adds the recurrent events to, or which the deterministic step adds to
-// the pulled recurrent currents.  Ring safety: the segment of ticks [64s, 64s + 64) is
-// computed right before tick 64s's launch and overwrites the slots of ticks up to
-// 64s - 3, whose last reader (the step of that tick) ran in launch 64s - 2 at the latest.
+// the pulled recurrent currents.  The pass of segment s + 1 runs on the cell's side stream
+// beside segment s's ticks: it is enqueued at tick 64 s after an event on the caller's
+// stream (all launches before tick 64 s), and tick 64 (s + 1)'s launch waits for it.  Ring
+// safety: it overwrites the slots of ticks 64 (s + 1) - 130 .. 64 s - 3, whose last reader
+// (the step of that tick) ran in launch 64 s - 2 at the latest.
 constexpr int kLgnSeg = 64;
-constexpr int kLgnRing = kLgnSeg + 2;
+constexpr int kLgnRing = 2 * kLgnSeg + 2;
 constexpr int kLgnPosts = 8;     // posts (waves) per k_lgn_rows workgroup
 constexpr int kLgnMaxBatch = 8;      // batch accumulators per lane of k_lgn_rows
 constexpr int kLgnEventMinBatch = 3; // event mode computes LGN ahead from this batch size up
 
 // Whether this cell computes its LGN currents ahead of the loop at batch size B.
 static bool lgn_ahead(const Cell *c, int B) { return B <= kLgnMaxBatch && c->lgn->n_cols > 0; }
+
+static void release_side(Cell *c) {
+    if (!c->side) return;
+    int cur = 0;
+    const bool restore = hipGetDevice(&cur) == hipSuccess && cur != c->side_dev;
+    if (restore) (void)hipSetDevice(c->side_dev);
+    (void)hipStreamDestroy(c->side);
+    for (hipEvent_t e : {c->ev_main, c->ev_seg[0], c->ev_seg[1]})
+        if (e) (void)hipEventDestroy(e);
+    if (restore) (void)hipSetDevice(cur);
+    c->side = nullptr;
+    c->ev_main = c->ev_seg[0] = c->ev_seg[1] = nullptr;
+    c->side_dev = -1;
+}
+
+// The cell's side stream on the current device (default priority) and its events; false
+// when they cannot be made (the LGN passes then run on the caller's stream).
+static bool ensure_side(Cell *c) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    if (c->side && c->side_dev == dev) return true;
+    release_side(c);
+    if (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess) {
+        c->side = nullptr;
+        return false;
+    }
+    c->side_dev = dev;
+    for (hipEvent_t *e : {&c->ev_main, &c->ev_seg[0], &c->ev_seg[1]})
+        if (hipEventCreateWithFlags(e, hipEventDisableTiming) != hipSuccess) {
+            *e = nullptr;
+            release_side(c);
+            return false;
+        }
+    return true;
+}
 
 // Backward window width (reverse ticks per table pass) and G row length.
 static int win_width(int B) { return 3 * B <= 16 ? 3 : 1; }
@@ -1595,6 +1632,7 @@ int glif_cell_create(const glif_cell_config *cfg, const float *decay, const floa
 void glif_cell_destroy(glif_cell *cc) {
     Cell *c = reinterpret_cast<Cell *>(cc);
     if (!c) return;
+    release_side(c);
     for (void *p : {static_cast<void *>(c->decay), static_cast<void *>(c->cf),
                     static_cast<void *>(c->asc_decay), static_cast<void *>(c->asc_amps),
                     static_cast<void *>(c->tref), static_cast<void *>(c->g_type)})
@@ -1641,6 +1679,15 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         (rc = build_batch_mask_lists(lgn, T, B, tl->n_cols, w.lgn_off, w.lgn_pre, w.lgn_mask, w.scratch, s)))
         return rc;
     const int nseg = (T + kLgnSeg - 1) / kLgnSeg;
+    // with more than one segment, each segment's LGN pass after the first runs on the cell's
+    // side stream beside the previous segment's ticks (held for the rest of this call)
+    std::unique_lock<std::mutex> side_lock(c->side_mu, std::defer_lock);
+    bool side = false;
+    if (ahead && nseg > 1) {
+        side_lock.lock();
+        side = ensure_side(c);
+        if (!side) side_lock.unlock();
+    }
     if (ahead) {
         hipLaunchKernelGGL(k_lgn_tmask, dim3(ceil_div(static_cast<int64_t>(B) * tl->n_cols, kBlock), nseg),
                            dim3(kBlock), 0, s, lgn, T, B, static_cast<int32_t>(tl->n_cols), w.lgnT);
@@ -1841,9 +1888,31 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
         sa.lgn_x = lgn + static_cast<int64_t>(t) * B * tl->n_cols;
         sa.bkg_x = bkg + static_cast<int64_t>(t) * B * tb->n_cols;
         if (ahead && t % kLgnSeg == 0) {
-            la.seg = t / kLgnSeg;
-            ProfScope p(kProfLgn, s, true);
-            launch_lgn_rows(la, s);
+            const int sg = t / kLgnSeg;
+            if (!side) {
+                la.seg = sg;
+                ProfScope p(kProfLgn, s, true);
+                launch_lgn_rows(la, s);
+            } else {
+                if (sg == 0) {
+                    la.seg = 0;
+                    ProfScope p(kProfLgn, s, true);
+                    launch_lgn_rows(la, s);
+                } else {
+                    GLIF_HIP(hipStreamWaitEvent(s, c->ev_seg[sg & 1], 0));
+                }
+                if (sg + 1 < nseg) {
+                    // segment sg + 1 on the side stream, after every launch enqueued so far
+                    GLIF_HIP(hipEventRecord(c->ev_main, s));
+                    GLIF_HIP(hipStreamWaitEvent(c->side, c->ev_main, 0));
+                    la.seg = sg + 1;
+                    {
+                        ProfScope p(kProfLgn, c->side, true);
+                        launch_lgn_rows(la, c->side);
+                    }
+                    GLIF_HIP(hipEventRecord(c->ev_seg[(sg + 1) & 1], c->side));
+                }
+            }
         }
         if (event) {
             PushArgs early = pa;

@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "../../include/glif.h"
@@ -176,6 +177,14 @@ struct Cell {
     // the step folding the slots through the basis, instead of one atomic per receptor
     bool basis_dense = false;
     bool push_typed = false;
+    // The LGN pass of segment s + 1 runs on a stream of the cell's own while the caller's
+    // stream runs segment s's ticks (created on first use, on that call's device; events
+    // order the two).  The mutex keeps concurrent forwards on one cell from interleaving their
+    // event records and waits.
+    int side_dev = -1;
+    hipStream_t side = nullptr;
+    hipEvent_t ev_main = nullptr, ev_seg[2] = {nullptr, nullptr};
+    std::mutex side_mu;
 };
 
 // Small per-cell constants passed by value to kernels.
