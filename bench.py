@@ -493,6 +493,10 @@ def main():
     else:
         cols_a = n_cols
     s_a = int(np.count_nonzero(tb.rec.col < cols_a))
+    # the window's dW passes run in the walk's launch when one G buffer is at most 32 MiB,
+    # else in the next adjoint's launch (libglif's glif_cell_backward)
+    g_rows = cell.g_layout()[0]
+    dw_walk = split and N * g_rows * Rg * 4 <= (32 << 20)
     windows = max(T - 2, 1) / Wwin
     if dominant == "bwd_rec":
         # per launch = one backward window of Wwin timesteps (the last window may be
@@ -503,11 +507,11 @@ def main():
             # its columns, their pointers, the dz rows of the window's steps, G read once
             # + the window's recurrent and LGN dW behind it (per active synapse event: 4-byte
             # entry, the dW read and written, one G element)
-            act_ev = (e_rec + e_lgn) / max(T, 1) * steps_per_launch
+            act_ev = (e_rec + e_lgn) / max(T, 1) * steps_per_launch if dw_walk else 0.0
             alg_bytes = (s_a * 8 + (cols_a + 1) * 4 + steps_per_launch * B * cols_a * 4 + N * nt * Rg * 4
                          + act_ev * 16)
             unit_desc = (f"bytes per backward window of {Wwin} timesteps (recurrent dz over the {cols_a} columns "
-                         f"of delays <= {max(0, 2 * Wwin - 3)}, and the window's dW)")
+                         f"of delays <= {max(0, 2 * Wwin - 3)}" + (", and the window's dW)" if dw_walk else ")"))
         else:
             # dz and the dW of the window's active events in one pass
             active = e_rec / max(T, 1) * steps_per_launch
@@ -519,11 +523,14 @@ def main():
         # (D dz values, saved voltage, refractory bit; gV, gP, gR read and written once per
         # launch), its G rows written, and the rest of the previous window's dz walk (8-byte
         # entries of the other columns, their pointers and dz rows)
-        rows = cell.g_layout()[0]
+        # (+ with a large G the previous window's dW: per active synapse event 4-byte entry, the
+        # dW read and written, one G element)
+        act_ev = 0.0 if dw_walk else (e_rec + e_lgn) / max(T, 1) * Wwin
         alg_bytes = (Wwin * B * N * (D * 4 + 4) + Wwin * B * words * 8 + 2 * B * N * (1 + 2 * nb) * 4
-                     + N * rows * Rg * 4
+                     + N * g_rows * Rg * 4 + act_ev * 16
                      + (S - s_a) * 8 + (n_cols - cols_a + 1) * 4 + Wwin * B * (n_cols - cols_a) * 4)
-        unit_desc = f"bytes per backward window of {Wwin} timesteps (adjoint + previous window's dz rest)"
+        unit_desc = (f"bytes per backward window of {Wwin} timesteps (adjoint + previous window's dz rest"
+                     + (")" if dw_walk else " and dW)"))
     elif dominant == "step" and args.mode == "deterministic":
         # per launch = one tick: the row pull (every recurrent entry's bitmap index, and the
         # LGN ones when their currents are not computed ahead, 4 bytes; the row pointers; each

@@ -1347,11 +1347,13 @@ __global__ void __launch_bounds__(kBlock) k_bwd_rec_gs_dw(GsArgs a, ActWin act, 
 }
 
 // The rest of window j - 1's dz walk (the columns of delays > 2 W - 3, which the next
-// window's adjoint does not read), run beside window j's adjoint.
+// window's adjoint does not read), run beside window j's adjoint, and with a large G window
+// j - 1's weight-gradient passes too (dw.rec_blocks / lgn_blocks 0: they ran beside the walk).
 struct WalkRest {
     GsArgs gb;
     ActWin act;
     int32_t walk_blocks;
+    WinDw dw;
 };
 
 template <int NB>
@@ -1364,6 +1366,8 @@ __global__ void __launch_bounds__(kBlock) k_adj_dw(AdjArgs a, int adj_blocks, Wa
     }
     bid -= p.walk_blocks;
     if (bid < adj_blocks) adj_body<NB>(a, bid);
+    else if (bid < adj_blocks + p.dw.rec_blocks) rec_dw_body(p.dw.da, p.dw.act, bid - adj_blocks);
+    else bwd_in_body<false>(p.dw.la, bid - adj_blocks - p.dw.rec_blocks, p.dw.lgn_blocks);
 }
 
 static void launch_bwd_in(const BwdInArgs &ia, int64_t max_units, hipStream_t s) {
@@ -1476,7 +1480,7 @@ static void launch_adj(const AdjArgs &aa, int nb, hipStream_t s, const WalkRest 
     size_t use = with_adj ? adj_stage_lds(k, aa.R, aa.tc) : 0;
     if (prev && prev->walk_blocks) use = std::max(use, sizeof(float) * (kBlock / kWave) * kGsStage);
     const int adj_blocks = with_adj ? ceil_div(k.N, kBlock / k.B) : 0;
-    const dim3 grid(adj_blocks + (prev ? prev->walk_blocks : 0));
+    const dim3 grid(adj_blocks + (prev ? prev->walk_blocks + prev->dw.rec_blocks + prev->dw.lgn_blocks : 0));
     if (grid.x == 0) return;
     switch (nb) {
 #define GLIF_ADJ(NB)                                                                                   \
@@ -2081,8 +2085,13 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     // window j's weight-gradient passes (recurrent, then LGN) behind it (k_bwd_rec_gs_dw), and
     // the rest of the walk in window j + 1's adjoint launch (k_adj_dw); windows alternate
     // between two G buffers so that launch reads one while the adjoint writes the other.
-    // dW in the walk's launch instead of the adjoint's: 53.4 against 53.7 ms per training step.
+    // dW in the walk's launch instead of the adjoint's: 53.4 against 53.7 ms per training step
+    // at config 2 (one G buffer 21 MB).  With a larger G the dW passes' gathers over it evict the
+    // slices the walk reads from the L2, and they run in window j + 1's adjoint launch instead
+    // (class-pair types, 46 MB: 39.4 against 37.7 ms of backward per step beside the walk; 121
+    // type-major rows, 511 MB: 108.4 against 103.3).
     const bool defer = gs && dw_rec;
+    const bool dw_with_walk = defer && g_elems * sizeof(float) <= (size_t(32) << 20);
     WalkRest prev{};
     bool have_prev = false;
     const int64_t n_groups = (tr->n_cols + kGsCols - 1) / kGsCols;
@@ -2112,7 +2121,7 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         la.s0 = s0;
         {
             ProfScope p(kProfBwdRec, s, true);
-            if (defer) {
+            if (dw_with_walk) {
                 GsArgs g1 = ga;
                 g1.g_hi = g_split;
                 WinDw dw{};
@@ -2135,6 +2144,14 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         }
         if (defer) {
             prev.act = act;
+            prev.dw = WinDw{};
+            if (!dw_with_walk) {
+                prev.dw.da = da;
+                prev.dw.act = act;
+                prev.dw.la = la;
+                prev.dw.rec_blocks = ceil_div(tr->n_cols, kBlock);
+                prev.dw.lgn_blocks = dw_lgn ? grid_subwaves(lgn_units, kWave) : 0;
+            }
             prev.gb = ga;
             prev.gb.g_lo = g_split;
             prev.walk_blocks = g_split < n_groups ? ceil_div((n_groups - g_split) * 4, kBlock) : 0;
@@ -2150,7 +2167,8 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
             launch_bwd_in(ka, bkg_units, s);
         }
     }
-    if (have_prev && prev.walk_blocks > 0) {  // the rest of the last window's dz walk
+    if (have_prev && prev.walk_blocks + prev.dw.rec_blocks + prev.dw.lgn_blocks > 0) {
+        // the rest of the last window's dz walk (and its dW passes where they follow the adjoint)
         ProfScope p(kProfAdj, s, true);
         launch_adj(aa, c->nb, s, &prev, false);
     }
