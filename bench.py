@@ -120,17 +120,23 @@ def load_traffic(name):
 
 
 class RateCalibrator:
-    """One global factor on all three weight populations of a cell, set by bisection in log
-    space on deterministic rollouts so that the mean firing rate meets a target (the
-    configurations fix the network's shape, not its rate; the factor is reported)."""
+    """One factor on a cell's weight populations, set by bisection in log space on deterministic
+    rollouts so that the mean firing rate meets a target (the configurations fix the network's
+    shape, not its rate; the factor is reported).  populations ("rec",) scales the recurrent
+    weights only, the role of the reference's recurrent_weight_scale (models.py:664), the LGN
+    and background weights staying as generated; ("rec", "lgn", "bkg") scales all three."""
 
-    def __init__(self, cell, lgn, bkg):
+    def __init__(self, cell, lgn, bkg, populations=("rec", "lgn", "bkg")):
         import torch
         self.cell, self.lgn, self.bkg = cell, lgn, bkg
-        self.ws = (cell.recurrent_weight_values, cell.input_weight_values, cell.bkg_input_weights)
+        every = {"rec": cell.recurrent_weight_values, "lgn": cell.input_weight_values,
+                 "bkg": cell.bkg_input_weights}
+        self.populations = tuple(populations)
+        self.ws = tuple(every[k] for k in self.populations)
         self.base = [w.detach().clone() for w in self.ws]
         B, N = lgn.shape[1], cell.tables.n_neurons
         self.sc = torch.zeros((B, N), dtype=torch.int32, device=cell.device)
+        self.floor_hz = None   # recurrent-only: the rate with the recurrent weights at zero
 
     def set_scale(self, f):
         import torch
@@ -149,11 +155,19 @@ class RateCalibrator:
         return float(self.sc.sum().item()) / self.sc.numel() / Tp * 1000.0
 
     def find_scale(self, target, Tp):   # the whole rollout: the rate ramps up from rest
+        """The factor that meets `target` Hz; with the recurrent weights alone, 0.0 when the
+        inputs by themselves already drive the network at or above it (the lowest reachable
+        rate is then floor_hz)."""
         import numpy as np
+        if self.populations == ("rec",):
+            if self.floor_hz is None:
+                self.floor_hz = self.rate_hz(0.0, Tp)
+            if self.floor_hz >= target:
+                return 0.0
         lo, hi = None, None
         f = 1.0
         r = self.rate_hz(f, Tp)
-        for _ in range(10):   # bracket
+        for _ in range(12):   # bracket
             if r < target:
                 lo = (f, r)
                 if hi is not None:
@@ -167,7 +181,7 @@ class RateCalibrator:
             r = self.rate_hz(f, Tp)
         if lo is None or hi is None:
             return f
-        for _ in range(7):   # bisect in log space
+        for _ in range(9):   # bisect in log space
             f = float(np.sqrt(lo[0] * hi[0]))
             r = self.rate_hz(f, Tp)
             if r < target:
@@ -178,10 +192,11 @@ class RateCalibrator:
 
 
 def sweep_rates(args):
-    """Config 4: forward throughput of the event push and the deterministic row pull
-    at several mean firing rates.  One global factor scales all three weight
-    populations; it is set per target rate by bisection in log space on short rollouts
-    (the achieved rate of the timed rollout is reported)."""
+    """Config 4: forward throughput of the event push and the deterministic row pull at
+    several mean firing rates.  One factor scales the recurrent weights only (the role of
+    the reference's recurrent_weight_scale, models.py:664; the LGN and background weights stay
+    as generated); it is set per target rate by bisection in log space on whole rollouts (the
+    achieved rate of the timed rollout is reported)."""
     import numpy as np
     import torch
     from v1_glif_model_amd import _lib
@@ -199,7 +214,7 @@ def sweep_rates(args):
     dev = cell.device
     lgn = torch.tensor(lgn_np, device=dev)
     bkg = torch.tensor(bkg_np, device=dev)
-    cal = RateCalibrator(cell, lgn, bkg)
+    cal = RateCalibrator(cell, lgn, bkg, populations=("rec",))
     sc = cal.sc
     set_scale = cal.set_scale
 
@@ -232,7 +247,8 @@ def sweep_rates(args):
         ev_ms, ev_rate, ev_k = timed("event")
         pl_ms, pl_rate, pl_k = timed("deterministic")
         events = ev_rate / 1000.0 * B * S   # recurrent synaptic events per step
-        rows.append({"target_hz": target, "weight_factor": round(f, 4), "rate_hz": round(ev_rate, 3),
+        rows.append({"target_hz": target, "recurrent_weight_factor": round(f, 5), "rate_hz": round(ev_rate, 3),
+                     "reachable": f > 0.0 or (cal.floor_hz or 0.0) <= target,
                      "event_ms_per_step": round(ev_ms, 4), "pull_ms_per_step": round(pl_ms, 4),
                      "event_kernel_us_per_step": ev_k, "pull_kernel_us_per_step": pl_k,
                      "rec_events_per_step": round(events),
@@ -251,8 +267,11 @@ def sweep_rates(args):
         "ms_per_step": min(best5["event_ms_per_step"], best5["pull_ms_per_step"]) if best5 else None,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"config 4: {N} GLIF_3 neurons, {S} recurrent synapses, B={B}, T={T}, "
-                               "modulated LGN, forward; event push vs deterministic row pull",
-                   "neurons": N, "recurrent_synapses": S, "batch": B, "seq_len": T},
+                               "modulated LGN, forward; recurrent weights scaled to each rate; event push vs "
+                               "deterministic row pull",
+                   "neurons": N, "recurrent_synapses": S, "batch": B, "seq_len": T,
+                   "rate_with_recurrent_weights_at_zero_hz": round(cal.floor_hz, 3) if cal.floor_hz is not None
+                   else None},
         "sweep": rows}))
 
 

@@ -82,7 +82,9 @@ int64_t glif_table_n_syn(const glif_table *t);
 int glif_table_pre_ind(const glif_table *t, const int32_t **order, const int32_t **row_splits);
 /* refresh_recurrent_weight_shadow (models.py:966-976): copy the trainable weight
  * vector w [n_syn] (device, reference order) into the table's column- and
- * row-grouped copies.  Must be called before use and after every weight update. */
+ * row-grouped copies.  Must be called before use and after every weight update.  It
+ * writes the table's weight copies (and stages through a buffer of the table's), so calls
+ * on one table must not overlap, and no call that reads the table may run beside one. */
 int glif_table_set_weights(glif_table *t, const float *w, void *stream);
 
 /* --------------------------------------- synaptic-current op (fwd, grad) ----
@@ -168,12 +170,43 @@ int glif_cell_forward(glif_cell *c, int32_t B, int32_t T, int32_t mode, const ui
                       int32_t *spike_count, void *ws, size_t ws_bytes, void *stream);
 
 /* BPTT through the last glif_cell_forward on `ws` (zero initial state assumed for
- * the adjoint; gradients do not flow into the initial state).
+ * the adjoint; gradients do not flow into the initial state).  All its scratch, the
+ * reordering of the weight gradients included, lives in `ws`, so backwards on one cell with
+ * workspaces of their own may run on different streams at once.
  * device in (each may be NULL): gz [T][B][N] dL/dz, gz_neuron [N] dL/dz broadcast
  * over b and the ticks of the trimming window, gv [T][B][N] dL/dv.  out (each may be NULL): dw_rec, dw_lgn, dw_bkg,
  * gradients of the three weight vectors in reference order (overwritten). */
 int glif_cell_backward(glif_cell *c, int32_t B, int32_t T, const float *gz,
                        const float *gz_neuron, const float *gv, float *dw_rec, float *dw_lgn,
+                       float *dw_bkg, void *ws, size_t ws_bytes, void *stream);
+
+/* ----------------------------------------------- one step's backward --------
+ * The gradient of one V1Column.call (models.py:1059-1135) for callers that keep the Keras
+ * RNN (models.py:1317-1322) and let a tape differentiate it step by step (the reference's
+ * GradientTape over the RNN, multi_training.py:368-372, 485-493).  The step's forward is
+ * glif_cell_forward with T = 1 (its state in/out and its z, v outputs).
+ * Gradients of the state tuple (r and noise_step have none); every field may be NULL. */
+typedef struct {
+    float *z_buf;      /* [B][D*N] */
+    float *v;          /* [B][N] */
+    float *asc;        /* [B][N*2] */
+    float *psc_rise;   /* [B][N*nb] */
+    float *psc;        /* [B][N*nb] */
+} glif_state_grad;
+
+size_t glif_step_workspace(const glif_cell *c, int32_t B);
+/* device in: lgn [B][n_lgn] u8 and bkg [B][n_bkg] u8 (the step's inputs; needed for dw_lgn /
+ * dw_bkg), z_buf [B][D*N] the step's OLD spike buffer (needed for g_old->z_buf and dw_rec),
+ * v_new [B][N] the step's output voltage, r_new [B][N] int16 its new refractory counter;
+ * gz, gv [B][N] dL/dz and dL/dv of the step's outputs (nullable); g_new: dL/d(new state)
+ * (nullable, as its fields).  out: g_old, dL/d(old state) for each non-NULL field
+ * (overwritten); dw_rec, dw_lgn, dw_bkg [n_syn] this step's weight gradients in reference
+ * order (nullable, overwritten).  With the straight-through dampening of models.py:284-296
+ * (rd on the spike buffer, 1 - vgd on v), stop_gradient on the previous spikes and r, the
+ * surrogate masked where r_new > 0, and hard reset cutting the voltage path there. */
+int glif_step_backward(glif_cell *c, int32_t B, const uint8_t *lgn, const uint8_t *bkg, const float *z_buf,
+                       const float *v_new, const int16_t *r_new, const float *gz, const float *gv,
+                       const glif_state_grad *g_new, glif_state_grad *g_old, float *dw_rec, float *dw_lgn,
                        float *dw_bkg, void *ws, size_t ws_bytes, void *stream);
 
 /* Fused voltage regularization (VoltageRegularization, loss_functions.py:1047-1119):
@@ -205,8 +238,9 @@ int glif_cell_set_trim(glif_cell *c, int32_t pre_delay, int32_t post_delay);
 int glif_cell_g_layout(const glif_cell *c, int32_t *rows_per_post, int32_t *compact);
 /* Choose the layout (for timing the two against each other): compact 0 = type-major rows,
  * 1 = compact rows (GLIF_EINVAL when the cell has none).  The workspace size follows the
- * layout: query glif_cell_workspace again, and run glif_cell_backward only after a forward
- * made under the same layout. */
+ * layout: query glif_cell_workspace again.  What a backward reads of its forward sits at
+ * offsets that do not depend on the layout, so a backward after a switch is valid on a
+ * workspace large enough for the new layout (GLIF_ENOMEM otherwise). */
 int glif_cell_set_g_layout(glif_cell *c, int32_t compact);
 
 /* ----------------------------------------------------------------- losses -----

@@ -18,7 +18,13 @@ reference:
 
 Spikes are teacher-forced to a given train (the CPU oracle's) so the float64 graph
 follows the same trajectory as the float32 run it checks; the surrogate is still
-evaluated on this run's own voltage.
+evaluated on this run's own voltage (or on given voltages, ``psi_v``).
+
+The rollout may start from a given state and also return the gradients of that initial
+state (what the reference's tape gives for the RNN's initial state), and with
+``absolute=True`` every signed factor (weights, basis entries, loss gradients) is replaced by
+its absolute value, so each returned gradient is the sum of the absolute values of its terms:
+the scale fp32 rounding in any summation order is proportional to.
 """
 from __future__ import annotations
 
@@ -28,8 +34,8 @@ import torch
 
 class _SpikeForced(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, v_sc, z, pseudo_gauss, sigma, amp):
-        ctx.save_for_backward(v_sc)
+    def forward(ctx, v_sc, z, pseudo_gauss, sigma, amp, v_sc_psi=None):
+        ctx.save_for_backward(v_sc if v_sc_psi is None else v_sc_psi)
         ctx.p = (pseudo_gauss, sigma, amp)
         return z.clone()
 
@@ -41,7 +47,7 @@ class _SpikeForced(torch.autograd.Function):
             psi = torch.exp(-torch.square(v_sc) / (sigma * sigma)) * amp      # models.py:17-21
         else:
             psi = amp * torch.clamp(1.0 - torch.abs(v_sc), min=0.0)           # models.py:23-28
-        return dy * psi, None, None, None, None
+        return dy * psi, None, None, None, None, None
 
 
 def _st_dampen(x, d):
@@ -60,15 +66,22 @@ def _syn(z_src, table, w, basis, B, N, nb):
 
 
 def bptt(tb, lgn, bkg, z_forced, gz, gv, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.5,
-         pseudo_gauss=True, hard_reset=False, zbuf0=None):
+         pseudo_gauss=True, hard_reset=False, zbuf0=None, state0=None, state_grad=False, psi_v=None,
+         absolute=False):
     """Returns ({'rec','lgn','bkg'}: dL/dW float64 arrays, v [T,B,N]) for
     L = sum(z * gz) + sum(v * gv), from a zero state with the spike history zbuf0 [B, D*N]
-    (None: no spikes); the history's spikes are inputs (no gradient flows into them)."""
+    (None: no spikes), or from state0 (dict of the state tuple's arrays in the reference
+    layouts: zbuf, v, r, asc, psc_rise, psc).  The history's spikes are inputs; with
+    state_grad a third dict holds dL/d(initial state) for zbuf, v, asc, psc_rise, psc, in the
+    same layouts (the gradient that flows into the initial spike buffer included).  psi_v
+    [T,B,N]: voltages the surrogate is evaluated at (default: this run's); absolute: every
+    signed factor by its absolute value (the sum-of-absolute-terms scale)."""
     T, B = lgn.shape[:2]
     N, D, nb = tb.n_neurons, tb.max_delay, tb.n_basis
     f = lambda a: torch.tensor(np.asarray(a, dtype=np.float64))
-    W = {k: f(getattr(tb, k).weight).requires_grad_(True) for k in ("rec", "lgn", "bkg")}
-    basis = f(tb.basis)
+    fa = (lambda a: torch.tensor(np.abs(np.asarray(a, dtype=np.float64)))) if absolute else f
+    W = {k: fa(getattr(tb, k).weight).requires_grad_(True) for k in ("rec", "lgn", "bkg")}
+    basis = fa(tb.basis)
     decay, cf = f(tb.decay), f(tb.current_factor)
     ad, amp = f(tb.asc_decay), f(tb.asc_amps)
     tref = torch.tensor(tb.t_ref_steps.astype(np.int64))
@@ -77,6 +90,7 @@ def bptt(tb, lgn, bkg, z_forced, gz, gv, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.
     zf = torch.tensor(np.asarray(z_forced, dtype=np.float64))
     x_lgn = torch.tensor((np.asarray(lgn) > 0).astype(np.float64))
     x_bkg = torch.tensor(np.asarray(bkg).astype(np.float64))
+    vpsi = None if psi_v is None else torch.tensor(np.asarray(psi_v, dtype=np.float64)) - 1.0
 
     z_buf = torch.zeros((B, D * N), dtype=torch.float64)
     if zbuf0 is not None:
@@ -86,9 +100,20 @@ def bptt(tb, lgn, bkg, z_forced, gz, gv, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.
     asc = torch.zeros((B, N, 2), dtype=torch.float64)
     R = torch.zeros((B, N, nb), dtype=torch.float64)
     P = torch.zeros((B, N, nb), dtype=torch.float64)
+    if state0 is not None:
+        z_buf, v = f(state0["zbuf"]).reshape(B, D * N), f(state0["v"]).reshape(B, N)
+        r = torch.tensor(np.asarray(state0["r"]).astype(np.int64)).reshape(B, N)
+        asc = f(state0["asc"]).reshape(B, N, 2)
+        R, P = f(state0["psc_rise"]).reshape(B, N, nb), f(state0["psc"]).reshape(B, N, nb)
+    leaves = {}
+    if state_grad:
+        leaves = {"zbuf": z_buf.clone().requires_grad_(True), "v": v.clone().requires_grad_(True),
+                  "asc": asc.clone().requires_grad_(True), "psc_rise": R.clone().requires_grad_(True),
+                  "psc": P.clone().requires_grad_(True)}
+        z_buf, v, asc, R, P = (leaves[k] for k in ("zbuf", "v", "asc", "psc_rise", "psc"))
     loss = torch.zeros((), dtype=torch.float64)
     vs = []
-    gz_t, gv_t = torch.tensor(np.asarray(gz, np.float64)), torch.tensor(np.asarray(gv, np.float64))
+    gz_t, gv_t = fa(gz), fa(gv)
     for t in range(T):
         prev_z = z_buf[:, :N]
         rec_z_buf = _st_dampen(z_buf, 1.0 - rd)
@@ -104,11 +129,17 @@ def bptt(tb, lgn, bkg, z_forced, gz, gv, vgd=0.5, rd=0.5, gauss_std=0.5, damp=0.
         new_r = torch.clamp(r + prev_z.detach().long() * tref - 1, min=0)
         if hard_reset:
             new_v = torch.where(new_r > 0, torch.zeros_like(new_v), new_v)
-        z = _SpikeForced.apply(new_v - 1.0, zf[t], pseudo_gauss, gauss_std, damp)
+        z = _SpikeForced.apply(new_v - 1.0, zf[t], pseudo_gauss, gauss_std, damp,
+                               None if vpsi is None else vpsi[t])
         z = torch.where(new_r > 0, torch.zeros_like(z), z)
         z_buf = torch.cat([z, z_buf[:, :-N]], dim=1)
         loss = loss + (z * gz_t[t]).sum() + (new_v * gv_t[t]).sum()
         vs.append(new_v.detach())
         v, r, asc, R, P = new_v, new_r, new_asc, new_R, new_P
     loss.backward()
-    return {k: W[k].grad.numpy() for k in W}, torch.stack(vs).numpy()
+    dw = {k: W[k].grad.numpy() for k in W}
+    if not state_grad:
+        return dw, torch.stack(vs).numpy()
+    g0 = {k: (t.grad if t.grad is not None else torch.zeros_like(t)).reshape(B, -1).numpy()
+          for k, t in leaves.items()}
+    return dw, torch.stack(vs).numpy(), g0

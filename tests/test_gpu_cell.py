@@ -282,10 +282,12 @@ def test_call_steps_equal_rollout():
     for t in range(T):
         inp = torch.tensor(lgn[t], dtype=torch.float32, device="cuda")
         (z, v), state = cell.call(inp, state, bkg_counts=torch.tensor(bkg[t], device="cuda"))
-        np.testing.assert_array_equal(z.cpu().numpy(), zr[t].cpu().numpy())
-        np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), vr[t].cpu().numpy().view(np.uint32))
+        np.testing.assert_array_equal(z.detach().cpu().numpy(), zr[t].cpu().numpy())
+        np.testing.assert_array_equal(v.detach().cpu().numpy().view(np.uint32), vr[t].cpu().numpy().view(np.uint32))
     assert int(state[6][0].item()) == T
-    (z, v), st2 = cell.call(torch.tensor(lgn[0], dtype=torch.float32, device="cuda"), state)
+    with torch.no_grad():   # not recorded: plain tensors
+        (z, v), st2 = cell.call(torch.tensor(lgn[0], dtype=torch.float32, device="cuda"), state)
+    assert z.grad_fn is None and not z.requires_grad
     assert z.shape == (B, tn[1].n_neurons) and int(st2[6][0].item()) == T + 1
 
 

@@ -16,10 +16,14 @@ against the C oracle on identical seeded inputs.
   144 KB-LDS, 1024-lane chunk pull), event counts within the bar;
 * config 2's network with the reference's type structure (121 class-pair types, 4 receptors,
   5 Hz): compact G rows, deterministic forward bit-exact over 150 ms and BPTT within the bar;
-* config 4 (B = 32, per-batch sinusoidal LGN) at the rate sweep's 5 Hz and 50 Hz weight
-  factors: deterministic forward bit-exact over 500 ms, event counts within the bar (5 Hz;
-  at 50 Hz the agreement is reported), and a B = 32 BPTT at the 50 Hz factor (one-tick
-  windows, 32-float G rows) against the oracle.
+* config 4 (B = 32, per-batch sinusoidal LGN) with the recurrent weights alone scaled to the
+  rate sweep's points (the role of the reference's recurrent_weight_scale, models.py:664; the
+  LGN and background weights as generated): 5, 20 and 50 Hz, and for 1 Hz the lowest rate
+  recurrent scaling reaches (factor 0: the inputs alone drive the network at ~4.5 Hz).  At
+  every point the deterministic forward is bit-exact over 500 ms, the event forward's spike
+  trains equal the oracle's for 50 ms from onset and its per-(batch, neuron) counts agree for
+  >= 99.9 %; and a B = 32 BPTT at the 50 Hz factor (one-tick windows, 32-float G rows)
+  against the oracle.
 
 The oracle runs its OpenMP loops (same bits as one thread).  Each step prints a progress line.
 """
@@ -202,8 +206,10 @@ def test_config3_forward():
 
 
 # ------------------------------------------------------------------ config 4 ----
-# weight factors of the rate sweep (profiles/rate_sweep_config4.md): mean rate 5 and 50 Hz
-FACTORS = {"5Hz": 0.9866, "50Hz": 1.9946}
+# recurrent weight factors of the rate sweep (bench.py --config 4, profiles/rate_sweep_config4.md):
+# mean rate 5, 20 and 50 Hz; 1 Hz lies below what recurrent scaling reaches, whose floor (factor 0,
+# ~4.5 Hz) stands in for it
+REC_FACTORS = {"1Hz_floor": 0.0, "5Hz": 0.70091, "20Hz": 5.28304, "50Hz": 8.45088}
 
 
 @pytest.fixture(scope="module")
@@ -216,7 +222,7 @@ def config4():
 
 
 def _scaled_cell(net, f, mode="deterministic"):
-    """The config-4 network with all three weight populations scaled by f (float32)."""
+    """The network with all three weight populations scaled by f (float32)."""
     from v1_glif_model_amd.models import V1Column
     cell = V1Column(net, mode=mode, **CELL_KW)
     tb = cell.tables
@@ -231,10 +237,18 @@ def _scaled_cell(net, f, mode="deterministic"):
     return cell, tbs
 
 
-@pytest.mark.parametrize("rate", list(FACTORS))
+def _rec_scaled_cell(net, f, mode="deterministic"):
+    """The network with its recurrent weights scaled by f through the reference's own knob,
+    recurrent_weight_scale (models.py:664): the cell's tables are the oracle's."""
+    from v1_glif_model_amd.models import V1Column
+    cell = V1Column(net, mode=mode, recurrent_weight_scale=f, **CELL_KW)
+    return cell, cell.tables
+
+
+@pytest.mark.parametrize("rate", list(REC_FACTORS))
 def test_config4_forward(config4, rate):
     cfg, net, lgn, bkg = config4
-    cell, tbs = _scaled_cell(net, FACTORS[rate])
+    cell, tbs = _rec_scaled_cell(net, REC_FACTORS[rate])
     T, B, N = lgn.shape[0], lgn.shape[1], tbs.n_neurons
     zd, vd, _ = cell.rollout(lgn, bkg)
     ze, _, _ = cell.rollout(lgn, bkg, mode="event")
@@ -249,24 +263,24 @@ def test_config4_forward(config4, rate):
     differ = np.flatnonzero((ze != oz).any(axis=(1, 2)))
     agree = count_agreement(ze, oz)
     say(f"config 4 {rate} event: first differing ms", differ[0] if differ.size else None, "count agreement", agree)
+    assert t0 + 50 <= T
     np.testing.assert_array_equal(ze[:t0 + 50], oz[:t0 + 50])
-    if rate == "5Hz":
-        assert agree >= 0.999
+    assert agree >= 0.999
 
 
 def test_config4_bptt_batch32(config4):
     """B = 32: one-tick backward windows, 32-float G rows (8 lanes per column in the
-    type-phased walk); 80 ms from rest at the 50 Hz factor (spikes from ~33 ms)."""
+    type-phased walk); 150 ms from rest at the 50 Hz recurrent factor (onset at 46 ms)."""
     cfg, net, lgn, bkg = config4
-    cell, tbs = _scaled_cell(net, FACTORS["50Hz"])
-    T = 80
+    cell, tbs = _rec_scaled_cell(net, REC_FACTORS["50Hz"])
+    T = 150
     lgn, bkg = lgn[:T], bkg[:T]
     z, v, _ = cell.rollout(lgn, bkg)
     oc = orc.OracleCell(tbs, **ORC_KW)
     oz, ov, oref, _ = oc.forward(lgn, bkg)
     np.testing.assert_array_equal(z.cpu().numpy().astype(np.uint8), oz)
     say("config 4 B=32 BPTT window:", int(oz.sum()), "spikes")
-    assert oz.sum() > 10000
+    assert oz.sum() > 1_000_000
     gz = np.random.default_rng(44).normal(0, 1, oz.shape).astype(np.float32)
     g = {k: t.cpu().numpy() for k, t in cell.backward(gz=torch.tensor(gz, device="cuda")).items()}
     del cell
@@ -344,11 +358,13 @@ def test_config2_op_level(config2):
     ref = orc.syn_fwd(tb.rec, z, tb.basis)
     np.testing.assert_array_equal(det.view(np.uint32), ref.view(np.uint32))
     scale = dense.syn_fwd_abs(tb.rec, z, tb.basis)
-    assert np.max(np.abs(ev - ref) - 1e-5 * scale) <= 1e-6
+    say("op level: event currents", error_summary(ev, ref, scale))
+    assert_grads_per_element(ev, ref, scale, what="event currents")
     rdz, rdw = orc.syn_bwd(tb.rec, z, tb.basis, dy)
     _, _, dz_abs, dw_abs = dense.syn_bwd_f64(tb.rec, z, tb.basis, dy)
     say("op level: events", int(np.count_nonzero(z)), "max |dz|", float(np.abs(rdz).max()),
         "nonzero dW", int(np.count_nonzero(rdw)))
     assert np.count_nonzero(rdw) > 0
-    assert np.max(np.abs(dz - rdz) - 1e-5 * dz_abs) <= 1e-6
-    assert np.max(np.abs(dw - rdw) - 1e-5 * dw_abs) <= 1e-6
+    say("op level: dz", error_summary(dz, rdz, dz_abs), "dW", error_summary(dw, rdw, dw_abs))
+    assert_grads_per_element(dz, rdz, dz_abs, what="dz")
+    assert_grads_per_element(dw, rdw, dw_abs, what="dW")

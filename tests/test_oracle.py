@@ -311,3 +311,87 @@ def test_threaded_oracle_gives_the_same_bits():
     np.testing.assert_array_equal(v1.view(np.uint32), v4.view(np.uint32))
     for k in g1:
         np.testing.assert_array_equal(g1[k].view(np.uint32), g4[k].view(np.uint32))
+
+
+# ------------------------------------ gradients of the initial state (float64) ----
+def _quiet_tables(seed=7, n=60):
+    """A small network whose weights are scaled down so that nothing spikes: the rollout is
+    then linear in its initial state and weights."""
+    cfg = tiny_config(n=n, fanin=8, delays=3, n_lgn=20, lgn_fanin=4, n_bkg=5, bkg_fanin=2, rs=2.0, ins=3.0)
+    _, tb = network(cfg, seed=seed, dense_basis=True)
+    small = {k: dataclasses.replace(getattr(tb, k), weight=(getattr(tb, k).weight * np.float32(1e-3)))
+             for k in ("rec", "lgn", "bkg")}
+    return cfg, dataclasses.replace(tb, **small)
+
+
+def _random_state(tb, B, rng):
+    N, D, nb = tb.n_neurons, tb.max_delay, tb.n_basis
+    return dict(zbuf=rng.uniform(0, 1, (B, D * N)), v=rng.uniform(-0.3, 0.3, (B, N)),
+                r=np.zeros((B, N), np.int64), asc=rng.normal(0, 0.05, (B, 2 * N)),
+                psc_rise=rng.normal(0, 0.05, (B, N * nb)), psc=rng.normal(0, 0.05, (B, N * nb)))
+
+
+def test_state_gradients_equal_finite_differences():
+    """With vgd = 0, rd = 1 (no straight-through dampening), no spikes and a loss on the
+    voltages only, the rollout is linear in its initial state, so the restatement's
+    dL/d(initial state) equals central differences of its float64 forward, element by element
+    (the spike buffer's slot 0 feeds the reset only through stop_gradient and is left out)."""
+    torch = pytest.importorskip("torch")
+    from oracle import torch_ref
+    cfg, tb = _quiet_tables()
+    T, B, N = 8, 2, tb.n_neurons
+    lgn, bkg = sy.make_inputs(cfg, seed=3, seq_len=T, batch=B)
+    rng = np.random.default_rng(11)
+    s0 = _random_state(tb, B, rng)
+    z = np.zeros((T, B, N), np.float32)
+    gz = np.zeros((T, B, N))
+    gv = rng.normal(0, 1, (T, B, N))
+    kw = dict(vgd=0.0, rd=1.0)
+    _, v, g0 = torch_ref.bptt(tb, lgn, bkg, z, gz, gv, state0=s0, state_grad=True, **kw)
+    assert np.max(v) < 0.9           # quiet: no neuron near threshold
+
+    def loss(st):
+        _, vv = torch_ref.bptt(tb, lgn, bkg, z, gz, gv, state0=st, **kw)
+        return float(np.sum(vv * gv))
+
+    eps = 1e-4
+    for key in ("zbuf", "v", "asc", "psc_rise", "psc"):
+        lo = N if key == "zbuf" else 0
+        for j in rng.integers(lo, s0[key].shape[1], size=6):
+            b = int(rng.integers(0, B))
+            up, dn = copy.deepcopy(s0), copy.deepcopy(s0)
+            up[key][b, j] += eps
+            dn[key][b, j] -= eps
+            fd = (loss(up) - loss(dn)) / (2 * eps)
+            assert abs(fd - g0[key][b, j]) <= 1e-7 * max(1.0, abs(fd)), (key, b, j, fd, g0[key][b, j])
+
+
+def test_state_gradients_carry_the_dampening_factors():
+    """Closed forms the finite differences cannot see: with zero weights and a loss on the
+    voltages, dL/dv_0 = sum_t gv_t (decay (1 - vgd))^(t+1) (straight_through_dampen(v, vgd));
+    and the initial spike buffer's slots >= 1 reach the loss only through the synaptic op, so
+    their gradient at rd is rd times their gradient at rd = 1."""
+    torch = pytest.importorskip("torch")
+    from oracle import torch_ref
+    cfg, tb = _quiet_tables(seed=8)
+    T, B, N = 6, 1, tb.n_neurons
+    lgn, bkg = sy.make_inputs(cfg, seed=4, seq_len=T, batch=B)
+    rng = np.random.default_rng(12)
+    s0 = _random_state(tb, B, rng)
+    z = np.zeros((T, B, N), np.float32)
+    gv = rng.normal(0, 1, (T, B, N))
+    zero_w = dataclasses.replace(tb, **{k: dataclasses.replace(getattr(tb, k), weight=np.zeros_like(
+        getattr(tb, k).weight)) for k in ("rec", "lgn", "bkg")})
+    vgd = 0.3
+    _, _, g0 = torch_ref.bptt(zero_w, lgn, bkg, z, np.zeros_like(gv), gv, vgd=vgd, rd=0.5, state0=s0,
+                              state_grad=True)
+    m = tb.decay.astype(np.float64) * (1.0 - vgd)
+    expect = sum(gv[t] * m ** (t + 1) for t in range(T))
+    np.testing.assert_allclose(g0["v"], expect, rtol=1e-12, atol=1e-14)
+    g_rd = {}
+    for rd in (1.0, 0.2):
+        _, _, g = torch_ref.bptt(tb, lgn, bkg, z, np.zeros_like(gv), gv, vgd=0.0, rd=rd, state0=s0,
+                                 state_grad=True)
+        g_rd[rd] = g["zbuf"][:, N:]
+    assert np.max(np.abs(g_rd[1.0])) > 0
+    np.testing.assert_allclose(g_rd[0.2], 0.2 * g_rd[1.0], rtol=1e-9, atol=1e-9 * np.max(np.abs(g_rd[1.0])))

@@ -35,6 +35,11 @@ class State(C.Structure):
     _fields_ = [("z_buf", vp), ("v", vp), ("r", vp), ("asc", vp), ("psc_rise", vp), ("psc", vp)]
 
 
+class StateGrad(C.Structure):
+    """glif_state_grad: device pointers of the gradients of the state tuple (NULL: none)."""
+    _fields_ = [("z_buf", vp), ("v", vp), ("asc", vp), ("psc_rise", vp), ("psc", vp)]
+
+
 SIGNATURES = {
     "glif_last_error": (C.c_char_p, []),
     "glif_version": (C.c_int, []),
@@ -57,6 +62,9 @@ SIGNATURES = {
     "glif_cell_forward": (C.c_int, [vp, i32, i32, i32, vp, vp, C.POINTER(State), vp, vp, vp, vp,
                                     sz, vp]),
     "glif_cell_backward": (C.c_int, [vp, i32, i32, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
+    "glif_step_workspace": (sz, [vp, i32]),
+    "glif_step_backward": (C.c_int, [vp, i32, vp, vp, vp, vp, vp, vp, vp, C.POINTER(StateGrad),
+                                     C.POINTER(StateGrad), vp, vp, vp, vp, sz, vp]),
     "glif_cell_set_voltage_loss": (C.c_int, [vp, i32, C.c_float]),
     "glif_cell_voltage_loss": (C.c_int, [vp, i32, i32, vp, vp, sz, vp]),
     "glif_cell_set_trim": (C.c_int, [vp, i32, i32]),

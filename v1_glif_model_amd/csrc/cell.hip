@@ -69,6 +69,7 @@ struct CellWs {
     uint8_t *bkg_cnt;   // [T][B][n_bkg]
     void *scratch;
     float *dZ;          // [ring][B][D * N]
+    float *stage;       // from dZ on: staging of the gradient reorderings (after the walks)
     float *G;           // [2][n_types][N][R], or [2][N][g_rows][R] with compact rows
                         // (windows alternate between the two)
     float *gV;          // [B][N]
@@ -142,12 +143,15 @@ static int ring_size(const Cell *c) { return c->D + 6; }
 // compact rows when there are more of them.
 static int i_slots(const Cell *c) { return std::max(c->nb, c->push_typed ? c->g_rows : 0); }
 
+// The regions a backward reads of its forward (spike bits, saved voltages, input lists) come
+// first, at offsets that depend on B, T and the network only; the two whose size depends on the
+// G layout (glif_cell_set_g_layout) -- G and the pushed currents I -- come after them, so a
+// backward run after a layout switch still finds its forward's data.
 static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *bytes) {
     Carver cv(ws, SIZE_MAX);
     CellWs w{};
     const int64_t BN = static_cast<int64_t>(B) * c->N;
     const int64_t nl = c->lgn->n_cols, nk = c->bkg->n_cols;
-    w.I = cv.take<float>(2 * BN * i_slots(c));   // event mode alternates between the two halves by tick
     w.R = cv.take<float>(BN * c->nb);
     w.P = cv.take<float>(BN * c->nb);
     w.A = cv.take<float>(BN * 2);
@@ -175,8 +179,15 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.kw_mask = cv.take<uint32_t>(static_cast<size_t>(nwin) * nk);
     w.bkg_cnt = cv.take<uint8_t>(static_cast<size_t>(T) * B * nk);
     w.scratch = cv.take<char>(std::max(compact_scratch_bytes(T, nl), compact_scratch_bytes(T, nk)));
+    // the dz ring and G, then (when they are shorter) enough bytes that the span from the ring's
+    // start holds the staging of the gradient reorderings, which run after the last reader of both
+    const size_t z0 = cv.mark();
     w.dZ = cv.take<float>(static_cast<size_t>(ring_size(c)) * B * c->D * c->N);
     w.G = cv.take<float>(2 * static_cast<size_t>(c->N) * c->g_rows * g_row(Wwin, B));
+    const size_t stage_bytes = sizeof(float) * static_cast<size_t>(std::max(
+        c->rec->pinv.runs ? c->rec->n_syn : 0, c->lgn->pinv.runs ? c->lgn->n_syn : 0));
+    if (cv.off - z0 < stage_bytes) cv.take<char>(stage_bytes - (cv.off - z0));
+    w.stage = w.dZ;
     w.gV = cv.take<float>(BN);
     w.gP = cv.take<float>(BN * c->nb);
     w.gR = cv.take<float>(BN * c->nb);
@@ -184,6 +195,7 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.dw_rec = cv.take<float>(std::max<int64_t>(c->rec->n_syn, 1));
     w.dw_lgn = cv.take<float>(std::max<int64_t>(c->lgn->n_syn, 1));
     w.dw_bkg = cv.take<float>(std::max<int64_t>(c->bkg->n_syn, 1));
+    w.I = cv.take<float>(2 * BN * i_slots(c));   // event mode alternates between the two halves by tick
     if (bytes) *bytes = cv.off;
     return w;
 }
@@ -1567,6 +1579,113 @@ static int chunks_for(const Table *t, int L) {
 
 using namespace glif;
 
+// ------------------------------------------------------- one step's backward ----
+// The gradient of one V1Column.call (models.py:1059-1135) as the reference's tape takes it
+// when the Keras RNN runs the cell step by step: from the gradients of the step's outputs
+// (z, v) and of its new state to those of its old state and of the three weight vectors.
+// Per (b, n), with V' the step's voltage and r' its refractory counter:
+//   gV'   = [r' == 0] gz psi(V' - 1) + dL/dv + dL/dv_state,  gz = dL/dz + dL/dz_buf'[slot 0]
+//           (zero where r' > 0 under hard reset, whose where() cuts the path)
+//   gv    = (gV' decay)(1 - vgd)                       (straight_through_dampen(v, vgd))
+//   gasc_j = gasc'_j asc_decay_j + gV' cf              (c1 = sum P + sum asc, old P and asc)
+//   gP_r  = gP'_r sd_r + gV' cf
+//   gR_r  = gR'_r sd_r + gP'_r (dt sd_r)               (P' = P sd + (dt sd) R)
+//   dy_r  = (gR'_r p0_r) lr                            (R' = R sd + (I lr) p0)
+// dy then goes through the synaptic op's gradient (glif_syn_bwd): dz over all recurrent
+// synapses, scaled by rd (straight_through_dampen(z_buf, 1 - rd)) and added to the shifted
+// dL/dz_buf' (z_buf' = [z, z_buf[:, :-N]]), and the weight gradients of the step's events.
+struct StepAdjArgs {
+    CellConst k;
+    const float *decay, *cf, *asc_decay;
+    const float *v_new;
+    const int16_t *r_new;
+    const float *gz, *gv;                                   // [B][N] (nullable)
+    const float *gzb_new, *gv_new, *gasc_new, *gR_new, *gP_new;  // the new state's (nullable)
+    float *gv_old, *gasc_old, *gR_old, *gP_old;             // the old state's (nullable)
+    float *dy;                                              // [B * N][nb]
+};
+
+__global__ void __launch_bounds__(kBlock) k_step_adj(StepAdjArgs a) {
+    const CellConst &k = a.k;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(k.B) * k.N) return;
+    const int n = static_cast<int>(i % k.N);
+    const int64_t b = i / k.N;
+    const bool refr = a.r_new[i] > 0;
+    float gzz = a.gz ? a.gz[i] : 0.0f;
+    if (a.gzb_new) gzz = gzz + a.gzb_new[b * k.D * k.N + n];
+    float gV = 0.0f;
+    if (!refr) {
+        const float vsc = a.v_new[i] - 1.0f;
+        float psi;
+        if (k.pseudo_gauss) {
+            const float q = -(vsc * vsc) / (k.gauss_std * k.gauss_std);
+            psi = expf(q) * k.damp;
+        } else {
+            const float m = 1.0f - fabsf(vsc);
+            psi = k.damp * (m > 0.0f ? m : 0.0f);
+        }
+        gV = gzz * psi;
+    }
+    if (a.gv) gV = gV + a.gv[i];
+    if (a.gv_new) gV = gV + a.gv_new[i];
+    if (k.hard_reset && refr) gV = 0.0f;
+    if (a.gv_old) a.gv_old[i] = (gV * a.decay[n]) * k.om;
+    const float gc = gV * a.cf[n];
+    if (a.gasc_old)
+        for (int j = 0; j < 2; ++j)
+            a.gasc_old[i * 2 + j] = (a.gasc_new ? a.gasc_new[i * 2 + j] * a.asc_decay[n * 2 + j] : 0.0f) + gc;
+    for (int q = 0; q < k.nb; ++q) {
+        const int64_t e = i * k.nb + q;
+        const float gRn = a.gR_new ? a.gR_new[e] : 0.0f;
+        const float gPn = a.gP_new ? a.gP_new[e] : 0.0f;
+        if (a.gP_old) a.gP_old[e] = gPn * k.sd[q] + gc;
+        if (a.gR_old) a.gR_old[e] = gRn * k.sd[q] + gPn * k.dtsd[q];
+        a.dy[e] = (gRn * k.p0[q]) * k.lr;
+    }
+}
+
+// gzb[b][c] = rd * dz[b][c] + dL/dz_buf'[b][c + N] (the shifted slots; the last slot has none)
+__global__ void __launch_bounds__(kBlock)
+    k_step_zbuf_grad(float *__restrict__ gzb, const float *__restrict__ gzb_new, int64_t n, int64_t DN, int32_t N,
+                     float rd) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float g = gzb[i] * rd;
+    if (gzb_new && i % DN < DN - N) g = g + gzb_new[i + N];
+    gzb[i] = g;
+}
+
+__global__ void __launch_bounds__(kBlock) k_u8_to_f32(float *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                        int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = static_cast<float>(src[i]);
+}
+
+struct StepWs {
+    float *dy;      // [B * N][nb]
+    float *xl, *xk; // the step's LGN spikes and background counts as floats
+    void *syn;      // the op gradients' workspace (one at a time)
+    size_t syn_bytes;
+};
+
+static StepWs carve_step(void *ws, const Cell *c, int32_t B, size_t *bytes) {
+    Carver cv(ws, SIZE_MAX);
+    StepWs w{};
+    const int64_t BN = static_cast<int64_t>(B) * c->N;
+    w.dy = cv.take<float>(BN * c->nb);
+    w.xl = cv.take<float>(std::max<int64_t>(static_cast<int64_t>(B) * c->lgn->n_cols, 1));
+    w.xk = cv.take<float>(std::max<int64_t>(static_cast<int64_t>(B) * c->bkg->n_cols, 1));
+    const glif_table *tabs[3] = {reinterpret_cast<const glif_table *>(c->rec),
+                                 reinterpret_cast<const glif_table *>(c->lgn),
+                                 reinterpret_cast<const glif_table *>(c->bkg)};
+    w.syn_bytes = 0;
+    for (const glif_table *t : tabs) w.syn_bytes = std::max(w.syn_bytes, glif_syn_workspace(t, B));
+    w.syn = cv.take<char>(std::max<size_t>(w.syn_bytes, 1));
+    if (bytes) *bytes = cv.off;
+    return w;
+}
+
 extern "C" {
 
 int glif_cell_create(const glif_cell_config *cfg, const float *decay, const float *current_factor,
@@ -2173,10 +2292,12 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
         launch_adj(aa, c->nb, s, &prev, false);
     }
     GLIF_HIP(hipGetLastError());
-    if (dw_rec && (rc = gs ? launch_perm_gather(dw_rec, w.dw_rec, tr->order_inv, tr->pinv, tr->n_syn, s)
+    if (dw_rec && (rc = gs ? launch_perm_gather(dw_rec, w.dw_rec, tr->order_inv, tr->pinv, tr->n_syn, w.stage, s)
                            : launch_gather_f32(dw_rec, w.dw_rec, tr->ph_inv, tr->n_syn, s)))
         return rc;
-    if (dw_lgn && (rc = launch_perm_gather(dw_lgn, w.dw_lgn, tl->order_inv, tl->pinv, tl->n_syn, s))) return rc;
+    if (dw_lgn &&
+        (rc = launch_perm_gather(dw_lgn, w.dw_lgn, tl->order_inv, tl->pinv, tl->n_syn, w.stage, s)))
+        return rc;
     if (dw_bkg && (rc = launch_gather_f32(dw_bkg, w.dw_bkg, tb->order_inv, tb->n_syn, s))) return rc;
     return GLIF_OK;
 }
@@ -2243,6 +2364,83 @@ int glif_cell_voltage_loss(glif_cell *cc, int32_t B, int32_t T, float *loss_out,
     const float scale =
         c->vloss_cost / static_cast<float>(c->vloss_mask ? static_cast<int64_t>(T) * B * c->vloss_n : n);
     hipLaunchKernelGGL(k_vloss_final, dim3(1), dim3(kBlock), 0, s, w.vloss_part, kVlossBlocks, scale, loss_out);
+    GLIF_HIP(hipGetLastError());
+    return GLIF_OK;
+}
+
+size_t glif_step_workspace(const glif_cell *cc, int32_t B) {
+    const Cell *c = reinterpret_cast<const Cell *>(cc);
+    if (!c || B <= 0 || B > kMaxBatch) return 0;
+    size_t bytes = 0;
+    carve_step(nullptr, c, B, &bytes);
+    return bytes;
+}
+
+int glif_step_backward(glif_cell *cc, int32_t B, const uint8_t *lgn, const uint8_t *bkg, const float *z_buf,
+                       const float *v_new, const int16_t *r_new, const float *gz, const float *gv,
+                       const glif_state_grad *g_new, glif_state_grad *g_old, float *dw_rec, float *dw_lgn,
+                       float *dw_bkg, void *ws, size_t ws_bytes, void *stream) {
+    Cell *c = reinterpret_cast<Cell *>(cc);
+    if (!c || !v_new || !r_new) return fail(GLIF_EINVAL, "NULL argument");
+    if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
+    const bool want_dz = g_old && g_old->z_buf;
+    if ((want_dz || dw_rec) && !z_buf) return fail(GLIF_EINVAL, "z_buf is needed for dL/dz_buf and dw_rec");
+    if (dw_lgn && !lgn) return fail(GLIF_EINVAL, "lgn is needed for dw_lgn");
+    if (dw_bkg && !bkg) return fail(GLIF_EINVAL, "bkg is needed for dw_bkg");
+    if (!ws || ws_bytes < glif_step_workspace(cc, B)) return fail(GLIF_ENOMEM, "workspace too small");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    StepWs w = carve_step(ws, c, B, nullptr);
+    const int64_t BN = static_cast<int64_t>(B) * c->N;
+    StepAdjArgs a{};
+    a.k = make_const(c, B);
+    a.decay = c->decay;
+    a.cf = c->cf;
+    a.asc_decay = c->asc_decay;
+    a.v_new = v_new;
+    a.r_new = r_new;
+    a.gz = gz;
+    a.gv = gv;
+    if (g_new) {
+        a.gzb_new = g_new->z_buf;
+        a.gv_new = g_new->v;
+        a.gasc_new = g_new->asc;
+        a.gR_new = g_new->psc_rise;
+        a.gP_new = g_new->psc;
+    }
+    if (g_old) {
+        a.gv_old = g_old->v;
+        a.gasc_old = g_old->asc;
+        a.gR_old = g_old->psc_rise;
+        a.gP_old = g_old->psc;
+    }
+    a.dy = w.dy;
+    hipLaunchKernelGGL(k_step_adj, dim3(ceil_div(BN, kBlock)), dim3(kBlock), 0, s, a);
+    GLIF_HIP(hipGetLastError());
+    int rc;
+    const glif_table *rec = reinterpret_cast<const glif_table *>(c->rec);
+    if ((want_dz || dw_rec) &&
+        (rc = glif_syn_bwd(rec, z_buf, w.dy, B, 0, want_dz ? g_old->z_buf : nullptr, dw_rec, w.syn, w.syn_bytes, s)))
+        return rc;
+    if (want_dz) {
+        const int64_t DN = static_cast<int64_t>(c->D) * c->N, n = static_cast<int64_t>(B) * DN;
+        hipLaunchKernelGGL(k_step_zbuf_grad, dim3(ceil_div(n, kBlock)), dim3(kBlock), 0, s, g_old->z_buf,
+                           g_new ? g_new->z_buf : nullptr, n, DN, c->N, a.k.rd_scale);
+        GLIF_HIP(hipGetLastError());
+    }
+    if (dw_lgn) {
+        const int64_t n = static_cast<int64_t>(B) * c->lgn->n_cols;
+        if (n) hipLaunchKernelGGL(k_u8_to_f32, dim3(ceil_div(n, kBlock)), dim3(kBlock), 0, s, w.xl, lgn, n);
+        if ((rc = glif_syn_bwd(reinterpret_cast<const glif_table *>(c->lgn), w.xl, w.dy, B, 0, nullptr, dw_lgn,
+                               w.syn, w.syn_bytes, s)))
+            return rc;
+    }
+    if (dw_bkg) {
+        const int64_t n = static_cast<int64_t>(B) * c->bkg->n_cols;
+        if (n) hipLaunchKernelGGL(k_u8_to_f32, dim3(ceil_div(n, kBlock)), dim3(kBlock), 0, s, w.xk, bkg, n);
+        if ((rc = glif_syn_bwd(reinterpret_cast<const glif_table *>(c->bkg), w.xk, w.dy, B, 1, nullptr, dw_bkg,
+                               w.syn, w.syn_bytes, s)))
+            return rc;
+    }
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;
 }

@@ -73,7 +73,7 @@ struct PermPlan {
     int4 *runs = nullptr;      // {first staging position, length, first source of the chunk, 0}
     uint16_t *off1 = nullptr;  // [n] per staging position: source - first source of its chunk
     uint16_t *off2 = nullptr;  // [n] per destination: staging position - superblock start
-    float *mid = nullptr;      // [n] staging (the plan's own: gathers with one plan do not overlap)
+    float *mid = nullptr;      // [n] staging of the plan's own, or nullptr (callers pass one)
 };
 
 struct Table {
@@ -209,14 +209,20 @@ struct Carver {
         return p;
     }
     bool ok() const { return off <= cap; }
+    // the next region's offset (aligned as take() aligns it)
+    size_t mark() {
+        off = (off + 255) & ~size_t(255);
+        return off;
+    }
 };
 
 // ---- launch helpers (defined in the .hip files) ----------------------------
 int launch_fill_u32(void *p, uint32_t value, size_t n, hipStream_t s);
 int launch_gather_f32(float *dst, const float *src, const int32_t *idx, int64_t n, hipStream_t s);
-// dst[k] = src[idx[k]] through the plan when it is built, else one gather
+// dst[k] = src[idx[k]] through the plan when it is built (staging through mid, n floats),
+// else one gather
 int launch_perm_gather(float *dst, const float *src, const int32_t *idx, const PermPlan &plan, int64_t n,
-                       hipStream_t s);
+                       float *mid, hipStream_t s);
 
 inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
 

@@ -97,12 +97,13 @@ int launch_gather_f32(float *dst, const float *src, const int32_t *idx, int64_t 
 }
 
 int launch_perm_gather(float *dst, const float *src, const int32_t *idx, const PermPlan &plan, int64_t n,
-                       hipStream_t s) {
+                       float *mid, hipStream_t s) {
     if (!plan.runs) return launch_gather_f32(dst, src, idx, n, s);
-    hipLaunchKernelGGL(k_perm_runs, dim3(plan.n_runs), dim3(kBlock), 0, s, src, plan.mid, plan.runs, plan.off1);
+    if (!mid) return fail(GLIF_EINVAL, "permutation plan without a staging buffer");
+    hipLaunchKernelGGL(k_perm_runs, dim3(plan.n_runs), dim3(kBlock), 0, s, src, mid, plan.runs, plan.off1);
     GLIF_HIP(hipGetLastError());
     const int64_t blocks = 8 * ((n + 8 * kBlock - 1) / (8 * kBlock));
-    hipLaunchKernelGGL(k_perm_local, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, plan.mid, dst, plan.off2,
+    hipLaunchKernelGGL(k_perm_local, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, mid, dst, plan.off2,
                        n);
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;
@@ -188,8 +189,9 @@ static void free_plan(PermPlan &pp) {
 
 // The two-pass plan of dst[k] = src[P[k]], k < n (P a permutation of 0..n-1).  Staging
 // position of source j: in the superblock of its destination, after the sources j' < j that go
-// there, so each (chunk, superblock) pair's sources are one contiguous run.
-static int build_perm_plan(PermPlan *pp, const int32_t *P, int64_t n) {
+// there, so each (chunk, superblock) pair's sources are one contiguous run.  With own_mid the
+// plan allocates its staging (n floats); otherwise each caller passes one.
+static int build_perm_plan(PermPlan *pp, const int32_t *P, int64_t n, bool own_mid) {
     constexpr int64_t kSB = int64_t(1) << kPermShift;
     const int64_t nsb = (n + kSB - 1) / kSB;
     std::vector<int32_t> Pinv(n), mpos(n), fill(nsb, 0), snap(nsb);
@@ -224,10 +226,12 @@ static int build_perm_plan(PermPlan *pp, const int32_t *P, int64_t n) {
         free_plan(*pp);
         return rc;
     }
-    hipError_t e = hipMalloc(reinterpret_cast<void **>(&pp->mid), n * sizeof(float));
-    if (e != hipSuccess) {
-        free_plan(*pp);
-        return hip_fail(e, "hipMalloc(permutation staging)");
+    if (own_mid) {
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(&pp->mid), n * sizeof(float));
+        if (e != hipSuccess) {
+            free_plan(*pp);
+            return hip_fail(e, "hipMalloc(permutation staging)");
+        }
     }
     pp->n_runs = static_cast<int32_t>(runs.size());
     return GLIF_OK;
@@ -576,9 +580,12 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         return rc;
     }
     // two-pass plans of the two reorderings done every training step (config 2's recurrent
-    // table: 305 us each as one gather)
-    if (n_syn >= kPermMinSyn && ((rc = build_perm_plan(&t->pcol, order.data(), n_syn)) ||
-                                 (rc = build_perm_plan(&t->pinv, order_inv.data(), n_syn)))) {
+    // table: 305 us each as one gather).  The weight refresh stages through the table's own
+    // buffer (refreshes of one table write its weight copies, so they never overlap); the
+    // gradient reorder of a cell's backward stages through that backward's workspace, so
+    // backwards on other streams stay independent.
+    if (n_syn >= kPermMinSyn && ((rc = build_perm_plan(&t->pcol, order.data(), n_syn, true)) ||
+                                 (rc = build_perm_plan(&t->pinv, order_inv.data(), n_syn, false)))) {
         free_table(t);
         return rc;
     }
@@ -604,7 +611,7 @@ int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
     if (!tt || !w) return fail(GLIF_EINVAL, "NULL argument");
     Table *t = reinterpret_cast<Table *>(tt);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    int rc = launch_perm_gather(t->w_col, w, t->order, t->pcol, t->n_syn, s);
+    int rc = launch_perm_gather(t->w_col, w, t->order, t->pcol, t->n_syn, t->pcol.mid, s);
     if (rc) return rc;
     // the type-phased and grouped copies from w_col (near-sequential reads)
     if (t->n_syn) {

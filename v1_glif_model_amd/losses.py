@@ -43,37 +43,59 @@ _MODES = {"range": 1, "threshold": 2}
 
 
 class VoltageRegularization:
+    """The cell holds one fused voltage loss: the regularizer that claimed it last (by being
+    constructed, or by a fused ``reg()`` call) owns it, and only the owner switches it off
+    (``disable()``, or when it is deleted).  A fused ``reg()`` re-claims it, with this object's
+    penalty, cost and core mask, if another regularizer took it meanwhile."""
+
     def __init__(self, cell, voltage_cost=1e-5, dtype=torch.float32, core_mask=None, penalty_mode="range"):
+        self._cell = None
+        self._tok = object()   # the marker the cell keeps of its owner (it does not keep this object alive)
         if penalty_mode not in _MODES:
             raise ValueError("penalty_mode must be 'range' or 'threshold'")
         self._cell = cell
         self._voltage_cost = float(voltage_cost)
         self._penalty_mode = penalty_mode
         self._core_mask = None
+        self._mask_u8 = None
+        self._fused = False
         if core_mask is not None:
             m = torch.as_tensor(core_mask, device=cell.device).to(torch.bool).reshape(-1)
             if m.numel() != cell._n_neurons or not bool(m.any()):
                 raise ValueError("core_mask must select at least one of the cell's neurons")
             self._core_mask = m
-            self._mask_u8 = m.to(torch.uint8).contiguous()   # kept alive while enabled
-            check(lib().glif_cell_set_voltage_mask(cell.handle, ptr(self._mask_u8), int(m.sum().item())))
-        else:
-            check(lib().glif_cell_set_voltage_mask(cell.handle, None, 0))
-        self._set_fused(True)
+            self._mask_u8 = m.to(torch.uint8).contiguous()   # kept alive while this object owns the loss
+        self._claim()
 
-    def _set_fused(self, on: bool):
-        mode, cost = (_MODES[self._penalty_mode], self._voltage_cost) if on else (0, 0.0)
-        check(lib().glif_cell_set_voltage_loss(self._cell.handle, mode, cost))
-        self._fused = on
+    def _owns(self) -> bool:
+        cell = self._cell
+        return cell is not None and getattr(cell, "_vloss_owner", None) is self._tok
+
+    def _claim(self):
+        """Enable the fused loss on the cell with this object's penalty, cost and mask."""
+        cell = self._cell
+        n_sel = int(self._core_mask.sum().item()) if self._core_mask is not None else 0
+        check(lib().glif_cell_set_voltage_mask(cell.handle, ptr(self._mask_u8), n_sel))
+        check(lib().glif_cell_set_voltage_loss(cell.handle, _MODES[self._penalty_mode], self._voltage_cost))
+        cell._vloss_owner = self._tok
+        cell._vloss_mask_ref = self._mask_u8
+        self._fused = True
+
+    def _release(self):
+        """Switch the fused loss off, if this object still owns it."""
+        cell = self._cell
+        if self._owns() and getattr(cell, "handle", None) is not None:
+            check(lib().glif_cell_set_voltage_loss(cell.handle, 0, 0.0))
+            check(lib().glif_cell_set_voltage_mask(cell.handle, None, 0))
+            cell._vloss_owner = None
+            cell._vloss_mask_ref = None
+        self._fused = False
 
     def disable(self):
-        """Switch the fused gradient off and release the core mask on the cell."""
-        cell = getattr(self, "_cell", None)
-        if cell is None or getattr(cell, "handle", None) is None:
+        """Switch the fused gradient off (if this object still owns it) and detach from the cell."""
+        if getattr(self, "_cell", None) is None:
             return
-        check(lib().glif_cell_set_voltage_loss(cell.handle, 0, 0.0))
-        check(lib().glif_cell_set_voltage_mask(cell.handle, None, 0))
-        self._fused = False
+        self._release()
         self._cell = None
 
     def __del__(self):
@@ -97,13 +119,12 @@ class VoltageRegularization:
         if voltages is not None:
             # autograd carries this gradient (as gv): the fused one must not be added too
             if self._fused:
-                check(lib().glif_cell_set_voltage_loss(cell.handle, 0, 0.0))
-                self._fused = False
+                self._release()
             if self._core_mask is not None:
                 voltages = voltages[:, :, self._core_mask]   # tf.boolean_mask(..., axis=2)
             return self.penalty(voltages, self._penalty_mode).mean() * self._voltage_cost
-        if not self._fused:
-            self._set_fused(True)
+        if not self._fused or not self._owns():
+            self._claim()
         rec = cell.check_rollout()
         out = torch.empty((), dtype=torch.float32, device=cell.device)
         check(lib().glif_cell_voltage_loss(cell.handle, rec.B, rec.T, ptr(out), ptr(rec.ws), rec.ws.numel(),

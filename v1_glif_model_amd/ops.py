@@ -103,6 +103,8 @@ class SynapseTable:
         self.n_syn = post.size
         self.n_types, self.n_basis = basis.shape
         self.n_delay_slots = int(n_delay_slots)
+        # the device the table is uploaded to (the current one); its entry points take tensors there
+        self.device = torch.device("cuda", torch.cuda.current_device())
         h = C.c_void_p()
         check(lib().glif_table_create(post.ctypes.data_as(C.c_void_p), col.ctypes.data_as(C.c_void_p),
                                       sid.ctypes.data_as(C.c_void_p), self.n_syn, self.n_post,
@@ -132,8 +134,8 @@ class SynapseTable:
         """refresh_recurrent_weight_shadow (models.py:966-976): copy w into the table.
 
         Skipped when the same tensor at the same version was copied last time."""
-        if w.dtype != torch.float32 or not w.is_cuda or w.numel() != self.n_syn:
-            raise ValueError("weights must be a float32 CUDA tensor with one entry per synapse")
+        if not torch.is_tensor(w) or w.dtype != torch.float32 or w.device != self.device or w.numel() != self.n_syn:
+            raise ValueError(f"weights must be a float32 tensor on {self.device} with one entry per synapse")
         w = w.detach().contiguous()
         key = (w.data_ptr(), w._version)
         if force or key != self._w_key:
@@ -149,7 +151,23 @@ class SynapseTable:
             self._ws[(B, str(device))] = ws
         return ws
 
+    def _check_z(self, z):
+        """ValueError unless z is a [B, n_cols] tensor on the table's device with 1 <= B <= 32."""
+        if not torch.is_tensor(z) or z.dim() != 2:
+            raise ValueError("z must be a 2-D tensor [B, n_cols]")
+        if z.device != self.device:
+            raise ValueError(f"z is on {z.device}, the table on {self.device}")
+        if z.shape[1] != self.n_cols:
+            raise ValueError(f"z must have {self.n_cols} columns (dense_shape[1]), got {z.shape[1]}")
+        if not 1 <= z.shape[0] <= 32:
+            raise ValueError(f"batch size must be in [1, 32], got {z.shape[0]}")
+        if z.dtype.is_complex:
+            raise ValueError(f"z must be a real tensor, got {z.dtype}")
+
     def forward(self, z: torch.Tensor, counts: bool = False, mode: str = "event") -> torch.Tensor:
+        self._check_z(z)
+        if mode not in MODES:
+            raise ValueError(f"mode must be one of {sorted(MODES)}")
         B = z.shape[0]
         z = z.contiguous()
         if z.dtype != torch.float32:
@@ -162,7 +180,13 @@ class SynapseTable:
 
     def backward(self, z: torch.Tensor, dy: torch.Tensor, counts: bool = False, want_dz: bool = True,
                  want_dw: bool = True):
+        self._check_z(z)
         B = z.shape[0]
+        if not torch.is_tensor(dy) or tuple(dy.shape) != (B * self.n_post, self.n_basis):
+            raise ValueError(f"dy must have shape {(B * self.n_post, self.n_basis)} ([B * n_post, n_basis]), "
+                             f"got {tuple(dy.shape) if torch.is_tensor(dy) else type(dy).__name__}")
+        if dy.device != self.device:
+            raise ValueError(f"dy is on {dy.device}, the table on {self.device}")
         z = z.contiguous().float()
         dy = dy.contiguous().float()
         dz = torch.empty((B, self.n_cols), dtype=torch.float32, device=z.device) if want_dz else None
@@ -175,8 +199,10 @@ class SynapseTable:
 
 def where_gt0(z: torch.Tensor) -> torch.Tensor:
     """tf.where(z > 0) for a 2-D float32 CUDA tensor (models.py:128): [n, 2] int64, row-major."""
-    if z.dim() != 2:
+    if not torch.is_tensor(z) or z.dim() != 2:
         raise ValueError("where_gt0 takes a 2-D tensor")
+    if not z.is_cuda:
+        raise ValueError("where_gt0 takes a device tensor")
     z = z.contiguous().float()
     rows, cols = z.shape
     pairs = torch.empty((max(rows * cols, 1), 2), dtype=torch.int64, device=z.device)
