@@ -45,12 +45,13 @@ def _args():
                     help="mse: the configuration's firing-rate MSE against lognormal(4 Hz) targets; "
                          "reference: the reference's rate-distribution target + voltage regularization")
     ap.add_argument("--seq-len", type=int, default=None)
-    ap.add_argument("--cpu-steps", type=int, default=30,
+    ap.add_argument("--cpu-steps", type=int, default=None,
                     help="timesteps of the CPU baseline sample, timed with one thread and with the "
-                         "host's cores (0: skip)")
-    ap.add_argument("--cpu-start", type=int, default=200,
+                         "host's cores (0: skip; default 30, config 0 its whole 50 ms)")
+    ap.add_argument("--cpu-start", type=int, default=None,
                     help="first tick of the CPU baseline sample (the state there comes from the GPU's "
-                         "deterministic rollout; config 2 is silent for its first ~70 ms)")
+                         "deterministic rollout; configs 1-3 are silent for their first ~50-70 ms: default "
+                         "200, config 0 from tick 0)")
     ap.add_argument("--forward-only", action="store_true")
     ap.add_argument("--syn-types", type=int, default=None,
                     help="synapse types of the generated network (the configurations use 5; the "
@@ -82,8 +83,17 @@ def _args():
                          "z_buf spikes at 5 Hz")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (5 times): the "
-                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
-    return ap.parse_args()
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE for streaming kernels")
+    ap.add_argument("--gather-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 16M random 64-byte row gathers (torch index_select, 5 times) from a "
+                         "MIB MiB table: a known-size gather kernel for rocprofv3's read counters (its "
+                         "requests mix 128- and 64-byte reads, unlike the copy's 128-byte ones)")
+    args = ap.parse_args()
+    if args.cpu_steps is None:
+        args.cpu_steps = 50 if args.config == 0 else 30
+    if args.cpu_start is None:
+        args.cpu_start = 0 if args.config == 0 else 200
+    return args
 
 
 def copy_calibration(mib):
@@ -95,6 +105,23 @@ def copy_calibration(mib):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read_per_launch": n * 4, "copy_bytes_written_per_launch": n * 4,
+                      "launches": 5}))
+
+
+def gather_calibration(mib, n_gathers=1 << 24):
+    """index_select of n_gathers random rows of 16 float32 (64 bytes) from a [rows, 16] table of
+    mib MiB: per launch it reads n_gathers * 64 bytes at random rows plus the int64 indices
+    (8 bytes each, streamed) and writes n_gathers * 64 bytes (streamed)."""
+    import torch
+    rows = mib * (1 << 20) // 64
+    src = torch.ones((rows, 16), dtype=torch.float32, device="cuda")
+    idx = torch.randint(0, rows, (n_gathers,), dtype=torch.int64, device="cuda")
+    out = torch.empty((n_gathers, 16), dtype=torch.float32, device="cuda")
+    for _ in range(5):
+        torch.index_select(src, 0, idx, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps({"gather_rows_per_launch": n_gathers, "row_bytes": 64, "table_bytes": rows * 64,
+                      "bytes_read_per_launch": n_gathers * (64 + 8), "bytes_written_per_launch": n_gathers * 64,
                       "launches": 5}))
 
 
@@ -337,6 +364,9 @@ def main():
         return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.gather_calibration:
+        gather_calibration(args.gather_calibration)
         return
     if args.config == 4 and args.gpus == 1:
         sweep_rates(args)

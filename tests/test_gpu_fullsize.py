@@ -22,8 +22,8 @@ against the C oracle on identical seeded inputs.
   recurrent scaling reaches (factor 0: the inputs alone drive the network at ~4.5 Hz).  At
   every point the deterministic forward is bit-exact over 500 ms, the event forward's spike
   trains equal the oracle's for 50 ms from onset and its per-(batch, neuron) counts agree for
-  >= 99.9 %; and a B = 32 BPTT at the 50 Hz factor (one-tick windows, 32-float G rows)
-  against the oracle.
+  >= 99.9 %; and a B = 32 BPTT at the 50 Hz factor (one-tick windows, 32-float G rows) over
+  ticks 300-379 from the carried state, against the oracle.
 
 The oracle runs its OpenMP loops (same bits as one thread).  Each step prints a progress line.
 """
@@ -270,14 +270,19 @@ def test_config4_forward(config4, rate):
 
 def test_config4_bptt_batch32(config4):
     """B = 32: one-tick backward windows, 32-float G rows (8 lanes per column in the
-    type-phased walk); 150 ms from rest at the 50 Hz recurrent factor (onset at 46 ms)."""
+    type-phased walk), at the 50 Hz recurrent factor over 80 ms of the active regime: ticks
+    300-379, from the state the deterministic rollout reaches at tick 300 (bit-exact with the
+    oracle's), so its spike history feeds the first ticks' recurrent dW."""
     cfg, net, lgn, bkg = config4
     cell, tbs = _rec_scaled_cell(net, REC_FACTORS["50Hz"])
-    T = 150
-    lgn, bkg = lgn[:T], bkg[:T]
-    z, v, _ = cell.rollout(lgn, bkg)
+    t_a, T, B = 300, 80, lgn.shape[1]
+    _, _, st = cell.rollout(lgn[:t_a], bkg[:t_a], state=cell.zero_state(B), record_z=False, record_v=False)
+    st0 = dict(zbuf=st[0].cpu().numpy(), v=st[1].cpu().numpy(), r=st[2].cpu().numpy().astype(np.int32),
+               asc=st[3].cpu().numpy(), psc_rise=st[4].cpu().numpy(), psc=st[5].cpu().numpy())
+    lgn, bkg = lgn[t_a:t_a + T], bkg[t_a:t_a + T]
+    z, v, _ = cell.rollout(lgn, bkg, state=[s.clone() for s in st])
     oc = orc.OracleCell(tbs, **ORC_KW)
-    oz, ov, oref, _ = oc.forward(lgn, bkg)
+    oz, ov, oref, _ = oc.forward(lgn, bkg, state=st0)
     np.testing.assert_array_equal(z.cpu().numpy().astype(np.uint8), oz)
     say("config 4 B=32 BPTT window:", int(oz.sum()), "spikes")
     assert oz.sum() > 1_000_000
@@ -285,8 +290,8 @@ def test_config4_bptt_batch32(config4):
     g = {k: t.cpu().numpy() for k, t in cell.backward(gz=torch.tensor(gz, device="cuda")).items()}
     del cell
     say("config 4 B=32 GPU BPTT done; oracle")
-    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz)
-    scale = orc.bptt_abs_scale(tbs, lgn, bkg, oz, oref, ov, gz_loss=gz, **ORC_KW)
+    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz, zbuf0=st0["zbuf"])
+    scale = orc.bptt_abs_scale(tbs, lgn, bkg, oz, oref, ov, gz_loss=gz, zbuf0=st0["zbuf"], **ORC_KW)
     for k in ("rec", "lgn", "bkg"):
         say("config 4 B=32", k, error_summary(g[k], og[k], scale[k]))
         assert np.count_nonzero(og[k]) > 0
