@@ -619,14 +619,52 @@ def main():
         alg_bytes = ((S + (0 if lgn_ahead else tb.lgn.n_syn)) * 4 + tables * (N + 1) * 4 + active * 9
                      + tables * nb * B * N * 4)
         unit_desc = "bytes per forward timestep (deterministic row pull)"
+    # the per-step algorithmic bytes of the path's operations, independent of how the kernels
+    # batch them (the op's backward re-reads its table every step; the forward's push reads each
+    # event's entry): per step, op backward (dz, + dW) 9 B per synapse (entry + syn_id), the
+    # column pointers, dz written, dy read, 8 B per recurrent event (dW read-modify-write); the
+    # GLIF_3 step (3 nb * 4 + 13 B read, 2 nb * 4 + 21 B written per (b, n), + 25 B of constants
+    # per neuron); the adjoint (4 + 8 nb + 13 B read, 4 + 12 nb B written per (b, n)); the push
+    # per source: per active column 12 B (column and row pointers), per event 9 B (post, weight,
+    # type), the currents written once; the row pull 9 B per synapse, the packed spikes, the
+    # currents written.  Times the steps one launch covers, over the launch's columns.
+    e_step = e_rec / max(T, 1)
+    a_step = float(sc_host.sum()) / max(T, 1) * D   # active (b, column) pairs per step, all delays
+    k3 = B * N * ((3 * nb * 4 + 13) + (2 * nb * 4 + 21)) + 25 * N
+    k4_cols = lambda syn, cols: syn * 9 + (cols + 1) * 4 + B * cols * 4
+    k_bytes = None
+    if dominant == "bwd_rec":
+        steps_per_launch = (T - 2) / max(breakdown[dominant]["launches"], 1)
+        k_bytes = steps_per_launch * (k4_cols(s_a, cols_a) + B * N * nb * 4 + e_step * 8)
+        k_desc = (f"per-step op-backward bytes over the launch's {cols_a} columns (9 B per synapse, column "
+                  f"pointers, dz written, dy read, 8 B per recurrent event) x {steps_per_launch:.2f} steps")
+    elif dominant == "adj":
+        k5 = B * N * ((4 + 2 * nb * 4 + 13) + (4 + 3 * nb * 4))
+        k_bytes = Wwin * (k5 + k4_cols(S - s_a, n_cols - cols_a))
+        k_desc = (f"per-step adjoint bytes (4 + 8 nb + 13 B read, 4 + 12 nb B written per (b, n)) + op-backward "
+                  f"bytes over the other {n_cols - cols_a} columns, x {Wwin} steps")
+    elif dominant == "step" and args.mode == "deterministic":
+        k_bytes = k3 + S * 9 + B * D * N / 8 + B * N * nb * 4
+        k_desc = "per-step bytes of the GLIF_3 step + the recurrent row pull (9 B per synapse, packed spikes)"
+    elif dominant == "step":
+        k_bytes = k3 + a_step * 12 + e_step * 9 + B * N * nb * 4
+        k_desc = "per-step bytes of the GLIF_3 step + the recurrent push (12 B per active column, 9 B per event)"
     avg_ms = tot_ms / max(launches, 1)
+    own_bytes, own_desc = alg_bytes, unit_desc
+    if k_bytes is not None:
+        alg_bytes, unit_desc = k_bytes, k_desc
     achieved = alg_bytes / (avg_ms / 1000.0) / 1e9 if avg_ms > 0 else 0.0
+    own_achieved = own_bytes / (avg_ms / 1000.0) / 1e9 if avg_ms > 0 else 0.0
     # measured traffic per kernel class (deterministic mode's fused launch has its own)
     traffic = load_traffic("pull_step" if (dominant == "step" and args.mode == "deterministic") else dominant)
     roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic.get("bytes_per_launch") if traffic else None,
                 "algorithmic_bytes_per_launch": int(alg_bytes), "basis": unit_desc,
+                # the same launch on the bytes this build's kernels cannot avoid (the table read
+                # once per backward window of several steps, G read once, ...)
+                "own_algorithmic_bytes_per_launch": int(own_bytes), "own_basis": own_desc,
+                "own_achieved": round(own_achieved, 1), "own_frac": round(own_achieved / HBM_PEAK_GBS, 4),
                 "avg_launch_us": round(avg_ms * 1000.0, 2), "launches_timed": launches,
                 "launch_sampling": f"every {stride} of the kernel's launches" if stride > 1 else "every launch"}
     if traffic and avg_ms > 0:

@@ -155,3 +155,47 @@ def test_step_backward_of_one_call_alone():
     exp_zb[:, :-N] += g_new["zbuf"][:, N:]
     np.testing.assert_allclose(leaves["zbuf"].grad.cpu().numpy(), exp_zb, rtol=1e-5,
                                atol=1e-5 * np.abs(exp_zb).max())
+
+
+@pytest.mark.parametrize("i", [0, 1, 3, 4, 7, 9])
+def test_call_loop_gradients_irregular_shapes(i):
+    """The per-step backward over the shape sweep's irregular networks (1-200 neurons, 1-9 delay
+    slots, 1-8 receptors, 1-20 types, batch 1-17, both surrogates; case 9 has one delay slot, so
+    the spike buffer has no shifted slots): a loop of calls from rest, its weight gradients and
+    the gradients of its initial state against the float64 restatement, within both bars."""
+    from tests.test_gpu_shapes import _case
+    from v1_glif_model_amd.models import V1Column
+    net, tb, lgn, bkg, kw, ckw = _case(i)
+    T, B = lgn.shape[:2]
+    T = min(T, 12)
+    lgn, bkg = lgn[:T], bkg[:T]
+    oc = OracleCell(tb, **kw)
+    oz, ov, _, _ = oc.forward(lgn, bkg)
+    rng = np.random.default_rng(300 + i)
+    gz = rng.normal(0, 1, oz.shape).astype(np.float32)
+    gv = rng.normal(0, 0.1, oz.shape).astype(np.float32)
+    cell = V1Column(net, mode="deterministic", train_recurrent_per_type=False, train_input=True, **ckw)
+    dev = "cuda"
+    st0 = oc.zero_state(B)
+    leaves = {k: torch.tensor(st0[k], device=dev).requires_grad_(True) for k in ("zbuf", "v", "asc", "psc_rise", "psc")}
+    state = (leaves["zbuf"], leaves["v"], torch.tensor(st0["r"].astype(np.int8), device=dev), leaves["asc"],
+             leaves["psc_rise"], leaves["psc"], None)
+    loss = torch.zeros((), device=dev)
+    zs = []
+    for t in range(T):
+        (z, v), state = cell.call(torch.tensor(lgn[t], dtype=torch.float32, device=dev), state,
+                                  bkg_counts=torch.tensor(bkg[t], device=dev))
+        loss = loss + (z * torch.tensor(gz[t], device=dev)).sum() + (v * torch.tensor(gv[t], device=dev)).sum()
+        zs.append(z.detach())
+    loss.backward()
+    np.testing.assert_array_equal(torch.stack(zs).cpu().numpy().astype(np.uint8), oz)
+    s0 = {k: st0[k].astype(np.float64) for k in st0}
+    tg, _, tg0 = torch_ref.bptt(tb, lgn, bkg, oz, gz, gv, state0=s0, state_grad=True, **kw)
+    sw, _, ss0 = torch_ref.bptt(tb, lgn, bkg, oz, gz, gv, state0=s0, state_grad=True, psi_v=ov, absolute=True,
+                                **kw)
+    got_w = {"rec": cell.recurrent_weight_values.grad, "lgn": cell.input_weight_values.grad,
+             "bkg": cell.bkg_input_weights.grad}
+    for k in ("rec", "lgn", "bkg"):
+        assert_grads_per_element(got_w[k].cpu().numpy(), tg[k], sw[k], what=f"case {i} dW {k}")
+    for k in ("zbuf", "v", "asc", "psc_rise", "psc"):
+        assert_grads_per_element(leaves[k].grad.cpu().numpy(), tg0[k], ss0[k], what=f"case {i} d(initial {k})")
