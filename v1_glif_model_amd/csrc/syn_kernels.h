@@ -403,13 +403,16 @@ __device__ inline void bwd_groups(const GsArgs &a, const Act &act, float *stage,
                 const uint32_t col = group_bcast<LG>(my[u % EPL].x, u / EPL) >> kGsRowBits;
                 const float wu = __uint_as_float(group_bcast<LG>(my[u % EPL].y, u / EPL));
                 const float t0 = wu * gv[u].x, t1 = wu * gv[u].y, t2 = wu * gv[u].z, t3 = wu * gv[u].w;
+                // acc[col] += t with one fma per element: m * t is exactly t or 0, so fma(m, t, acc)
+                // rounds acc + t once, as the add does, and leaves acc alone otherwise (acc starts
+                // at +0 and never becomes -0, so adding a signed zero changes nothing)
 #pragma unroll
                 for (int j = 0; j < kGsCols; ++j) {
-                    const bool m = col == static_cast<uint32_t>(j);
-                    acc[j][0] += m ? t0 : 0.0f;
-                    acc[j][1] += m ? t1 : 0.0f;
-                    acc[j][2] += m ? t2 : 0.0f;
-                    acc[j][3] += m ? t3 : 0.0f;
+                    const float m = col == static_cast<uint32_t>(j) ? 1.0f : 0.0f;
+                    acc[j][0] = __builtin_fmaf(m, t0, acc[j][0]);
+                    acc[j][1] = __builtin_fmaf(m, t1, acc[j][1]);
+                    acc[j][2] = __builtin_fmaf(m, t2, acc[j][2]);
+                    acc[j][3] = __builtin_fmaf(m, t3, acc[j][3]);
                 }
             }
         }
