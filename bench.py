@@ -20,6 +20,7 @@ from __future__ import annotations
 import argparse
 import dataclasses
 import json
+import math
 import os
 import sys
 import time
@@ -492,7 +493,13 @@ def main():
     dominant = max(breakdown, key=lambda k: breakdown[k]["ms_per_step"])
     # a class launched once per tick is sampled (about 50 bracketed launches per step): two
     # event records per launch would cost more host time than the launches themselves
-    stride = max(1, breakdown[dominant]["launches"] // 50)
+    # the stride is coprime with the class's launches per step, so that over the timed steps
+    # every phase of the step is sampled alike (a stride dividing 500 would time the same ticks
+    # every step, tick 0's first-launch work among them)
+    per_step = breakdown[dominant]["launches"]
+    stride = max(1, per_step // 50)
+    while math.gcd(stride, per_step) != 1:
+        stride += 1
     _lib.prof_stride(stride)
     _lib.prof_enable([dominant])
     _lib.prof_collect()
