@@ -55,7 +55,8 @@ def test_pop_names_to_cell_types(tmp_path):
     assert f("e4Rorb") == "L4 Exc" and f("i4Pvalb") == "L4 PV" and f("i23Sst") == "L2/3 SST"
     assert f("e5ET") == "L5 ET" and f("e5ET", ignore_l5e_subtypes=True) == "L5 Exc"
     assert f("i1Htr3a") == "L1 Htr3a" and f("i6Vip") == "L6 VIP" and f("i5Htr3a") == "L5 VIP"
-    assert f("e23Cux2") == "L2/3 Exc"
+    assert f("e23Cux2") == "L2/3 Exc" and f("i23Vip") == "L2/3 VIP" and f("e5IT") == "L5 IT"
+    assert f("e6Ntsr1") == "L6 Exc" and f("i6Sst") == "L6 SST" and f("i1Vip") == "L1 Htr3a"
     nt = tmp_path / "v1_node_types.csv"
     nt.write_text("node_type_id pop_name model_type\n100 e23Cux2 point\n101 i4Pvalb point\n102 e5IT point\n")
     ct = ingest.cell_types_from_node_types(str(nt), np.array([102, 100, 101, 100]))

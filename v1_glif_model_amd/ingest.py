@@ -58,27 +58,23 @@ def load_basis_table(basis_csv: str, synaptic_models_dir: str) -> Tuple[np.ndarr
     return np.asarray(rows, dtype=np.float32), model_to_id
 
 
+# Inhibitory classes of a population name and the subclass each maps to; every other class
+# is excitatory (other_v1_utils.py:23-52).
+_INHIBITORY_SUBCLASS = {"Pvalb": "PV", "Sst": "SST", "Vip": "VIP", "Htr3a": "VIP"}
+
+
 def pop_name_to_cell_type(pop_name: str, ignore_l5e_subtypes: bool = False) -> str:
     """``other_v1_utils.py:23-52``: 'e4Rorb' -> 'L4 Exc', 'i4Pvalb' -> 'L4 PV',
     'i23Sst' -> 'L2/3 SST', 'e5ET' -> 'L5 ET' (or 'L5 Exc' with ignore_l5e_subtypes),
-    layer 1 -> 'L1 Htr3a'."""
-    shift = 0
-    layer = pop_name[1]
-    if layer == "2":
-        layer, shift = "2/3", 1
-    elif layer == "1":
+    layer 1 -> 'L1 Htr3a'.  A name is <e|i><layer><class>; layer 2/3 is written with two
+    digits, every other layer with one."""
+    layer_char = pop_name[1]
+    if layer_char == "1":
         return "L1 Htr3a"
-    cls = pop_name[2 + shift:]
-    if cls == "Pvalb":
-        sub = "PV"
-    elif cls == "Sst":
-        sub = "SST"
-    elif cls in ("Vip", "Htr3a"):
-        sub = "VIP"
-    elif layer == "5" and not ignore_l5e_subtypes:
-        sub = cls
-    else:
-        sub = "Exc"
+    layer, cls = ("2/3", pop_name[3:]) if layer_char == "2" else (layer_char, pop_name[2:])
+    sub = _INHIBITORY_SUBCLASS.get(cls)
+    if sub is None:   # excitatory: layer 5 keeps its subtype unless asked not to
+        sub = cls if layer == "5" and not ignore_l5e_subtypes else "Exc"
     return f"L{layer} {sub}"
 
 
