@@ -100,9 +100,10 @@ int glif_syn_fwd(const glif_table *t, const float *z, int32_t B, int32_t counts,
  * the same arguments, results and errors minus the workspace, whose place takes a static
  * device array of GLIF_NOALLOC_SCRATCH_BYTES in the library -- one per GPU the library runs
  * on, held until the process ends, its address looked up on the first call on each device.
- * The forward needs about 12 bytes of scratch per column (n_cols): 32 MiB covers tables of up
- * to ~2.7M columns (the 230k-neuron, 5-delay recurrent table has 1.15M); larger ones fail with
- * GLIF_ENOMEM.  Calls on one GPU share the array: calls that overlap on one GPU (other
+ * The forward needs about 4 bytes of scratch per column (n_cols; the deterministic row pull's
+ * batch masks and activity bits -- the event push uses none, but the limit holds for both
+ * modes): 32 MiB covers tables of up to ~8M columns (the 230k-neuron, 5-delay recurrent table
+ * has 1.15M); larger ones fail with GLIF_ENOMEM.  Calls on one GPU share the array: calls that overlap on one GPU (other
  * streams, other threads) race, so serialise them.  The stream must belong to the calling
  * thread's current device.  No allocation, no synchronisation. */
 #define GLIF_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)

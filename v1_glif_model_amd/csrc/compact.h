@@ -19,9 +19,4 @@ int build_window_mask_lists(const uint8_t *x, int32_t T, int32_t B, int64_t C, i
                             int32_t n_windows, int64_t *row_off, int32_t *pre, uint32_t *mask,
                             void *scratch, hipStream_t s);
 
-// For a dense z [B][C] float: ascending list of columns with any z[b][c] > 0 and
-// their batch masks; row_off [2] int64 = {0, count}.
-int build_col_mask_list_f32(const float *z, int32_t B, int64_t C, int64_t *row_off, int32_t *cols,
-                            uint32_t *mask, void *scratch, hipStream_t s);
-
 }  // namespace glif

@@ -179,23 +179,6 @@ struct SinkPreMask {
 };
 
 // Dense [B][C] float input, one row: column c is active when any z[b][c] > 0.
-struct SrcColMaskF32 {
-    const float *z;
-    int32_t B;
-    int64_t C;
-    __device__ uint32_t eval(int64_t, int64_t c) const {
-        uint32_t m = 0;
-        for (int b = 0; b < B; ++b) m |= (z[b * C + c] > 0.0f ? 1u : 0u) << b;
-        return m;
-    }
-};
-
-int build_col_mask_list_f32(const float *z, int32_t B, int64_t C, int64_t *row_off, int32_t *cols,
-                            uint32_t *mask, void *scratch, hipStream_t s) {
-    return run_compact(SrcColMaskF32{z, B, C}, SinkPreMask{cols, mask}, 1, C, row_off, nullptr,
-                       scratch, s);
-}
-
 // Backward windows over inputs [T][B][C]: window j covers the reverse steps
 // s0 - w (w < nw) with t0 = T-1-j*W, s0 = t0-2, nw = min(W, t0-1); column c is
 // active when any x[s0-w][b][c] > 0 and its mask has bit w*B + b set for those.

@@ -44,71 +44,88 @@ __global__ void __launch_bounds__(kBlock)
     for (int r = 0; r < nb; ++r) dst[r] = acc[r];
 }
 
-// Event push over a (column, batch-mask) list.
-template <int L, bool COUNTS>
+// Event push straight from z [B][n_cols]: a wave per 64 consecutive columns builds each
+// column's batch mask (z > 0, the test of tf.where at models.py:128-130), and all 64 lanes
+// push the wave's active columns one after another.  No column list, no count pass.
+template <bool COUNTS>
 __global__ void __launch_bounds__(kBlock)
-    k_syn_push_list(const int32_t *__restrict__ cols, const uint32_t *__restrict__ masks,
-                    const int64_t *__restrict__ n_items, const float *__restrict__ z, int64_t n_cols,
-                    const int32_t *__restrict__ col_ptr, const uint32_t *__restrict__ ps,
-                    const float *__restrict__ w, const float *__restrict__ basis, int n_types, int nb,
-                    int32_t n_post, float *__restrict__ I) {
+    k_syn_push_scan(const float *__restrict__ z, int32_t B, int64_t n_cols, const int32_t *__restrict__ col_ptr,
+                    const uint32_t *__restrict__ ps, const float *__restrict__ w, const float *__restrict__ basis,
+                    int n_types, int nb, int32_t n_post, float *__restrict__ I) {
     extern __shared__ float basis_lds[];
     load_basis_lds(basis_lds, basis, n_types * nb);
-    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int lane_s = threadIdx.x % L;
-    const int64_t n_subs = static_cast<int64_t>(gridDim.x) * blockDim.x / L;
-    const int64_t total = *n_items;
-    for (int64_t it = gt / L; it < total; it += n_subs) {
-        const int32_t c = cols[it];
-        const uint32_t m = masks[it];
-        if (COUNTS)
-            push_column<L>(lane_s, col_ptr[c], col_ptr[c + 1], m, MultF32{z + c, n_cols}, ps, w,
-                           basis_lds, nb, static_cast<int64_t>(n_post) * nb, nb, 1, I);
-        else
-            push_column<L>(lane_s, col_ptr[c], col_ptr[c + 1], m, MultOne{}, ps, w, basis_lds, nb,
-                           static_cast<int64_t>(n_post) * nb, nb, 1, I);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t n_words = (n_cols + kWave - 1) / kWave;
+    const int64_t waves = static_cast<int64_t>(gridDim.x) * (blockDim.x / kWave);
+    const int64_t u0 = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    for (int64_t u = u0; u < n_words; u += waves) {
+        const int64_t c = u * kWave + lane;
+        uint32_t m = 0u;
+        if (c < n_cols)
+            for (int b = 0; b < B; ++b) m |= (z[b * n_cols + c] > 0.0f ? 1u : 0u) << b;
+        uint64_t act = __ballot(m != 0u);
+        while (act) {
+            const int l = __builtin_ctzll(act);
+            act &= act - 1ull;
+            const uint32_t ml = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), l));
+            const int64_t cl = u * kWave + l;
+            if (COUNTS)
+                push_column<kWave>(lane, col_ptr[cl], col_ptr[cl + 1], ml, MultF32{z + cl, n_cols}, ps, w,
+                                   basis_lds, nb, static_cast<int64_t>(n_post) * nb, nb, 1, I);
+            else
+                push_column<kWave>(lane, col_ptr[cl], col_ptr[cl + 1], ml, MultOne{}, ps, w, basis_lds, nb,
+                                   static_cast<int64_t>(n_post) * nb, nb, 1, I);
+        }
     }
 }
 
 // ---------------------------------------------------------------- backward ----
+// G rows from dy [B][n_post][nb]: a thread per row quarter (four batch entries of one G row,
+// one 16-byte store; consecutive threads write consecutive quarters, so a wave's stores are
+// contiguous), padding entries b >= B written +0 (no separate fill).  Type-major rows:
+// G[s * n_post + post][b] = sum_r dy[b][post][r] * basis[s][r]; a table's own compact rows
+// (COMPACT): G[post * rows + q][b] with s = gtype[post][q], +0 past the post's types.  Each
+// element sums r ascending from dy[0] * bs[0], one rounding per product and per add.
+template <bool COMPACT>
 __global__ void __launch_bounds__(kBlock)
-    k_make_G(const float *__restrict__ dy, int32_t B, int32_t n_post, int Bp,
-             const float *__restrict__ basis, int n_types, int nb, float *__restrict__ G) {
+    k_make_G(const float *__restrict__ dy, int32_t B, int32_t n_post, int Bp, const float *__restrict__ basis,
+             int n_types, int nb, const uint8_t *__restrict__ gtype, int rows, float *__restrict__ G) {
     extern __shared__ float basis_lds[];
     load_basis_lds(basis_lds, basis, n_types * nb);
-    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (gt >= static_cast<int64_t>(B) * n_post) return;
-    const int b = static_cast<int>(gt / n_post);
-    const int64_t n = gt % n_post;
-    float d[kMaxBasis];
-    for (int r = 0; r < nb; ++r) d[r] = dy[gt * nb + r];
-    write_G(G, n, b, Bp, d, basis_lds, n_types, nb, n_post);
-}
-
-// G over a table's own compact rows: G[n * rows + q][b] = sum_r dy[b][n][r] * basis[gtype[n][q]][r]
-// (sequential r as write_G), 0 past the post's types.
-__global__ void __launch_bounds__(kBlock)
-    k_make_G_compact(const float *__restrict__ dy, int32_t B, int32_t n_post, int Bp,
-                     const float *__restrict__ basis, int n_types, int nb, const uint8_t *__restrict__ gtype,
-                     int rows, float *__restrict__ G) {
-    extern __shared__ float basis_lds[];
-    load_basis_lds(basis_lds, basis, n_types * nb);
-    const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (gt >= static_cast<int64_t>(B) * n_post) return;
-    const int b = static_cast<int>(gt / n_post);
-    const int64_t n = gt % n_post;
-    float d[kMaxBasis];
-    for (int r = 0; r < nb; ++r) d[r] = dy[gt * nb + r];
-    for (int q = 0; q < rows; ++q) {
-        const int s = gtype[n * rows + q];
-        float e = 0.0f;
-        if (s != 0xFF) {
-            const float *bs = basis_lds + s * nb;
-            e = d[0] * bs[0];
-            for (int r = 1; r < nb; ++r) e = e + d[r] * bs[r];
-        }
-        G[(n * rows + q) * Bp + b] = e;
+    const int nrow = COMPACT ? rows : n_types;
+    const int nq = Bp / 4;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(n_post) * nrow * nq) return;
+    const int b0 = static_cast<int>(i % nq) * 4;
+    int64_t n, row;
+    int s;
+    if (COMPACT) {   // row quarters in memory order: post, then rank, then quarter
+        const int64_t pq = i / nq;
+        n = pq / rows;
+        row = pq;
+        s = gtype[pq];
+    } else {         // type, then post, then quarter
+        const int64_t rq = i / nq;
+        s = static_cast<int>(rq / n_post);
+        n = rq - static_cast<int64_t>(s) * n_post;
+        row = rq;
     }
+    float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (!COMPACT || s != 0xFF) {
+        const float *bs = basis_lds + s * nb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (b0 + j >= B) break;
+            const float *d = dy + (static_cast<int64_t>(b0 + j) * n_post + n) * nb;
+            float x = d[0] * bs[0];
+#pragma unroll
+            for (int r = 1; r < kMaxBasis; ++r)
+                if (r < nb) x = x + d[r] * bs[r];
+            e[j] = x;
+        }
+    }
+    *reinterpret_cast<float4 *>(G + row * Bp + b0) = make_float4(e[0], e[1], e[2], e[3]);
 }
 
 // Batch masks and "active in some batch entry" bitmaps of a dense z [B][n_cols] in the
@@ -138,10 +155,22 @@ __global__ void __launch_bounds__(kBlock) k_syn_bwd_cols(ColArgs a, ActDense act
     bwd_cols<LG, 2>(a, act);
 }
 
+// The grouped dz walk (the first walk_blocks workgroups) beside the zero fill of the dense dW
+// (the rest, grid-stride; the weight-gradient pass after this launch writes the active
+// synapses): the walk is bound by its gathers' latency, the fill by stores, and one launch
+// overlaps them.
 template <int LG>
-__global__ void __launch_bounds__(kBlock) k_syn_bwd_gs(GsArgs a, ActDense act) {
+__global__ void __launch_bounds__(kBlock)
+    k_syn_bwd_gs(GsArgs a, ActDense act, int walk_blocks, float *__restrict__ fill, int64_t n_fill) {
     __shared__ float stage[kBlock / kWave * kGsStage];
-    bwd_groups<LG>(a, act, stage, blockIdx.x);
+    if (static_cast<int>(blockIdx.x) < walk_blocks) {
+        bwd_groups<LG>(a, act, stage, blockIdx.x);
+        return;
+    }
+    const int64_t stride = static_cast<int64_t>(gridDim.x - walk_blocks) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x - walk_blocks) * blockDim.x + threadIdx.x; i < n_fill;
+         i += stride)
+        fill[i] = 0.0f;
 }
 
 // dW of the active columns (z[b][c] > 0) next to the grouped dz walk: a wave per 64
@@ -236,11 +265,7 @@ int batch_pad(int B) { return B <= 4 ? 4 : (B <= 8 ? 8 : (B <= 16 ? 16 : 32)); }
 struct SynWs {
     uint32_t *cm;      // [n_slots * pre_pad] batch masks (deterministic forward)
     uint64_t *cbits;   // [n_slots * pre_pad / 64] activity bitmaps
-    int64_t *row_off;
-    int32_t *cols;
-    uint32_t *masks;
-    float *G;
-    void *scratch;
+    float *G;          // the custom gradient's projection
 };
 
 // with_G: the backward's projection G too (the forward does not use it)
@@ -250,10 +275,6 @@ static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes, bool 
     const int64_t pre_pad = (static_cast<int64_t>(t->n_pre) + 63) / 64 * 64;
     w.cm = cv.take<uint32_t>(static_cast<size_t>(t->n_slots) * pre_pad);
     w.cbits = cv.take<uint64_t>(static_cast<size_t>(t->n_slots) * pre_pad / 64);
-    w.row_off = cv.take<int64_t>(2);
-    w.cols = cv.take<int32_t>(t->n_cols);
-    w.masks = cv.take<uint32_t>(t->n_cols);
-    w.scratch = cv.take<char>(compact_scratch_bytes(1, t->n_cols));
     // G: a row per (type, post), or per (post, own type) with the table's compact rows
     const int rows = t->og.rows ? t->og.rows : t->n_types;
     if (with_G) w.G = cv.take<float>(static_cast<size_t>(t->n_post) * rows * batch_pad(B));
@@ -320,18 +341,14 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
     }
     int rc = launch_fill_u32(I, 0u, static_cast<size_t>(nI) * t->n_basis, s);
     if (rc) return rc;
-    rc = build_col_mask_list_f32(z, B, t->n_cols, w.row_off, w.cols, w.masks, w.scratch, s);
-    if (rc) return rc;
-    const int L = sub_wave_for(t);
-    dim3 grid(grid_subwaves(std::min<int64_t>(t->n_cols, 262144), L));
-#define GLIF_PUSH(LL, CC)                                                                           \
-    hipLaunchKernelGGL((k_syn_push_list<LL, CC>), grid, dim3(kBlock), lds, s, w.cols, w.masks,      \
-                       w.row_off + 1, z, t->n_cols, t->col_ptr, t->ps, t->w_col, t->basis,          \
-                       t->n_types, t->n_basis, t->n_post, I)
-    if (L == 16) { if (counts) GLIF_PUSH(16, true); else GLIF_PUSH(16, false); }
-    else if (L == 32) { if (counts) GLIF_PUSH(32, true); else GLIF_PUSH(32, false); }
-    else { if (counts) GLIF_PUSH(64, true); else GLIF_PUSH(64, false); }
-#undef GLIF_PUSH
+    const dim3 grid(static_cast<unsigned>(std::max<int64_t>(
+        1, std::min<int64_t>(ceil_div(ceil_div(t->n_cols, kWave), kBlock / kWave), 32768))));
+    if (counts)
+        hipLaunchKernelGGL(k_syn_push_scan<true>, grid, dim3(kBlock), lds, s, z, B, t->n_cols, t->col_ptr, t->ps,
+                           t->w_col, t->basis, t->n_types, t->n_basis, t->n_post, I);
+    else
+        hipLaunchKernelGGL(k_syn_push_scan<false>, grid, dim3(kBlock), lds, s, z, B, t->n_cols, t->col_ptr, t->ps,
+                           t->w_col, t->basis, t->n_types, t->n_basis, t->n_post, I);
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;
 }
@@ -387,8 +404,9 @@ int glif_syn_fwd(const glif_table *tt, const float *z, int32_t B, int32_t counts
     if (mode != GLIF_MODE_EVENT && mode != GLIF_MODE_DETERMINISTIC) return fail(GLIF_EINVAL, "unknown mode");
     const Table *t = reinterpret_cast<const Table *>(tt);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // the dense-row pull (counts, or a table without the chunk form) needs no workspace
-    const bool needs_ws = mode == GLIF_MODE_EVENT || (!counts && t->pidx && t->chunk_desc);
+    // only the chunk pull (deterministic, spikes, a table with the chunk form) uses the
+    // workspace: the event push and the dense-row pull need none
+    const bool needs_ws = mode == GLIF_MODE_DETERMINISTIC && !counts && t->pidx && t->chunk_desc;
     if (needs_ws && (!ws || ws_bytes < glif_syn_workspace(tt, B))) return fail(GLIF_ENOMEM, "workspace too small");
     ProfScope prof(kProfSynFwd, s);
     return syn_fwd(t, z, B, counts, mode, I, carve_syn(ws, t, B, nullptr), s);
@@ -433,29 +451,33 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     ProfScope prof(kProfSynBwd, s);
     const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     int rc;
-    if (B < Bp && (rc = launch_fill_u32(w.G, 0u, static_cast<size_t>(t->n_post) * rows * Bp, s)))
-        return rc;
-    const int64_t nI = static_cast<int64_t>(B) * t->n_post;
+    const dim3 g_grid(ceil_div(static_cast<int64_t>(t->n_post) * rows * (Bp / 4), kBlock));
     if (cmp)
-        hipLaunchKernelGGL(k_make_G_compact, dim3(ceil_div(nI, kBlock)), dim3(kBlock), lds, s, dy, B, t->n_post, Bp,
-                           t->basis, t->n_types, t->n_basis, oc.gtype, rows, w.G);
+        hipLaunchKernelGGL(k_make_G<true>, g_grid, dim3(kBlock), lds, s, dy, B, t->n_post, Bp, t->basis,
+                           t->n_types, t->n_basis, oc.gtype, rows, w.G);
     else
-        hipLaunchKernelGGL(k_make_G, dim3(ceil_div(nI, kBlock)), dim3(kBlock), lds, s, dy, B, t->n_post, Bp,
-                           t->basis, t->n_types, t->n_basis, w.G);
+        hipLaunchKernelGGL(k_make_G<false>, g_grid, dim3(kBlock), lds, s, dy, B, t->n_post, Bp, t->basis,
+                           t->n_types, t->n_basis, nullptr, rows, w.G);
     GLIF_HIP(hipGetLastError());
-    // one pass writes every active synapse's dW once, in reference order; the rest stay 0
-    if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
     if ((cmp ? oc.n_gs : t->n_gs) && (Bp == 8 || Bp == 16)) {
-        // the grouped row-sliced walk for dz, then the active columns' dW
+        // the grouped row-sliced walk for dz beside the zero fill of dW, then the active
+        // columns' dW (every active synapse's written once, in reference order)
         ActDense act{z, dz, t->n_cols, counts};
         if (dz) {
             GsArgs ga{t->n_cols, (t->n_cols + kGsCols - 1) / kGsCols, B, cmp ? oc.gs_seg : t->gs_seg,
                       cmp ? oc.gs_pw : t->gs_pw, w.G};
             const int LG = Bp / 4;
-            const dim3 grid(ceil_div(t->n_groups * LG, kBlock));
-            if (LG == 2) hipLaunchKernelGGL(k_syn_bwd_gs<2>, grid, dim3(kBlock), 0, s, ga, act);
-            else hipLaunchKernelGGL(k_syn_bwd_gs<4>, grid, dim3(kBlock), 0, s, ga, act);
+            const int walk_blocks = static_cast<int>(ceil_div(t->n_groups * LG, kBlock));
+            const int fill_blocks = dw && t->n_syn ? 256 : 0;
+            const dim3 grid(walk_blocks + fill_blocks);
+            const int64_t n_fill = dw ? t->n_syn : 0;
+            if (LG == 2)
+                hipLaunchKernelGGL(k_syn_bwd_gs<2>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, dw, n_fill);
+            else
+                hipLaunchKernelGGL(k_syn_bwd_gs<4>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, dw, n_fill);
             GLIF_HIP(hipGetLastError());
+        } else if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) {
+            return rc;
         }
         if (dw) {
             SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->col_ptr,
@@ -465,6 +487,8 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
         }
         return GLIF_OK;
     }
+    // the type-phased column walk writes the active columns' synapses; the rest stay 0
+    if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
     ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, cmp ? oc.ph_pw : t->ph_pw, w.G, dz ? 1 : 0, dw,
                t->ph_order, cmp ? 1 : 0};
     ActDense act{z, dz, t->n_cols, counts};
