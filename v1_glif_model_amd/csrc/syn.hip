@@ -81,51 +81,91 @@ __global__ void __launch_bounds__(kBlock)
 }
 
 // ---------------------------------------------------------------- backward ----
-// G rows from dy [B][n_post][nb]: a thread per row quarter (four batch entries of one G row,
-// one 16-byte store; consecutive threads write consecutive quarters, so a wave's stores are
-// contiguous), padding entries b >= B written +0 (no separate fill).  Type-major rows:
-// G[s * n_post + post][b] = sum_r dy[b][post][r] * basis[s][r]; a table's own compact rows
-// (COMPACT): G[post * rows + q][b] with s = gtype[post][q], +0 past the post's types.  Each
-// element sums r ascending from dy[0] * bs[0], one rounding per product and per add.
+// G rows from dy [B][n_post][nb].  A workgroup takes P consecutive posts: it copies their dy
+// into LDS (coalesced), then each thread writes row quarters (four batch entries of one G row,
+// one 16-byte store; consecutive threads write consecutive quarters), padding entries b >= B
+// written +0 (no separate fill).  Type-major rows: G[s * n_post + post][b] =
+// sum_r dy[b][post][r] * basis[s][r]; a table's own compact rows (COMPACT): G[post * rows + q][b]
+// with s = gtype[post][q], +0 past the post's types.  Each element sums r ascending from
+// dy[0] * bs[0], one rounding per product and per add.
+// The workgroups from g_blocks on zero the dense dW instead (grid-stride), which the
+// weight-gradient pass after this launch writes for the active synapses.
 template <bool COMPACT>
 __global__ void __launch_bounds__(kBlock)
     k_make_G(const float *__restrict__ dy, int32_t B, int32_t n_post, int Bp, const float *__restrict__ basis,
-             int n_types, int nb, const uint8_t *__restrict__ gtype, int rows, float *__restrict__ G) {
-    extern __shared__ float basis_lds[];
-    load_basis_lds(basis_lds, basis, n_types * nb);
-    const int nrow = COMPACT ? rows : n_types;
-    const int nq = Bp / 4;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= static_cast<int64_t>(n_post) * nrow * nq) return;
-    const int b0 = static_cast<int>(i % nq) * 4;
-    int64_t n, row;
-    int s;
-    if (COMPACT) {   // row quarters in memory order: post, then rank, then quarter
-        const int64_t pq = i / nq;
-        n = pq / rows;
-        row = pq;
-        s = gtype[pq];
-    } else {         // type, then post, then quarter
-        const int64_t rq = i / nq;
-        s = static_cast<int>(rq / n_post);
-        n = rq - static_cast<int64_t>(s) * n_post;
-        row = rq;
+             int n_types, int nb, const uint8_t *__restrict__ gtype, int rows, int P, float *__restrict__ G,
+             int g_blocks, float *__restrict__ fill, int64_t n_fill) {
+    if (static_cast<int>(blockIdx.x) >= g_blocks) {
+        const int64_t stride = static_cast<int64_t>(gridDim.x - g_blocks) * blockDim.x;
+        for (int64_t i = static_cast<int64_t>(blockIdx.x - g_blocks) * blockDim.x + threadIdx.x; i < n_fill;
+             i += stride)
+            fill[i] = 0.0f;
+        return;
     }
-    float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (!COMPACT || s != 0xFF) {
-        const float *bs = basis_lds + s * nb;
+    extern __shared__ float lds_f[];
+    float *basis_lds = lds_f;
+    float *tile = lds_f + ((n_types * nb + 3) & ~3);   // [B][P][nb]
+    for (int i = threadIdx.x; i < n_types * nb; i += blockDim.x) basis_lds[i] = basis[i];
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * P;
+    const int np = static_cast<int>(min(static_cast<int64_t>(P), n_post - n0));
+    const int span = np * nb, total = B * span;
+    for (int base = 0; base < total; base += 8 * static_cast<int>(blockDim.x)) {
+        float v[8];   // the loads of a round go out together
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (b0 + j >= B) break;
-            const float *d = dy + (static_cast<int64_t>(b0 + j) * n_post + n) * nb;
-            float x = d[0] * bs[0];
+        for (int k = 0; k < 8; ++k) {
+            const int i = base + k * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+            const int b = i / span;
+            v[k] = i < total ? dy[(static_cast<int64_t>(b) * n_post + n0) * nb + (i - b * span)] : 0.0f;
+        }
 #pragma unroll
-            for (int r = 1; r < kMaxBasis; ++r)
-                if (r < nb) x = x + d[r] * bs[r];
-            e[j] = x;
+        for (int k = 0; k < 8; ++k) {
+            const int i = base + k * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+            const int b = i / span;
+            if (i < total) tile[b * P * nb + (i - b * span)] = v[k];
         }
     }
-    *reinterpret_cast<float4 *>(G + row * Bp + b0) = make_float4(e[0], e[1], e[2], e[3]);
+    __syncthreads();
+    const int nrow = COMPACT ? rows : n_types;
+    const int nq = Bp / 4;
+    const int items = nrow * np * nq;
+    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+        const int b0 = (it % nq) * 4;
+        int p, s;
+        int64_t row;
+        if (COMPACT) {   // memory order: post, then rank, then quarter
+            const int pq = it / nq;
+            p = pq / rows;
+            row = (n0 + p) * rows + (pq - p * rows);
+            s = gtype[row];
+        } else {         // type, then post, then quarter
+            const int sp = it / nq;
+            s = sp / np;
+            p = sp - s * np;
+            row = static_cast<int64_t>(s) * n_post + n0 + p;
+        }
+        float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (!COMPACT || s != 0xFF) {
+            const float *bs = basis_lds + s * nb;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (b0 + j >= B) break;
+                const float *d = tile + ((b0 + j) * P + p) * nb;
+                float x = d[0] * bs[0];
+#pragma unroll
+                for (int r = 1; r < kMaxBasis; ++r)
+                    if (r < nb) x = x + d[r] * bs[r];
+                e[j] = x;
+            }
+        }
+        *reinterpret_cast<float4 *>(G + row * Bp + b0) = make_float4(e[0], e[1], e[2], e[3]);
+    }
+}
+
+// Posts per workgroup of k_make_G: the dy tile holds at most 2048 floats.
+static int make_G_posts(int B, int nb) {
+    int P = 64;
+    while (P > 1 && B * P * nb > 2048) P >>= 1;
+    return P;
 }
 
 // Batch masks and "active in some batch entry" bitmaps of a dense z [B][n_cols] in the
@@ -155,24 +195,6 @@ __global__ void __launch_bounds__(kBlock) k_syn_bwd_cols(ColArgs a, ActDense act
     bwd_cols<LG, 2>(a, act);
 }
 
-// The grouped dz walk (the first walk_blocks workgroups) beside the zero fill of the dense dW
-// (the rest, grid-stride; the weight-gradient pass after this launch writes the active
-// synapses): the walk is bound by its gathers' latency, the fill by stores, and one launch
-// overlaps them.
-template <int LG>
-__global__ void __launch_bounds__(kBlock)
-    k_syn_bwd_gs(GsArgs a, ActDense act, int walk_blocks, float *__restrict__ fill, int64_t n_fill) {
-    __shared__ float stage[kBlock / kWave * kGsStage];
-    if (static_cast<int>(blockIdx.x) < walk_blocks) {
-        bwd_groups<LG>(a, act, stage, blockIdx.x);
-        return;
-    }
-    const int64_t stride = static_cast<int64_t>(gridDim.x - walk_blocks) * blockDim.x;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x - walk_blocks) * blockDim.x + threadIdx.x; i < n_fill;
-         i += stride)
-        fill[i] = 0.0f;
-}
-
 // dW of the active columns (z[b][c] > 0) next to the grouped dz walk: a wave per 64
 // consecutive columns finds each column's batch mask, then 16-lane sub-groups walk the
 // column-grouped synapses of four active columns at a time and write each synapse's dW
@@ -189,10 +211,10 @@ struct SynDwArgs {
     float *dw;  // reference order, zero-filled by the caller
 };
 
-__global__ void __launch_bounds__(kBlock) k_syn_bwd_dw(SynDwArgs a) {
+// Workgroup bid of the pass: a wave per 64 consecutive columns.
+__device__ inline void syn_dw_body(const SynDwArgs &a, int64_t bid) {
     const int lane = threadIdx.x % kWave;
-    const int64_t c0 =
-        static_cast<int64_t>(blockIdx.x) * blockDim.x + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave;
+    const int64_t c0 = bid * blockDim.x + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave;
     if (c0 >= a.n_cols) return;  // the whole wave leaves together
     const int64_t c = c0 + lane;
     const int64_t cl = min(c, a.n_cols - 1);
@@ -247,6 +269,18 @@ __global__ void __launch_bounds__(kBlock) k_syn_bwd_dw(SynDwArgs a) {
                 if (k0 + 16 * u + sl < chi) a.dw[a.order[k0 + 16 * u + sl]] = d[u];
         }
     }
+}
+
+__global__ void __launch_bounds__(kBlock) k_syn_bwd_dw(SynDwArgs a) { syn_dw_body(a, blockIdx.x); }
+
+// The grouped dz walk (the first walk_blocks workgroups) beside the weight-gradient pass of
+// the active columns (the rest): both read G only, the walk is bound by its gathers' latency,
+// and one launch overlaps them.
+template <int LG>
+__global__ void __launch_bounds__(kBlock) k_syn_bwd_gs(GsArgs a, ActDense act, int walk_blocks, SynDwArgs da) {
+    __shared__ float stage[kBlock / kWave * kGsStage];
+    if (static_cast<int>(blockIdx.x) < walk_blocks) bwd_groups<LG>(a, act, stage, blockIdx.x);
+    else syn_dw_body(da, blockIdx.x - walk_blocks);
 }
 
 int sub_wave_for(const Table *t) {  // lanes per column: ~ the mean column length
@@ -449,42 +483,38 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     if (static_cast<int64_t>(rows) * t->n_post * Bp * 4 >= (int64_t(1) << 32))
         return fail(GLIF_ERANGE, "G rows per post * n_post * padded batch * 4 bytes must be < 4 GiB");
     ProfScope prof(kProfSynBwd, s);
-    const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     int rc;
-    const dim3 g_grid(ceil_div(static_cast<int64_t>(t->n_post) * rows * (Bp / 4), kBlock));
+    const bool grouped = (cmp ? oc.n_gs : t->n_gs) && (Bp == 8 || Bp == 16);
+    // G, with the zero fill of dW beside it when the grouped path's weight-gradient pass
+    // writes only the active synapses
+    const int gP = make_G_posts(B, t->n_basis);
+    const int g_blocks = static_cast<int>(ceil_div(static_cast<int64_t>(t->n_post), gP));
+    const int fill_blocks = grouped && dw && t->n_syn ? 256 : 0;
+    const int64_t n_fill = fill_blocks ? t->n_syn : 0;
+    const dim3 g_grid(g_blocks + fill_blocks);
+    const size_t g_lds = sizeof(float) * (((t->n_types * t->n_basis + 3) & ~3) + static_cast<size_t>(B) * gP * t->n_basis);
     if (cmp)
-        hipLaunchKernelGGL(k_make_G<true>, g_grid, dim3(kBlock), lds, s, dy, B, t->n_post, Bp, t->basis,
-                           t->n_types, t->n_basis, oc.gtype, rows, w.G);
+        hipLaunchKernelGGL(k_make_G<true>, g_grid, dim3(kBlock), g_lds, s, dy, B, t->n_post, Bp, t->basis,
+                           t->n_types, t->n_basis, oc.gtype, rows, gP, w.G, g_blocks, dw, n_fill);
     else
-        hipLaunchKernelGGL(k_make_G<false>, g_grid, dim3(kBlock), lds, s, dy, B, t->n_post, Bp, t->basis,
-                           t->n_types, t->n_basis, nullptr, rows, w.G);
+        hipLaunchKernelGGL(k_make_G<false>, g_grid, dim3(kBlock), g_lds, s, dy, B, t->n_post, Bp, t->basis,
+                           t->n_types, t->n_basis, nullptr, rows, gP, w.G, g_blocks, dw, n_fill);
     GLIF_HIP(hipGetLastError());
-    if ((cmp ? oc.n_gs : t->n_gs) && (Bp == 8 || Bp == 16)) {
-        // the grouped row-sliced walk for dz beside the zero fill of dW, then the active
-        // columns' dW (every active synapse's written once, in reference order)
+    if (grouped) {
+        // the grouped row-sliced walk for dz beside the active columns' dW (every active
+        // synapse's written once, in reference order)
         ActDense act{z, dz, t->n_cols, counts};
-        if (dz) {
-            GsArgs ga{t->n_cols, (t->n_cols + kGsCols - 1) / kGsCols, B, cmp ? oc.gs_seg : t->gs_seg,
-                      cmp ? oc.gs_pw : t->gs_pw, w.G};
-            const int LG = Bp / 4;
-            const int walk_blocks = static_cast<int>(ceil_div(t->n_groups * LG, kBlock));
-            const int fill_blocks = dw && t->n_syn ? 256 : 0;
-            const dim3 grid(walk_blocks + fill_blocks);
-            const int64_t n_fill = dw ? t->n_syn : 0;
-            if (LG == 2)
-                hipLaunchKernelGGL(k_syn_bwd_gs<2>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, dw, n_fill);
-            else
-                hipLaunchKernelGGL(k_syn_bwd_gs<4>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, dw, n_fill);
-            GLIF_HIP(hipGetLastError());
-        } else if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) {
-            return rc;
-        }
-        if (dw) {
-            SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->col_ptr,
-                         cmp ? oc.ps : t->ps, t->order, w.G, dw};
-            hipLaunchKernelGGL(k_syn_bwd_dw, dim3(ceil_div(t->n_cols, kBlock)), dim3(kBlock), 0, s, da);
-            GLIF_HIP(hipGetLastError());
-        }
+        GsArgs ga{t->n_cols, (t->n_cols + kGsCols - 1) / kGsCols, B, cmp ? oc.gs_seg : t->gs_seg,
+                  cmp ? oc.gs_pw : t->gs_pw, w.G};
+        SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->col_ptr,
+                     cmp ? oc.ps : t->ps, t->order, w.G, dw};
+        const int LG = Bp / 4;
+        const int walk_blocks = dz ? static_cast<int>(ceil_div(t->n_groups * LG, kBlock)) : 0;
+        const int dw_blocks = dw ? static_cast<int>(ceil_div(t->n_cols, kBlock)) : 0;
+        const dim3 grid(walk_blocks + dw_blocks);
+        if (LG == 2) hipLaunchKernelGGL(k_syn_bwd_gs<2>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, da);
+        else hipLaunchKernelGGL(k_syn_bwd_gs<4>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, da);
+        GLIF_HIP(hipGetLastError());
         return GLIF_OK;
     }
     // the type-phased column walk writes the active columns' synapses; the rest stay 0
