@@ -271,7 +271,6 @@ __device__ inline void syn_dw_body(const SynDwArgs &a, int64_t bid) {
     }
 }
 
-__global__ void __launch_bounds__(kBlock) k_syn_bwd_dw(SynDwArgs a) { syn_dw_body(a, blockIdx.x); }
 
 // The grouped dz walk (the first walk_blocks workgroups) beside the weight-gradient pass of
 // the active columns (the rest): both read G only, the walk is bound by its gathers' latency,
