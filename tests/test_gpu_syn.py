@@ -122,6 +122,30 @@ def test_syn_bwd_matches_oracle(B):
         assert np.max(np.abs(got - ex) - 1e-5 * sc) <= 1e-6, what
 
 
+@pytest.mark.parametrize("B,nb", [(17, 8), (32, 8), (32, 1), (3, 2)])
+def test_syn_bwd_wide_and_narrow_rows(B, nb):
+    """G rows of 32 floats (B = 17-32, the type-phased column walk) and of 4 floats (B <= 4),
+    8 receptors and 1: the G build's dy tile at its smallest (8 posts of 32 batch entries x 8
+    receptors) and its largest, padding entries written as zero."""
+    import dataclasses
+    from v1_glif_model_amd.ops import SynapseTable
+    cfg = dataclasses.replace(tiny_config(n=257), n_basis=nb)
+    _, tb = network(cfg, seed=9, dense_basis=True)
+    t = SynapseTable(tb.rec.indices, tb.rec.syn_id, (tb.n_neurons, tb.rec.n_cols), tb.basis,
+                     n_delay_slots=tb.max_delay)
+    t.set_weights(torch.tensor(tb.rec.weight, device="cuda"))
+    rng = np.random.default_rng(B * 10 + nb)
+    z = _spikes(rng, B, tb.rec.n_cols, 0.05)
+    dy = rng.normal(0, 1, (B * tb.n_neurons, tb.n_basis)).astype(np.float32)
+    dz, dw = t.backward(torch.tensor(z, device="cuda"), torch.tensor(dy, device="cuda"))
+    dz, dw = dz.cpu().numpy(), dw.cpu().numpy()
+    rdz, rdw = orc.syn_bwd(tb.rec, z, tb.basis, dy)
+    _, _, dz_abs, dw_abs = dense.syn_bwd_f64(tb.rec, z, tb.basis, dy)
+    assert np.max(np.abs(dz - rdz) - 1e-5 * dz_abs) <= 1e-6
+    assert np.max(np.abs(dw - rdw) - 1e-5 * dw_abs) <= 1e-6
+    assert np.count_nonzero(dw) > 0
+
+
 @pytest.mark.parametrize("B", [5, 12])
 def test_syn_bwd_counts_and_partial_requests(B):
     """Poisson-count inputs (dW scaled by the count, models.py:917-931) through the grouped
