@@ -84,7 +84,8 @@ int glif_table_pre_ind(const glif_table *t, const int32_t **order, const int32_t
  * vector w [n_syn] (device, reference order) into the table's column- and
  * row-grouped copies.  Must be called before use and after every weight update.  It
  * writes the table's weight copies (and stages through a buffer of the table's), so calls
- * on one table must not overlap, and no call that reads the table may run beside one. */
+ * on one table must not overlap, and no call that reads the table may run beside one.
+ * A table without synapses has no weights: w may then be NULL and nothing is launched. */
 int glif_table_set_weights(glif_table *t, const float *w, void *stream);
 
 /* --------------------------------------- synaptic-current op (fwd, grad) ----

@@ -122,6 +122,25 @@ def test_syn_bwd_matches_oracle(B):
         assert np.max(np.abs(got - ex) - 1e-5 * sc) <= 1e-6, what
 
 
+@pytest.mark.parametrize("B", [1, 5])
+def test_op_on_a_table_without_synapses(B):
+    """S = 0 (every column empty): both forwards give zero currents, the gradient zero dz and an
+    empty dW, without a launch of zero workgroups."""
+    from v1_glif_model_amd.ops import SynapseTable
+    n_post, D, nb = 70, 3, 5
+    t = SynapseTable(np.zeros((0, 2), np.int64), np.zeros(0, np.uint8), (n_post, D * n_post),
+                     np.eye(5, nb, dtype=np.float32), n_delay_slots=D)
+    t.set_weights(torch.zeros(0, dtype=torch.float32, device="cuda"))
+    z = torch.tensor(_spikes(np.random.default_rng(B), B, D * n_post, 0.3), device="cuda")
+    for mode in ("deterministic", "event"):
+        I = t.forward(z, mode=mode).cpu().numpy()
+        assert I.shape == (B * n_post, nb) and not np.any(I)
+    dz, dw = t.backward(z, torch.ones((B * n_post, nb), dtype=torch.float32, device="cuda"))
+    assert dz.shape == (B, D * n_post) and not torch.any(dz).item()
+    assert dw.numel() == 0
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("B,nb", [(17, 8), (32, 8), (32, 1), (3, 2)])
 def test_syn_bwd_wide_and_narrow_rows(B, nb):
     """G rows of 32 floats (B = 17-32, the type-phased column walk) and of 4 floats (B <= 4),

@@ -492,12 +492,15 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     const int64_t n_fill = fill_blocks ? t->n_syn : 0;
     const dim3 g_grid(g_blocks + fill_blocks);
     const size_t g_lds = sizeof(float) * (((t->n_types * t->n_basis + 3) & ~3) + static_cast<size_t>(B) * gP * t->n_basis);
-    if (cmp)
+    if (g_grid.x == 0) {
+        // no posts and nothing to fill
+    } else if (cmp) {
         hipLaunchKernelGGL(k_make_G<true>, g_grid, dim3(kBlock), g_lds, s, dy, B, t->n_post, Bp, t->basis,
                            t->n_types, t->n_basis, oc.gtype, rows, gP, w.G, g_blocks, dw, n_fill);
-    else
+    } else {
         hipLaunchKernelGGL(k_make_G<false>, g_grid, dim3(kBlock), g_lds, s, dy, B, t->n_post, Bp, t->basis,
                            t->n_types, t->n_basis, nullptr, rows, gP, w.G, g_blocks, dw, n_fill);
+    }
     GLIF_HIP(hipGetLastError());
     if (grouped) {
         // the grouped row-sliced walk for dz beside the active columns' dW (every active
@@ -511,6 +514,7 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
         const int walk_blocks = dz ? static_cast<int>(ceil_div(t->n_groups * LG, kBlock)) : 0;
         const int dw_blocks = dw ? static_cast<int>(ceil_div(t->n_cols, kBlock)) : 0;
         const dim3 grid(walk_blocks + dw_blocks);
+        if (grid.x == 0) return GLIF_OK;   // no columns
         if (LG == 2) hipLaunchKernelGGL(k_syn_bwd_gs<2>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, da);
         else hipLaunchKernelGGL(k_syn_bwd_gs<4>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, da);
         GLIF_HIP(hipGetLastError());

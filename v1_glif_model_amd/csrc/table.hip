@@ -608,8 +608,10 @@ int glif_table_pre_ind(const glif_table *tt, const int32_t **order, const int32_
 }
 
 int glif_table_set_weights(glif_table *tt, const float *w, void *stream) {
-    if (!tt || !w) return fail(GLIF_EINVAL, "NULL argument");
+    if (!tt) return fail(GLIF_EINVAL, "NULL argument");
     Table *t = reinterpret_cast<Table *>(tt);
+    if (t->n_syn == 0) return GLIF_OK;   // no synapses, no weights (w may be NULL)
+    if (!w) return fail(GLIF_EINVAL, "NULL argument");
     hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = launch_perm_gather(t->w_col, w, t->order, t->pcol, t->n_syn, t->pcol.mid, s);
     if (rc) return rc;
