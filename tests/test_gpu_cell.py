@@ -438,3 +438,34 @@ def test_two_rollouts_before_backward():
     cell.rollout(lgn2, bkg2)
     with pytest.raises(RuntimeError, match="overwritten"):
         cell.backward(gz=gz, rollout=first)
+
+
+@pytest.mark.parametrize("B", [2, 5])
+def test_cell_without_recurrent_synapses(B):
+    """A network whose recurrent table is empty (fan-in 0; the inputs alone drive it): both
+    forwards as the oracle's (deterministic bit-exact, event spike trains equal), the BPTT
+    gradients of the input weights within the bar and an empty recurrent gradient."""
+    cfg = tiny_config(n=90, fanin=0, ins=2.0)
+    tn = network(cfg, seed=3, dense_basis=True)
+    assert tn[1].rec.n_syn == 0
+    T = 30
+    lgn, bkg = _inputs(cfg, T, B)
+    oc = _oracle(tn[1], **ORC_KW)
+    oz, ov, oref, _ = oc.forward(lgn, bkg)
+    assert oz.sum() > 0
+    for mode in ("deterministic", "event"):
+        cell = _cell(tn, mode, **CELL_KW)
+        z, v, _ = cell.rollout(lgn, bkg)
+        np.testing.assert_array_equal(z.cpu().numpy().astype(np.uint8), oz)
+        if mode == "deterministic":
+            np.testing.assert_array_equal(v.cpu().numpy().view(np.uint32), ov.view(np.uint32))
+    rng = np.random.default_rng(B)
+    gz = rng.normal(0, 1, oz.shape).astype(np.float32)
+    g = cell.backward(gz=torch.tensor(gz, device="cuda"))
+    og = oc.backward(lgn, bkg, oz, oref, ov, gz_loss=gz)
+    assert g["rec"].numel() == 0
+    for k in ("lgn", "bkg"):
+        a, e = g[k].cpu().numpy(), og[k]
+        scale = np.max(np.abs(e))
+        assert scale > 0
+        assert np.max(np.abs(a - e)) <= 1e-5 * scale + 1e-6, k
