@@ -42,9 +42,7 @@
 #include <omp.h>
 #endif
 
-#define ORC_EINVAL (-22)
-#define ORC_ERANGE (-34)
-#define ORC_ENOMEM (-12)
+#include "glif_oracle.h"
 
 /* Threads of the OpenMP loops (n < 1: 1); the number in use. */
 int orc_set_threads(int n)
@@ -179,25 +177,7 @@ void orc_syn_bwd(int B, int64_t n_post, int64_t n_cols, int nb, int64_t S, const
 }
 
 /* ---------------------------------------------------------------- cell ---- */
-typedef struct {
-    int64_t S, n_cols;
-    const int64_t *post, *col, *order, *row_splits;
-    const float *w;
-    const uint8_t *sid;
-} orc_table;
-
-typedef struct {
-    int64_t N, D;
-    int32_t nb, n_types;
-    const float *decay, *cf;            /* [N] */
-    const float *asc_decay, *asc_amps;  /* [N][2] */
-    const int32_t *tref;                /* [N] */
-    const float *syn_decay, *psc_initial; /* [nb] */
-    const float *basis;                 /* [n_types][nb] */
-    float dt, lr_scale, vgd, rd, gauss_std, damp;
-    int32_t pseudo_gauss, hard_reset;
-    orc_table rec, lgn, bkg;
-} orc_cell;
+/* orc_table, orc_cell: glif_oracle.h */
 
 static float surrogate(const orc_cell *c, float vsc)
 {
