@@ -82,6 +82,10 @@ def _args():
                     help="time the op-level entry points instead (calculate_synaptic_currents forward in "
                          "both modes and its custom gradient) on the config-2 recurrent table, B=5, "
                          "z_buf spikes at 5 Hz")
+    ap.add_argument("--step-loop", action="store_true",
+                    help="time the Keras-RNN form of the config-2 training step instead: a loop of T "
+                         "V1Column.call steps differentiated by autograd step by step (glif_step_backward "
+                         "per step), rate MSE loss, against the fused rollout + BPTT of the default run")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (5 times): the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE for streaming kernels")
@@ -303,6 +307,59 @@ def sweep_rates(args):
         "sweep": rows}))
 
 
+def bench_step_loop(args):
+    """The config-2 training step's forward and backward in the Keras RNN's form (models.py:1317-1322
+    with the tape of multi_training.py:368-372): T calls of V1Column.call, each an autograd node
+    whose backward is glif_step_backward, the rate MSE of the loop's spikes, loss.backward().
+    Same network, inputs, batch and loss targets as the default run; no optimizer step."""
+    import numpy as np
+    import torch
+    from v1_glif_model_amd import synthetic as sy
+    from v1_glif_model_amd.models import V1Column
+    cfg = sy.config(2)
+    T = args.seq_len or cfg.seq_len
+    B = cfg.batch
+    net = sy.make_network(cfg, seed=0)
+    lgn_np, bkg_np = sy.make_inputs(cfg, seed=1, seq_len=T, batch=B)
+    cell = V1Column(net, mode=args.mode, gauss_std=0.5, dampening_factor=0.5, train_recurrent_per_type=False,
+                    recurrent_dampening_factor=0.5, voltage_gradient_dampening=0.5, pseudo_gauss=True,
+                    train_input=True)
+    dev = cell.device
+    lgn = torch.tensor(lgn_np, dtype=torch.float32, device=dev)
+    bkg = torch.tensor(bkg_np, device=dev)
+    targets = torch.tensor(sy.make_rate_targets(cfg.n_neurons, seed=2), dtype=torch.float32, device=dev)
+    w_rec, w_lgn = cell.recurrent_weight_values, cell.input_weight_values
+    w_rec.requires_grad_(True)
+    w_lgn.requires_grad_(True)
+
+    def step():
+        w_rec.grad = None
+        w_lgn.grad = None
+        state = cell.zero_state(B)
+        zsum = torch.zeros((B, cfg.n_neurons), dtype=torch.float32, device=dev)
+        for t in range(T):
+            (z, _), state = cell.call(lgn[t], state, bkg_counts=bkg[t])
+            zsum = zsum + z
+        loss = ((zsum.mean(0) / T - targets) ** 2).mean()
+        loss.backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000 / args.steps
+    print(json.dumps({"metric": "Keras-RNN form: T calls + per-step autograd backward, ms per training step",
+                      "value": round(ms, 2), "unit": "ms per step", "steps": args.steps, "warmup": args.warmup,
+                      "higher_is_better": False, "dtype": "f32", "data": "synthetic",
+                      "config": {"workload": f"config 2 network, B={B}, T={T}, rate MSE, mode {args.mode}, "
+                                             "no optimizer step", "neurons": cfg.n_neurons, "batch": B,
+                                 "seq_len": T},
+                      "neuron_timesteps_per_s": round(B * cfg.n_neurons * T / (ms / 1000), 1)}), flush=True)
+
+
 def bench_op(args):
     """Op-level timing (glif_syn_fwd / glif_syn_bwd, models.py:103-263) on the config-2
     recurrent table: z_buf [5][D*N] Bernoulli(0.005) spikes, dy [5*N][nb] normal."""
@@ -362,6 +419,9 @@ def main():
     args = _args()
     if args.op and args.gpus == 1:
         bench_op(args)
+        return
+    if args.step_loop and args.gpus == 1:
+        bench_step_loop(args)
         return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)

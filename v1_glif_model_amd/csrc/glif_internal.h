@@ -18,6 +18,9 @@ constexpr int kMaxBasis = 8;
 constexpr int kMaxBatch = 32;
 constexpr uint32_t kLow24 = 0x00FFFFFFu;
 constexpr int kChunkEntries = 512;
+// work units of the op-level weight-gradient pass: at most 64 consecutive columns and this many
+// synapses, or one chunk of this many synapses of a longer column
+constexpr int kDwUnitEntries = 1024;
 constexpr int kChunkRows = 63;
 // grouped row-sliced backward order: kGsCols columns per lane group,
 // kGsSlices equal ranges of G rows, segments padded to kGsPad entries
@@ -112,6 +115,10 @@ struct Table {
     // kChunkEntries entries unless it is a single longer row
     int32_t n_chunks = 0;
     int4 *chunk_desc = nullptr;   // [n_chunks]
+    // work units of the op-level weight-gradient pass over the column-grouped table: unit u is
+    // {first column, columns, first position, end position} (kDwUnitEntries)
+    int32_t n_dwu = 0;
+    int4 *dwu = nullptr;          // [n_dwu]
     int32_t *ph_ptr = nullptr;    // [n_types * n_cols + 1]
     int32_t *ph_order = nullptr;  // [n_syn]       synapse id at position k
     uint2 *ph_pw = nullptr;       // [n_syn]       {post, weight bits}

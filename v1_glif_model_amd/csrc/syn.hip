@@ -204,6 +204,8 @@ struct SynDwArgs {
     int64_t n_cols;
     int32_t B, hm, lm, R, counts;  // G row of entry p: (p >> 24) * hm + (p & kLow24) * lm
     const float *z;  // [B][n_cols]
+    const int4 *units;  // the table's work units (Table::dwu), one wave each
+    int32_t n_units;
     const int32_t *col_ptr;
     const uint32_t *ps;
     const int32_t *order;
@@ -211,20 +213,33 @@ struct SynDwArgs {
     float *dw;  // reference order, zero-filled by the caller
 };
 
-// Workgroup bid of the pass: a wave per 64 consecutive columns.
+// Workgroup bid of the pass: a wave per work unit -- up to 64 consecutive short columns (lane l
+// tests column first + l), or one chunk of a long column, which the wave's four 16-lane
+// sub-groups split in quarters, so a table of few long columns (the background's) still spreads
+// over many waves.
 __device__ inline void syn_dw_body(const SynDwArgs &a, int64_t bid) {
     const int lane = threadIdx.x % kWave;
-    const int64_t c0 = bid * blockDim.x + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * kWave;
-    if (c0 >= a.n_cols) return;  // the whole wave leaves together
-    const int64_t c = c0 + lane;
-    const int64_t cl = min(c, a.n_cols - 1);
+    const int64_t ui = bid * (blockDim.x / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (ui >= a.n_units) return;  // the whole wave leaves together
+    const int4 un = a.units[ui];
+    const int64_t c0 = un.x;
+    const bool chunk = un.y == 1;  // one column: its [un.z, un.w) in four quarters
+    const int64_t c = c0 + (chunk ? 0 : lane);
+    // a chunk's quarters are held by lanes 0, 16, 32, 48, so the loop below gives one to
+    // each sub-group; otherwise lane l holds column c0 + l
+    const bool mine = chunk ? (lane % 16) == 0 : lane < un.y;
     uint32_t m = 0;
-    for (int b = 0; b < a.B; ++b) m |= (a.z[b * a.n_cols + cl] > 0.0f ? 1u : 0u) << b;
-    if (c >= a.n_cols) m = 0;
+    if (mine)
+        for (int b = 0; b < a.B; ++b) m |= (a.z[b * a.n_cols + c] > 0.0f ? 1u : 0u) << b;
     int32_t lo = 0, hi = 0;
     if (m) {
-        lo = a.col_ptr[c];
-        hi = a.col_ptr[c + 1];
+        lo = chunk ? un.z : a.col_ptr[c];
+        hi = chunk ? un.w : a.col_ptr[c + 1];
+        if (chunk) {   // quarter lane / 16 of the chunk
+            const int32_t q = (hi - lo + 3) / 4, s4 = lane / 16;
+            lo = min(hi, lo + s4 * q);
+            hi = min(hi, lo + q);
+        }
     }
     const int sub = lane / 16, sl = lane % 16;
     uint64_t live = __ballot(m != 0u);
@@ -245,7 +260,7 @@ __device__ inline void syn_dw_body(const SynDwArgs &a, int64_t bid) {
         const int32_t hsrc = __shfl(hi, sl_src, kWave);
         const uint32_t mm = src >= 0 ? msrc : 0u;
         const int32_t chi = src >= 0 ? hsrc : clo;
-        const int64_t cc = c0 + sl_src;
+        const int64_t cc = chunk ? c0 : c0 + sl_src;
         for (int32_t k0 = clo; k0 < chi; k0 += 64) {
             float d[4];
             const float *gp[4];
@@ -508,11 +523,11 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
         ActDense act{z, dz, t->n_cols, counts};
         GsArgs ga{t->n_cols, (t->n_cols + kGsCols - 1) / kGsCols, B, cmp ? oc.gs_seg : t->gs_seg,
                   cmp ? oc.gs_pw : t->gs_pw, w.G};
-        SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->col_ptr,
-                     cmp ? oc.ps : t->ps, t->order, w.G, dw};
+        SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->dwu, t->n_dwu,
+                     t->col_ptr, cmp ? oc.ps : t->ps, t->order, w.G, dw};
         const int LG = Bp / 4;
         const int walk_blocks = dz ? static_cast<int>(ceil_div(t->n_groups * LG, kBlock)) : 0;
-        const int dw_blocks = dw ? static_cast<int>(ceil_div(t->n_cols, kBlock)) : 0;
+        const int dw_blocks = dw ? static_cast<int>(ceil_div(t->n_dwu, kBlock / kWave)) : 0;
         const dim3 grid(walk_blocks + dw_blocks);
         if (grid.x == 0) return GLIF_OK;   // no columns
         if (LG == 2) hipLaunchKernelGGL(k_syn_bwd_gs<2>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, da);

@@ -243,7 +243,7 @@ static void free_table(Table *t) {
     free_plan(t->pinv);
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
                     t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
-                    t->chunk_desc, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src,
+                    t->chunk_desc, t->dwu, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src,
                     t->cg.ps, t->cg.ph_pw, t->cg.gs_seg, t->cg.gs_pw, t->cg.gs_src, t->cg.gtype,
                     t->og.ps, t->og.ph_pw, t->og.gs_seg, t->og.gs_pw, t->og.gs_src, t->og.gtype};
     for (void *p : ptrs)
@@ -540,6 +540,22 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         n = m;
     }
     t->n_chunks = static_cast<int32_t>(chunk_desc.size());
+    // weight-gradient work units: runs of short columns, chunks of long ones
+    std::vector<int4> dwu;
+    for (int64_t c = 0; c < n_cols;) {
+        const int32_t k0 = col_ptr[c], k1 = col_ptr[c + 1];
+        if (k1 - k0 > kDwUnitEntries) {
+            for (int32_t k = k0; k < k1; k += kDwUnitEntries)
+                dwu.push_back(make_int4(static_cast<int>(c), 1, k, std::min(k + kDwUnitEntries, k1)));
+            ++c;
+            continue;
+        }
+        int64_t m = c + 1;
+        while (m < n_cols && m - c < kWave && col_ptr[m + 1] - k0 <= kDwUnitEntries) ++m;
+        dwu.push_back(make_int4(static_cast<int>(c), static_cast<int>(m - c), k0, col_ptr[m]));
+        c = m;
+    }
+    t->n_dwu = static_cast<int32_t>(dwu.size());
     t->basis_host = new float[static_cast<size_t>(n_types) * n_basis];
     std::memcpy(t->basis_host, basis, sizeof(float) * n_types * n_basis);
     int rc = GLIF_OK;
@@ -549,6 +565,7 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         (rc = upload(&t->ps, ps.data(), ps.size())) ||
         (rc = upload(&t->row_ptr, row_ptr.data(), row_ptr.size())) ||
         (rc = upload(&t->chunk_desc, chunk_desc.data(), chunk_desc.size())) ||
+        (rc = upload(&t->dwu, dwu.data(), dwu.size())) ||
         (rc = upload(&t->perm, perm.data(), perm.size())) ||
         (rc = upload(&t->pd, pd.data(), pd.size())) ||
         (with_pidx && (rc = upload(&t->pidx, pidx.data(), pidx.size()))) ||
