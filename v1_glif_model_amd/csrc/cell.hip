@@ -96,8 +96,13 @@ constexpr int kLgnPosts = 8;     // posts (waves) per k_lgn_rows workgroup
 constexpr int kLgnMaxBatch = 8;      // batch accumulators per lane of k_lgn_rows
 constexpr int kLgnEventMinBatch = 3; // event mode computes LGN ahead from this batch size up
 
-// Whether this cell computes its LGN currents ahead of the loop at batch size B.
-static bool lgn_ahead(const Cell *c, int B) { return B <= kLgnMaxBatch && c->lgn->n_cols > 0; }
+constexpr int kLgnAheadMinTicks = 16;   // shorter rollouts (a per-step call: T = 1) push or pull
+                                        // the LGN events per tick: a segment pass costs as much
+                                        // for one tick as for 64
+// Whether this cell computes its LGN currents ahead of the loop at batch size B over T ticks.
+static bool lgn_ahead(const Cell *c, int B, int T) {
+    return B <= kLgnMaxBatch && T >= kLgnAheadMinTicks && c->lgn->n_cols > 0;
+}
 
 static void release_side(Cell *c) {
     if (!c->side) return;
@@ -162,7 +167,7 @@ static CellWs carve_cell(void *ws, const Cell *c, int32_t B, int32_t T, size_t *
     w.abits = cv.take<uint64_t>(static_cast<size_t>(T + c->D) * c->W);
     w.lbits = cv.take<uint64_t>(static_cast<size_t>(T) * ((nl + 63) / 64));
     w.I2 = cv.take<float>(2 * BN * c->nb);  // deterministic pull beside the step: two halves
-    if (lgn_ahead(c, B)) {
+    if (lgn_ahead(c, B, T)) {
         w.IL = cv.take<float>(static_cast<size_t>(kLgnRing) * BN * c->nb);
         w.lgnT = cv.take<uint64_t>(static_cast<size_t>((T + kLgnSeg - 1) / kLgnSeg) * nl * B);
     }
@@ -1794,7 +1799,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
     // events where that was measured cheaper: below kLgnEventMinBatch batch entries (config 3
     // at B = 1: 16.96 against 15.88 ms per rollout) and with per-type slots, whose single LGN
     // atomic per event the launch hides (class-pair types: 61.2 against 59.8 ms per step)
-    const bool ahead = lgn_ahead(c, B) && (!event || (!typed && B >= kLgnEventMinBatch));
+    const bool ahead = lgn_ahead(c, B, T) && (!event || (!typed && B >= kLgnEventMinBatch));
     const bool ring_is_I = event && ahead;
 
     // input lists (LGN push in the forward, LGN / background dW in the backward)
