@@ -1670,8 +1670,7 @@ __global__ void __launch_bounds__(kBlock) k_u8_to_f32(float *__restrict__ dst, c
 struct StepWs {
     float *dy;      // [B * N][nb]
     float *xl, *xk; // the step's LGN spikes and background counts as floats
-    void *syn;      // the op gradients' workspace (one at a time)
-    size_t syn_bytes;
+    float *G;       // the op gradients' projection, shared by the tables whose G layouts agree
 };
 
 static StepWs carve_step(void *ws, const Cell *c, int32_t B, size_t *bytes) {
@@ -1681,12 +1680,9 @@ static StepWs carve_step(void *ws, const Cell *c, int32_t B, size_t *bytes) {
     w.dy = cv.take<float>(BN * c->nb);
     w.xl = cv.take<float>(std::max<int64_t>(static_cast<int64_t>(B) * c->lgn->n_cols, 1));
     w.xk = cv.take<float>(std::max<int64_t>(static_cast<int64_t>(B) * c->bkg->n_cols, 1));
-    const glif_table *tabs[3] = {reinterpret_cast<const glif_table *>(c->rec),
-                                 reinterpret_cast<const glif_table *>(c->lgn),
-                                 reinterpret_cast<const glif_table *>(c->bkg)};
-    w.syn_bytes = 0;
-    for (const glif_table *t : tabs) w.syn_bytes = std::max(w.syn_bytes, glif_syn_workspace(t, B));
-    w.syn = cv.take<char>(std::max<size_t>(w.syn_bytes, 1));
+    size_t g = 1;
+    for (const Table *t : {c->rec, c->lgn, c->bkg}) g = std::max(g, syn_g_floats(t, B));
+    w.G = cv.take<float>(g);
     if (bytes) *bytes = cv.off;
     return w;
 }
@@ -2422,10 +2418,15 @@ int glif_step_backward(glif_cell *cc, int32_t B, const uint8_t *lgn, const uint8
     hipLaunchKernelGGL(k_step_adj, dim3(ceil_div(BN, kBlock)), dim3(kBlock), 0, s, a);
     GLIF_HIP(hipGetLastError());
     int rc;
-    const glif_table *rec = reinterpret_cast<const glif_table *>(c->rec);
-    if ((want_dz || dw_rec) &&
-        (rc = glif_syn_bwd(rec, z_buf, w.dy, B, 0, want_dz ? g_old->z_buf : nullptr, dw_rec, w.syn, w.syn_bytes, s)))
-        return rc;
+    // G is built once for the step's dy and reused by every table with the same layout
+    const Table *g_of = nullptr;
+    auto run = [&](const Table *t, const float *x, int32_t counts, float *dz, float *dw) {
+        const bool ready = g_of && same_g_layout(g_of, t);
+        const int r = syn_bwd_run(t, x, w.dy, B, counts, dz, dw, w.G, ready, s);
+        if (!r && (dz || dw)) g_of = t;
+        return r;
+    };
+    if ((want_dz || dw_rec) && (rc = run(c->rec, z_buf, 0, want_dz ? g_old->z_buf : nullptr, dw_rec))) return rc;
     if (want_dz) {
         const int64_t DN = static_cast<int64_t>(c->D) * c->N, n = static_cast<int64_t>(B) * DN;
         hipLaunchKernelGGL(k_step_zbuf_grad, dim3(ceil_div(n, kBlock)), dim3(kBlock), 0, s, g_old->z_buf,
@@ -2435,16 +2436,12 @@ int glif_step_backward(glif_cell *cc, int32_t B, const uint8_t *lgn, const uint8
     if (dw_lgn) {
         const int64_t n = static_cast<int64_t>(B) * c->lgn->n_cols;
         if (n) hipLaunchKernelGGL(k_u8_to_f32, dim3(ceil_div(n, kBlock)), dim3(kBlock), 0, s, w.xl, lgn, n);
-        if ((rc = glif_syn_bwd(reinterpret_cast<const glif_table *>(c->lgn), w.xl, w.dy, B, 0, nullptr, dw_lgn,
-                               w.syn, w.syn_bytes, s)))
-            return rc;
+        if ((rc = run(c->lgn, w.xl, 0, nullptr, dw_lgn))) return rc;
     }
     if (dw_bkg) {
         const int64_t n = static_cast<int64_t>(B) * c->bkg->n_cols;
         if (n) hipLaunchKernelGGL(k_u8_to_f32, dim3(ceil_div(n, kBlock)), dim3(kBlock), 0, s, w.xk, bkg, n);
-        if ((rc = glif_syn_bwd(reinterpret_cast<const glif_table *>(c->bkg), w.xk, w.dy, B, 1, nullptr, dw_bkg,
-                               w.syn, w.syn_bytes, s)))
-            return rc;
+        if ((rc = run(c->bkg, w.xk, 1, nullptr, dw_bkg))) return rc;
     }
     GLIF_HIP(hipGetLastError());
     return GLIF_OK;

@@ -235,6 +235,13 @@ inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) 
 
 // Batch padded to the float4 groups of G (4, 8, 16 or 32).
 int batch_pad(int B);
+// The op's custom gradient (glif_syn_bwd) on a given G buffer of syn_g_floats(t, B) floats;
+// g_ready: G already holds this dy's rows in t's layout (built for a table with
+// same_g_layout), so only dz / dW are computed.
+size_t syn_g_floats(const Table *t, int32_t B);
+bool same_g_layout(const Table *a, const Table *b);
+int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int32_t counts, float *dz, float *dw,
+                float *G, bool g_ready, hipStream_t s);
 // Lanes per column for the column-grouped kernels (16, 32 or 64).
 int sub_wave_for(const Table *t);
 // Blocks for `items` sub-waves of L lanes (capped; kernels grid-stride).

@@ -1,6 +1,7 @@
 // Op-level entry points of calculate_synaptic_currents (models.py:103-263):
 // forward (event push or deterministic pull) and the custom gradient.
 #include <algorithm>
+#include <cstring>
 #include <mutex>
 
 #include "compact.h"
@@ -485,10 +486,30 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     if (B <= 0 || B > kMaxBatch) return fail(GLIF_EINVAL, "B must be in [1, 32]");
     if (!dz && !dw) return GLIF_OK;
     const Table *t = reinterpret_cast<const Table *>(tt);
-    hipStream_t s = static_cast<hipStream_t>(stream);
     size_t need = glif_syn_workspace(tt, B);
     if (!ws || ws_bytes < need) return fail(GLIF_ENOMEM, "workspace too small");
-    SynWs w = carve_syn(ws, t, B, nullptr);
+    return syn_bwd_run(t, z, dy, B, counts, dz, dw, carve_syn(ws, t, B, nullptr).G, false,
+                       static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace glif {
+
+size_t syn_g_floats(const Table *t, int32_t B) {
+    const int rows = t->og.rows ? t->og.rows : t->n_types;
+    return static_cast<size_t>(t->n_post) * rows * batch_pad(B);
+}
+
+bool same_g_layout(const Table *a, const Table *b) {
+    return a->og.rows == 0 && b->og.rows == 0 && a->n_post == b->n_post && a->n_types == b->n_types &&
+           a->n_basis == b->n_basis &&
+           std::memcmp(a->basis_host, b->basis_host, sizeof(float) * a->n_types * a->n_basis) == 0;
+}
+
+int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int32_t counts, float *dz, float *dw,
+                float *G, bool g_ready, hipStream_t s) {
+    if (!dz && !dw) return GLIF_OK;
     const int Bp = batch_pad(B);
     // the table's own compact rows (post * rows + rank) when it has them, else type-major rows
     const CompactRows &oc = t->og;
@@ -502,7 +523,7 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     // G, with the zero fill of dW beside it when the grouped path's weight-gradient pass
     // writes only the active synapses
     const int gP = make_G_posts(B, t->n_basis);
-    const int g_blocks = static_cast<int>(ceil_div(static_cast<int64_t>(t->n_post), gP));
+    const int g_blocks = g_ready ? 0 : static_cast<int>(ceil_div(static_cast<int64_t>(t->n_post), gP));
     const int fill_blocks = grouped && dw && t->n_syn ? 256 : 0;
     const int64_t n_fill = fill_blocks ? t->n_syn : 0;
     const dim3 g_grid(g_blocks + fill_blocks);
@@ -511,10 +532,10 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
         // no posts and nothing to fill
     } else if (cmp) {
         hipLaunchKernelGGL(k_make_G<true>, g_grid, dim3(kBlock), g_lds, s, dy, B, t->n_post, Bp, t->basis,
-                           t->n_types, t->n_basis, oc.gtype, rows, gP, w.G, g_blocks, dw, n_fill);
+                           t->n_types, t->n_basis, oc.gtype, rows, gP, G, g_blocks, dw, n_fill);
     } else {
         hipLaunchKernelGGL(k_make_G<false>, g_grid, dim3(kBlock), g_lds, s, dy, B, t->n_post, Bp, t->basis,
-                           t->n_types, t->n_basis, nullptr, rows, gP, w.G, g_blocks, dw, n_fill);
+                           t->n_types, t->n_basis, nullptr, rows, gP, G, g_blocks, dw, n_fill);
     }
     GLIF_HIP(hipGetLastError());
     if (grouped) {
@@ -522,9 +543,9 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
         // synapse's written once, in reference order)
         ActDense act{z, dz, t->n_cols, counts};
         GsArgs ga{t->n_cols, (t->n_cols + kGsCols - 1) / kGsCols, B, cmp ? oc.gs_seg : t->gs_seg,
-                  cmp ? oc.gs_pw : t->gs_pw, w.G};
+                  cmp ? oc.gs_pw : t->gs_pw, G};
         SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->dwu, t->n_dwu,
-                     t->col_ptr, cmp ? oc.ps : t->ps, t->order, w.G, dw};
+                     t->col_ptr, cmp ? oc.ps : t->ps, t->order, G, dw};
         const int LG = Bp / 4;
         const int walk_blocks = dz ? static_cast<int>(ceil_div(t->n_groups * LG, kBlock)) : 0;
         const int dw_blocks = dw ? static_cast<int>(ceil_div(t->n_dwu, kBlock / kWave)) : 0;
@@ -537,7 +558,7 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     }
     // the type-phased column walk writes the active columns' synapses; the rest stay 0
     if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
-    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, cmp ? oc.ph_pw : t->ph_pw, w.G, dz ? 1 : 0, dw,
+    ColArgs ca{t->n_cols, t->n_post, t->n_types, B, t->ph_ptr, cmp ? oc.ph_pw : t->ph_pw, G, dz ? 1 : 0, dw,
                t->ph_order, cmp ? 1 : 0};
     ActDense act{z, dz, t->n_cols, counts};
     const dim3 grid(ceil_div(t->n_cols * (Bp / 4), kBlock));
@@ -551,4 +572,4 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     return GLIF_OK;
 }
 
-}  // extern "C"
+}  // namespace glif
