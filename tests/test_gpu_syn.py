@@ -190,6 +190,54 @@ def test_syn_bwd_counts_and_partial_requests(B):
     np.testing.assert_array_equal(dw_only.cpu().numpy(), dw)
 
 
+def _long_column_table(seed=3, n_post=6000):
+    """A table with columns longer than the dz walk handles well (the background table's
+    shape) beside the other work-unit kinds: long columns split into 1024-synapse chunks
+    (4097 entries: a 1-synapse last chunk), columns of 1025-2049, single columns too long to
+    share a run (700), runs of up to 64 short columns, and empty columns among them."""
+    from v1_glif_model_amd.tables import SynapseTable as Tab
+    rng = np.random.default_rng(seed)
+    lens = [5000, 0, 700, 700, 4097, 1025, 3, 0] + list(rng.integers(0, 40, 70)) + [2049, 1024, 0, 6000]
+    post, col = [], []
+    for c, n in enumerate(lens):
+        p = rng.choice(n_post, size=int(n), replace=False)
+        post.append(p)
+        col.append(np.full(int(n), c))
+    post, col = np.concatenate(post).astype(np.int64), np.concatenate(col).astype(np.int64)
+    o = np.lexsort((col, post))            # the reference's (post, pre) order
+    post, col = post[o], col[o]
+    S = post.size
+    return Tab(post=post, col=col, weight=rng.normal(0, 1, S).astype(np.float32),
+               syn_id=rng.integers(0, 5, S).astype(np.uint8), n_post=n_post, n_cols=len(lens))
+
+
+@pytest.mark.parametrize("B", [1, 5, 12, 32])
+def test_syn_bwd_long_columns(B):
+    """dz of a table with columns of thousands of synapses over the weight-gradient work
+    units (a wave per unit; a chunked column's units summed in order), with the dW pass
+    beside it; Poisson-count inputs, and dz-only / dW-only calls equal to the full call."""
+    from v1_glif_model_amd.ops import SynapseTable
+    tab = _long_column_table()
+    rng = np.random.default_rng(B + 70)
+    basis = rng.random((5, 3)).astype(np.float32)
+    t = SynapseTable(tab.indices, tab.syn_id, (tab.n_post, tab.n_cols), basis)
+    t.set_weights(torch.tensor(tab.weight, device="cuda"))
+    z = ((rng.random((B, tab.n_cols)) < 0.5) * rng.integers(1, 3, (B, tab.n_cols))).astype(np.float32)
+    dy = rng.normal(0, 1, (B * tab.n_post, 3)).astype(np.float32)
+    zt, dyt = torch.tensor(z, device="cuda"), torch.tensor(dy, device="cuda")
+    dz, dw = t.backward(zt, dyt, counts=True)
+    dz, dw = dz.cpu().numpy(), dw.cpu().numpy()
+    rdz, rdw = orc.syn_bwd(tab, z, basis, dy, use_count=True)
+    _, _, dz_abs, dw_abs = dense.syn_bwd_f64(tab, z, basis, dy, use_count=True)
+    assert np.max(np.abs(dz - rdz) - 1e-5 * dz_abs) <= 1e-6
+    assert np.max(np.abs(dw - rdw) - 1e-5 * dw_abs) <= 1e-6
+    assert np.all(dz[:, [1, 7]] == 0) and np.count_nonzero(dz[:, 0]) == B
+    dz_only, _ = t.backward(zt, dyt, counts=True, want_dw=False)
+    _, dw_only = t.backward(zt, dyt, counts=True, want_dz=False)
+    np.testing.assert_array_equal(dz_only.cpu().numpy(), dz)
+    np.testing.assert_array_equal(dw_only.cpu().numpy(), dw)
+
+
 @pytest.mark.parametrize("B", [5, 9])
 def test_syn_bwd_input_table(B):
     """The backward on an input population's table (one delay slot, n_pre != n_post)."""

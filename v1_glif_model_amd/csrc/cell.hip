@@ -2422,7 +2422,7 @@ int glif_step_backward(glif_cell *cc, int32_t B, const uint8_t *lgn, const uint8
     const Table *g_of = nullptr;
     auto run = [&](const Table *t, const float *x, int32_t counts, float *dz, float *dw) {
         const bool ready = g_of && same_g_layout(g_of, t);
-        const int r = syn_bwd_run(t, x, w.dy, B, counts, dz, dw, w.G, ready, s);
+        const int r = syn_bwd_run(t, x, w.dy, B, counts, dz, dw, w.G, ready, nullptr, s);
         if (!r && (dz || dw)) g_of = t;
         return r;
     };

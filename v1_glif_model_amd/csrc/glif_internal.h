@@ -119,6 +119,10 @@ struct Table {
     // {first column, columns, first position, end position} (kDwUnitEntries)
     int32_t n_dwu = 0;
     int4 *dwu = nullptr;          // [n_dwu]
+    // columns whose units hold one column each (a column of more than kDwUnitEntries synapses
+    // spreads over several): {column, first unit, units, 0}, for the chunked dz pass
+    int32_t n_dzc = 0;
+    int4 *dzc = nullptr;          // [n_dzc]
     int32_t *ph_ptr = nullptr;    // [n_types * n_cols + 1]
     int32_t *ph_order = nullptr;  // [n_syn]       synapse id at position k
     uint2 *ph_pw = nullptr;       // [n_syn]       {post, weight bits}
@@ -237,11 +241,12 @@ inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) 
 int batch_pad(int B);
 // The op's custom gradient (glif_syn_bwd) on a given G buffer of syn_g_floats(t, B) floats;
 // g_ready: G already holds this dy's rows in t's layout (built for a table with
-// same_g_layout), so only dz / dW are computed.
+// same_g_layout), so only dz / dW are computed.  partial: n_dwu * batch_pad(B) floats for the
+// unit dz pass of tables with few or long columns (nullptr: the walks only).
 size_t syn_g_floats(const Table *t, int32_t B);
 bool same_g_layout(const Table *a, const Table *b);
 int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int32_t counts, float *dz, float *dw,
-                float *G, bool g_ready, hipStream_t s);
+                float *G, bool g_ready, float *partial, hipStream_t s);
 // Lanes per column for the column-grouped kernels (16, 32 or 64).
 int sub_wave_for(const Table *t);
 // Blocks for `items` sub-waves of L lanes (capped; kernels grid-stride).

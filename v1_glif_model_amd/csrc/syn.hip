@@ -288,6 +288,79 @@ __device__ inline void syn_dw_body(const SynDwArgs &a, int64_t bid) {
 }
 
 
+// dz over the same work units, for tables whose grouped walk would run on few waves (few or
+// long columns: the LGN and background tables).  A wave per unit: in a run of whole columns
+// lane l sums column first + l over its synapses in column order straight into dz; in a
+// one-column unit (a whole column or one chunk of a long one) each lane sums every 64th
+// synapse, the wave adds the lanes' sums in a fixed butterfly order into partial[unit], and
+// k_dz_chunks adds a column's units in order.  Each term is w * G[row][b], as the walks form it.
+struct DzUnitArgs {
+    int64_t n_cols;
+    int32_t B, hm, lm, R;  // G row of entry p: (p >> 24) * hm + (p & kLow24) * lm, R floats
+    const int4 *units;
+    int32_t n_units;
+    const int32_t *col_ptr;
+    const uint32_t *ps;
+    const float *w;       // column-grouped weights
+    const float *G;
+    float *dz;            // [B][n_cols]
+    float *partial;       // [n_units][R]
+};
+
+template <int BP>
+__device__ inline void dz_unit_body(const DzUnitArgs &a, int64_t bid) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t ui = bid * (blockDim.x / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (ui >= a.n_units) return;  // the whole wave leaves together
+    const int4 un = a.units[ui];
+    float acc[BP];
+#pragma unroll
+    for (int b = 0; b < BP; ++b) acc[b] = 0.0f;
+    const bool run = un.y > 1;
+    int32_t k = run ? (lane < un.y ? a.col_ptr[un.x + lane] : 0) : un.z + lane;
+    const int32_t k_end = run ? (lane < un.y ? a.col_ptr[un.x + lane + 1] : 0) : un.w;
+    const int32_t step = run ? 1 : kWave;
+    for (; k < k_end; k += step) {
+        const uint32_t p = a.ps[k];
+        const float wk = a.w[k];
+        const float *g = a.G + (static_cast<int64_t>(p >> 24) * a.hm + static_cast<int64_t>(p & kLow24) * a.lm) * a.R;
+#pragma unroll
+        for (int b = 0; b < BP; ++b)
+            if (b < a.B) acc[b] = acc[b] + wk * g[b];
+    }
+    if (run) {
+        if (lane < un.y)
+#pragma unroll
+            for (int b = 0; b < BP; ++b)
+                if (b < a.B) a.dz[static_cast<int64_t>(b) * a.n_cols + un.x + lane] = acc[b];
+        return;
+    }
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1)
+#pragma unroll
+        for (int b = 0; b < BP; ++b) acc[b] = acc[b] + __shfl_xor(acc[b], o, kWave);
+    if (lane == 0)
+#pragma unroll
+        for (int b = 0; b < BP; ++b)
+            if (b < a.B) a.partial[ui * a.R + b] = acc[b];
+}
+
+template <int BP>
+__global__ void __launch_bounds__(kBlock) k_dz_units(DzUnitArgs a) { dz_unit_body<BP>(a, blockIdx.x); }
+
+// dz of the one-column units' columns: thread per (column, b), the column's units in order.
+__global__ void __launch_bounds__(kBlock)
+    k_dz_chunks(const int4 *__restrict__ dzc, int32_t n_dzc, const float *__restrict__ partial, int32_t B, int32_t R,
+                int64_t n_cols, float *__restrict__ dz) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(n_dzc) * B) return;
+    const int4 d = dzc[i / B];
+    const int b = static_cast<int>(i % B);
+    float s = partial[static_cast<int64_t>(d.y) * R + b];
+    for (int u = 1; u < d.z; ++u) s = s + partial[static_cast<int64_t>(d.y + u) * R + b];
+    dz[static_cast<int64_t>(b) * n_cols + d.x] = s;
+}
+
 // The grouped dz walk (the first walk_blocks workgroups) beside the weight-gradient pass of
 // the active columns (the rest): both read G only, the walk is bound by its gathers' latency,
 // and one launch overlaps them.
@@ -315,6 +388,7 @@ struct SynWs {
     uint32_t *cm;      // [n_slots * pre_pad] batch masks (deterministic forward)
     uint64_t *cbits;   // [n_slots * pre_pad / 64] activity bitmaps
     float *G;          // the custom gradient's projection
+    float *partial;    // [n_dwu][padded B] the unit dz pass's one-column sums
 };
 
 // with_G: the backward's projection G too (the forward does not use it)
@@ -326,7 +400,10 @@ static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes, bool 
     w.cbits = cv.take<uint64_t>(static_cast<size_t>(t->n_slots) * pre_pad / 64);
     // G: a row per (type, post), or per (post, own type) with the table's compact rows
     const int rows = t->og.rows ? t->og.rows : t->n_types;
-    if (with_G) w.G = cv.take<float>(static_cast<size_t>(t->n_post) * rows * batch_pad(B));
+    if (with_G) {
+        w.G = cv.take<float>(static_cast<size_t>(t->n_post) * rows * batch_pad(B));
+        w.partial = cv.take<float>(std::max<size_t>(static_cast<size_t>(t->n_dwu) * batch_pad(B), 1));
+    }
     if (bytes) *bytes = cv.off;
     return w;
 }
@@ -488,8 +565,8 @@ int glif_syn_bwd(const glif_table *tt, const float *z, const float *dy, int32_t 
     const Table *t = reinterpret_cast<const Table *>(tt);
     size_t need = glif_syn_workspace(tt, B);
     if (!ws || ws_bytes < need) return fail(GLIF_ENOMEM, "workspace too small");
-    return syn_bwd_run(t, z, dy, B, counts, dz, dw, carve_syn(ws, t, B, nullptr).G, false,
-                       static_cast<hipStream_t>(stream));
+    const SynWs w = carve_syn(ws, t, B, nullptr);
+    return syn_bwd_run(t, z, dy, B, counts, dz, dw, w.G, false, w.partial, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"
@@ -507,8 +584,20 @@ bool same_g_layout(const Table *a, const Table *b) {
            std::memcmp(a->basis_host, b->basis_host, sizeof(float) * a->n_types * a->n_basis) == 0;
 }
 
+// The unit dz pass replaces the walk for tables with a column longer than this: the walk
+// sums a column on one lane per 4 batch entries, so its time is the longest column's serial
+// gather chain (a 6600-synapse column: ~4 ms), while the units split long columns over many
+// waves and cost at most ~1.5x the walk on short ones (runs of short columns use few lanes).
+constexpr int32_t kUnitDzMinColLen = 2 * kDwUnitEntries;
+
+template <int BP>
+static void launch_dz_units(const DzUnitArgs &da, hipStream_t s) {
+    hipLaunchKernelGGL(k_dz_units<BP>, dim3(static_cast<unsigned>(ceil_div(da.n_units, kBlock / kWave))),
+                       dim3(kBlock), 0, s, da);
+}
+
 int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int32_t counts, float *dz, float *dw,
-                float *G, bool g_ready, hipStream_t s) {
+                float *G, bool g_ready, float *partial, hipStream_t s) {
     if (!dz && !dw) return GLIF_OK;
     const int Bp = batch_pad(B);
     // the table's own compact rows (post * rows + rank) when it has them, else type-major rows
@@ -538,6 +627,27 @@ int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int3
                            t->n_types, t->n_basis, nullptr, rows, gP, G, g_blocks, dw, n_fill);
     }
     GLIF_HIP(hipGetLastError());
+    // dz over work units instead of a walk whose time the longest column sets (the background
+    // table's few, long columns)
+    const bool dz_units = dz && partial && t->n_dwu > 0 && t->max_col_len > kUnitDzMinColLen;
+    if (dz_units) {
+        DzUnitArgs ua{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, t->dwu, t->n_dwu, t->col_ptr,
+                      cmp ? oc.ps : t->ps, t->w_col, G, dz, partial};
+        switch (Bp) {
+            case 4: launch_dz_units<4>(ua, s); break;
+            case 8: launch_dz_units<8>(ua, s); break;
+            case 16: launch_dz_units<16>(ua, s); break;
+            default: launch_dz_units<32>(ua, s); break;
+        }
+        GLIF_HIP(hipGetLastError());
+        if (t->n_dzc > 0) {
+            hipLaunchKernelGGL(k_dz_chunks, dim3(static_cast<unsigned>(ceil_div(static_cast<int64_t>(t->n_dzc) * B, kBlock))),
+                               dim3(kBlock), 0, s, t->dzc, t->n_dzc, partial, B, Bp, t->n_cols, dz);
+            GLIF_HIP(hipGetLastError());
+        }
+        dz = nullptr;   // done; the passes below compute dW only
+        if (!dw) return GLIF_OK;
+    }
     if (grouped) {
         // the grouped row-sliced walk for dz beside the active columns' dW (every active
         // synapse's written once, in reference order)

@@ -243,7 +243,7 @@ static void free_table(Table *t) {
     free_plan(t->pinv);
     void *ptrs[] = {t->basis, t->col_ptr, t->order, t->ps, t->w_col, t->row_ptr, t->perm,
                     t->pd, t->sid_row, t->w_row, t->ph_ptr, t->ph_order, t->ph_pw, t->ell_pw, t->ell_src,
-                    t->chunk_desc, t->dwu, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src,
+                    t->chunk_desc, t->dwu, t->dzc, t->pidx, t->order_inv, t->ph_inv, t->ph_src, t->gs_seg, t->gs_pw, t->gs_src,
                     t->cg.ps, t->cg.ph_pw, t->cg.gs_seg, t->cg.gs_pw, t->cg.gs_src, t->cg.gtype,
                     t->og.ps, t->og.ph_pw, t->og.gs_seg, t->og.gs_pw, t->og.gs_src, t->og.gtype};
     for (void *p : ptrs)
@@ -556,6 +556,15 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         c = m;
     }
     t->n_dwu = static_cast<int32_t>(dwu.size());
+    std::vector<int4> dzc;
+    for (int32_t u = 0; u < t->n_dwu;) {
+        if (dwu[u].y != 1) { ++u; continue; }
+        int32_t v = u + 1;
+        while (v < t->n_dwu && dwu[v].y == 1 && dwu[v].x == dwu[u].x) ++v;
+        dzc.push_back(make_int4(dwu[u].x, u, v - u, 0));
+        u = v;
+    }
+    t->n_dzc = static_cast<int32_t>(dzc.size());
     t->basis_host = new float[static_cast<size_t>(n_types) * n_basis];
     std::memcpy(t->basis_host, basis, sizeof(float) * n_types * n_basis);
     int rc = GLIF_OK;
@@ -566,6 +575,7 @@ int glif_table_create(const int64_t *post, const int64_t *col, const uint8_t *sy
         (rc = upload(&t->row_ptr, row_ptr.data(), row_ptr.size())) ||
         (rc = upload(&t->chunk_desc, chunk_desc.data(), chunk_desc.size())) ||
         (rc = upload(&t->dwu, dwu.data(), dwu.size())) ||
+        (rc = upload(&t->dzc, dzc.data(), dzc.size())) ||
         (rc = upload(&t->perm, perm.data(), perm.size())) ||
         (rc = upload(&t->pd, pd.data(), pd.size())) ||
         (with_pidx && (rc = upload(&t->pidx, pidx.data(), pidx.size()))) ||
