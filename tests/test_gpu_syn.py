@@ -238,6 +238,57 @@ def test_syn_bwd_long_columns(B):
     np.testing.assert_array_equal(dw_only.cpu().numpy(), dw)
 
 
+@pytest.mark.parametrize("B", [1, 5, 17])
+def test_syn_fwd_long_columns(B):
+    """Both forwards on the long-column table: the event push over the work units (a chunked
+    column's chunks on waves of their own), spikes and Poisson counts; the pull bit-exact."""
+    from v1_glif_model_amd.ops import SynapseTable
+    tab = _long_column_table(seed=4)
+    rng = np.random.default_rng(B + 90)
+    basis = rng.random((5, 3)).astype(np.float32)
+    t = SynapseTable(tab.indices, tab.syn_id, (tab.n_post, tab.n_cols), basis)
+    t.set_weights(torch.tensor(tab.weight, device="cuda"))
+    for counts in (False, True):
+        z = (rng.random((B, tab.n_cols)) < 0.5).astype(np.float32)
+        if counts:
+            z *= rng.integers(1, 4, z.shape)
+        zt = torch.tensor(z, device="cuda")
+        got = t.forward(zt, counts=counts, mode="event").cpu().numpy()
+        ref = orc.syn_fwd(tab, z, basis, use_count=counts)
+        scale = dense.syn_fwd_abs(tab, z, basis, use_count=counts)
+        assert np.max(np.abs(got - ref) - 1e-5 * scale) <= 1e-6
+        assert np.max(np.abs(got - dense.syn_fwd_f64(tab, z, basis, use_count=counts)) - 1e-5 * scale) <= 1e-6
+        det = t.forward(zt, counts=counts, mode="deterministic").cpu().numpy()
+        np.testing.assert_array_equal(det.view(np.uint32), ref.view(np.uint32))
+
+
+def test_syn_fwd_event_column_scan():
+    """The event push's column scan (a wave per 64 columns), taken by tables of at least
+    131,072 columns with no long column: 150,001 columns of 0-3 synapses."""
+    from v1_glif_model_amd.tables import SynapseTable as Tab
+    from v1_glif_model_amd.ops import SynapseTable
+    rng = np.random.default_rng(11)
+    n_post, n_cols = 2000, 150001
+    lens = rng.integers(0, 4, n_cols)
+    col = np.repeat(np.arange(n_cols), lens)
+    post = rng.integers(0, n_post, col.size)
+    key = post * n_cols + col
+    _, first = np.unique(key, return_index=True)      # distinct (post, column) pairs
+    post, col = post[first], col[first]
+    o = np.lexsort((col, post))
+    tab = Tab(post=post[o].astype(np.int64), col=col[o].astype(np.int64),
+              weight=rng.normal(0, 1, o.size).astype(np.float32),
+              syn_id=rng.integers(0, 3, o.size).astype(np.uint8), n_post=n_post, n_cols=n_cols)
+    basis = rng.random((3, 2)).astype(np.float32)
+    t = SynapseTable(tab.indices, tab.syn_id, (n_post, n_cols), basis)
+    t.set_weights(torch.tensor(tab.weight, device="cuda"))
+    z = (rng.random((3, n_cols)) < 0.05).astype(np.float32)
+    got = t.forward(torch.tensor(z, device="cuda"), mode="event").cpu().numpy()
+    ref = orc.syn_fwd(tab, z, basis)
+    scale = dense.syn_fwd_abs(tab, z, basis)
+    assert np.max(np.abs(got - ref) - 1e-5 * scale) <= 1e-6
+
+
 @pytest.mark.parametrize("B", [5, 9])
 def test_syn_bwd_input_table(B):
     """The backward on an input population's table (one delay slot, n_pre != n_post)."""

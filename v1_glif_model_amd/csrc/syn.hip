@@ -12,6 +12,16 @@
 
 namespace glif {
 
+// Tables with a column longer than this take the event push and dz over work units (the
+// background table's shape).  The dz walk sums a column on one lane per 4 batch entries and the
+// column scan pushes it on one wave, so their time is the longest column's serial chain (a
+// 6600-synapse column: ~4 ms for dz, ~5 ms for the push); the units split long columns over many
+// waves and cost at most ~1.5x the walk on short ones (runs of short columns use few lanes).
+constexpr int32_t kUnitDzMinColLen = 2 * kDwUnitEntries;
+// The event push takes the units too when the column scan (a wave per 64 columns) would run on
+// fewer waves than this (the LGN table's 17,400 columns: 272 waves).
+constexpr int64_t kPushUnitsMaxScanWaves = 2048;
+
 // ---------------------------------------------------------------- forward ----
 // Deterministic pull: thread per (b, post) walks the post's row in ascending
 // (column, synapse id) -- the order in which TF's CPU UnsortedSegmentSum meets the
@@ -48,6 +58,43 @@ __global__ void __launch_bounds__(kBlock)
 // Event push straight from z [B][n_cols]: a wave per 64 consecutive columns builds each
 // column's batch mask (z > 0, the test of tf.where at models.py:128-130), and all 64 lanes
 // push the wave's active columns one after another.  No column list, no count pass.
+// The event push over the table's work units (a run of up to 64 short columns, or a chunk of
+// at most kDwUnitEntries synapses of a long column), a wave per unit: the lanes hold the
+// run's columns' batch masks, and all 64 lanes push each active column's share of the unit.
+// For tables whose column scan would run on few waves (few columns, or long ones).
+template <bool COUNTS>
+__global__ void __launch_bounds__(kBlock)
+    k_syn_push_units(const float *__restrict__ z, int32_t B, int64_t n_cols, const int4 *__restrict__ units,
+                     int32_t n_units, const int32_t *__restrict__ col_ptr, const uint32_t *__restrict__ ps,
+                     const float *__restrict__ w, const float *__restrict__ basis, int n_types, int nb,
+                     int32_t n_post, float *__restrict__ I) {
+    extern __shared__ float basis_lds[];
+    load_basis_lds(basis_lds, basis, n_types * nb);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t ui = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) +
+                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    if (ui >= n_units) return;  // the whole wave leaves together
+    const int4 un = units[ui];
+    uint32_t m = 0u;
+    if (lane < un.y)
+        for (int b = 0; b < B; ++b) m |= (z[b * n_cols + un.x + lane] > 0.0f ? 1u : 0u) << b;
+    uint64_t act = __ballot(m != 0u);
+    while (act) {
+        const int l = __builtin_ctzll(act);
+        act &= act - 1ull;
+        const uint32_t ml = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), l));
+        const int64_t cl = un.x + l;
+        const int32_t lo = un.y == 1 ? un.z : col_ptr[cl];
+        const int32_t hi = un.y == 1 ? un.w : col_ptr[cl + 1];
+        if (COUNTS)
+            push_column<kWave>(lane, lo, hi, ml, MultF32{z + cl, n_cols}, ps, w, basis_lds, nb,
+                               static_cast<int64_t>(n_post) * nb, nb, 1, I);
+        else
+            push_column<kWave>(lane, lo, hi, ml, MultOne{}, ps, w, basis_lds, nb, static_cast<int64_t>(n_post) * nb,
+                               nb, 1, I);
+    }
+}
+
 template <bool COUNTS>
 __global__ void __launch_bounds__(kBlock)
     k_syn_push_scan(const float *__restrict__ z, int32_t B, int64_t n_cols, const int32_t *__restrict__ col_ptr,
@@ -467,6 +514,17 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
     }
     int rc = launch_fill_u32(I, 0u, static_cast<size_t>(nI) * t->n_basis, s);
     if (rc) return rc;
+    if (t->n_dwu > 0 && (ceil_div(t->n_cols, kWave) < kPushUnitsMaxScanWaves || t->max_col_len > kUnitDzMinColLen)) {
+        const dim3 grid(static_cast<unsigned>(ceil_div(t->n_dwu, kBlock / kWave)));
+        if (counts)
+            hipLaunchKernelGGL(k_syn_push_units<true>, grid, dim3(kBlock), lds, s, z, B, t->n_cols, t->dwu, t->n_dwu,
+                               t->col_ptr, t->ps, t->w_col, t->basis, t->n_types, t->n_basis, t->n_post, I);
+        else
+            hipLaunchKernelGGL(k_syn_push_units<false>, grid, dim3(kBlock), lds, s, z, B, t->n_cols, t->dwu, t->n_dwu,
+                               t->col_ptr, t->ps, t->w_col, t->basis, t->n_types, t->n_basis, t->n_post, I);
+        GLIF_HIP(hipGetLastError());
+        return GLIF_OK;
+    }
     const dim3 grid(static_cast<unsigned>(std::max<int64_t>(
         1, std::min<int64_t>(ceil_div(ceil_div(t->n_cols, kWave), kBlock / kWave), 32768))));
     if (counts)
@@ -583,12 +641,6 @@ bool same_g_layout(const Table *a, const Table *b) {
            a->n_basis == b->n_basis &&
            std::memcmp(a->basis_host, b->basis_host, sizeof(float) * a->n_types * a->n_basis) == 0;
 }
-
-// The unit dz pass replaces the walk for tables with a column longer than this: the walk
-// sums a column on one lane per 4 batch entries, so its time is the longest column's serial
-// gather chain (a 6600-synapse column: ~4 ms), while the units split long columns over many
-// waves and cost at most ~1.5x the walk on short ones (runs of short columns use few lanes).
-constexpr int32_t kUnitDzMinColLen = 2 * kDwUnitEntries;
 
 template <int BP>
 static void launch_dz_units(const DzUnitArgs &da, hipStream_t s) {
