@@ -21,6 +21,8 @@ constexpr int32_t kUnitDzMinColLen = 2 * kDwUnitEntries;
 // The event push takes the units too when the column scan (a wave per 64 columns) would run on
 // fewer waves than this (the LGN table's 17,400 columns: 272 waves).
 constexpr int64_t kPushUnitsMaxScanWaves = 2048;
+// dz takes the units too when the walk would run on fewer lanes than this.
+constexpr int64_t kUnitDzMaxWalkLanes = 1024 * kWave;
 
 // ---------------------------------------------------------------- forward ----
 // Deterministic pull: thread per (b, post) walks the post's row in ascending
@@ -335,12 +337,13 @@ __device__ inline void syn_dw_body(const SynDwArgs &a, int64_t bid) {
 }
 
 
-// dz over the same work units, for tables whose grouped walk would run on few waves (few or
-// long columns: the LGN and background tables).  A wave per unit: in a run of whole columns
-// lane l sums column first + l over its synapses in column order straight into dz; in a
-// one-column unit (a whole column or one chunk of a long one) each lane sums every 64th
-// synapse, the wave adds the lanes' sums in a fixed butterfly order into partial[unit], and
-// k_dz_chunks adds a column's units in order.  Each term is w * G[row][b], as the walks form it.
+// dz over the same work units, for tables whose walk runs on few lanes or whose time a long
+// column sets (the input tables).  A wave per unit.  A run of y columns gives each column
+// L = 64 / (y rounded up to a power of 2) lanes, which sum every L-th synapse of the column and
+// add their sums in a fixed butterfly order; lane 0 of the column's lanes writes dz.  A
+// one-column unit (a whole column or one chunk of a long one) uses all 64 lanes the same way
+// into partial[unit], and k_dz_chunks adds a column's units in order.  Each term is
+// w * G[row][b], as the walks form it.
 struct DzUnitArgs {
     int64_t n_cols;
     int32_t B, hm, lm, R;  // G row of entry p: (p >> 24) * hm + (p & kLow24) * lm, R floats
@@ -360,14 +363,22 @@ __device__ inline void dz_unit_body(const DzUnitArgs &a, int64_t bid) {
     const int64_t ui = bid * (blockDim.x / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     if (ui >= a.n_units) return;  // the whole wave leaves together
     const int4 un = a.units[ui];
+    int sh = 0;
+    while ((1 << sh) < un.y) ++sh;  // un.y <= 64: sh <= 6, the same in every lane
+    const int L = kWave >> sh;
+    const int j = lane / L, sl = lane % L;
     float acc[BP];
 #pragma unroll
     for (int b = 0; b < BP; ++b) acc[b] = 0.0f;
-    const bool run = un.y > 1;
-    int32_t k = run ? (lane < un.y ? a.col_ptr[un.x + lane] : 0) : un.z + lane;
-    const int32_t k_end = run ? (lane < un.y ? a.col_ptr[un.x + lane + 1] : 0) : un.w;
-    const int32_t step = run ? 1 : kWave;
-    for (; k < k_end; k += step) {
+    int32_t k = 0, k_end = 0;
+    if (un.y == 1) {
+        k = un.z + lane;
+        k_end = un.w;
+    } else if (j < un.y) {
+        k = a.col_ptr[un.x + j] + sl;
+        k_end = a.col_ptr[un.x + j + 1];
+    }
+    for (; k < k_end; k += L) {
         const uint32_t p = a.ps[k];
         const float wk = a.w[k];
         const float *g = a.G + (static_cast<int64_t>(p >> 24) * a.hm + static_cast<int64_t>(p & kLow24) * a.lm) * a.R;
@@ -375,21 +386,19 @@ __device__ inline void dz_unit_body(const DzUnitArgs &a, int64_t bid) {
         for (int b = 0; b < BP; ++b)
             if (b < a.B) acc[b] = acc[b] + wk * g[b];
     }
-    if (run) {
-        if (lane < un.y)
-#pragma unroll
-            for (int b = 0; b < BP; ++b)
-                if (b < a.B) a.dz[static_cast<int64_t>(b) * a.n_cols + un.x + lane] = acc[b];
-        return;
-    }
-#pragma unroll
-    for (int o = kWave / 2; o >= 1; o >>= 1)
+    for (int o = L / 2; o >= 1; o >>= 1)
 #pragma unroll
         for (int b = 0; b < BP; ++b) acc[b] = acc[b] + __shfl_xor(acc[b], o, kWave);
-    if (lane == 0)
+    if (un.y == 1) {
+        if (lane == 0)
+#pragma unroll
+            for (int b = 0; b < BP; ++b)
+                if (b < a.B) a.partial[ui * a.R + b] = acc[b];
+    } else if (sl == 0 && j < un.y) {
 #pragma unroll
         for (int b = 0; b < BP; ++b)
-            if (b < a.B) a.partial[ui * a.R + b] = acc[b];
+            if (b < a.B) a.dz[static_cast<int64_t>(b) * a.n_cols + un.x + j] = acc[b];
+    }
 }
 
 template <int BP>
@@ -407,6 +416,8 @@ __global__ void __launch_bounds__(kBlock)
     for (int u = 1; u < d.z; ++u) s = s + partial[static_cast<int64_t>(d.y + u) * R + b];
     dz[static_cast<int64_t>(b) * n_cols + d.x] = s;
 }
+
+__global__ void __launch_bounds__(kBlock) k_syn_dw_units(SynDwArgs da) { syn_dw_body(da, blockIdx.x); }
 
 // The grouped dz walk (the first walk_blocks workgroups) beside the weight-gradient pass of
 // the active columns (the rest): both read G only, the walk is bound by its gathers' latency,
@@ -661,11 +672,20 @@ int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int3
     ProfScope prof(kProfSynBwd, s);
     int rc;
     const bool grouped = (cmp ? oc.n_gs : t->n_gs) && (Bp == 8 || Bp == 16);
-    // G, with the zero fill of dW beside it when the grouped path's weight-gradient pass
-    // writes only the active synapses
+    // the work units instead of a walk whose time the longest column sets (the background
+    // table's few, long columns) or that runs on few lanes (the LGN table's 17,400 columns):
+    // for dz when the caller gives their partial sums room, and for dW, whose grouped-path
+    // pass always runs over them
+    const int64_t walk_lanes = (grouped ? t->n_groups : t->n_cols) * (Bp / 4);
+    const bool prefer_units =
+        t->n_dwu > 0 && (t->max_col_len > kUnitDzMinColLen || walk_lanes < kUnitDzMaxWalkLanes);
+    const bool dz_units = dz && partial && prefer_units;
+    const bool dw_units = dw && (grouped || prefer_units);
+    // G, with the zero fill of dW beside it when the units' weight-gradient pass writes only
+    // the active synapses
     const int gP = make_G_posts(B, t->n_basis);
     const int g_blocks = g_ready ? 0 : static_cast<int>(ceil_div(static_cast<int64_t>(t->n_post), gP));
-    const int fill_blocks = grouped && dw && t->n_syn ? 256 : 0;
+    const int fill_blocks = dw_units && t->n_syn ? 256 : 0;
     const int64_t n_fill = fill_blocks ? t->n_syn : 0;
     const dim3 g_grid(g_blocks + fill_blocks);
     const size_t g_lds = sizeof(float) * (((t->n_types * t->n_basis + 3) & ~3) + static_cast<size_t>(B) * gP * t->n_basis);
@@ -679,9 +699,6 @@ int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int3
                            t->n_types, t->n_basis, nullptr, rows, gP, G, g_blocks, dw, n_fill);
     }
     GLIF_HIP(hipGetLastError());
-    // dz over work units instead of a walk whose time the longest column sets (the background
-    // table's few, long columns)
-    const bool dz_units = dz && partial && t->n_dwu > 0 && t->max_col_len > kUnitDzMinColLen;
     if (dz_units) {
         DzUnitArgs ua{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, t->dwu, t->n_dwu, t->col_ptr,
                       cmp ? oc.ps : t->ps, t->w_col, G, dz, partial};
@@ -700,15 +717,16 @@ int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int3
         dz = nullptr;   // done; the passes below compute dW only
         if (!dw) return GLIF_OK;
     }
-    if (grouped) {
-        // the grouped row-sliced walk for dz beside the active columns' dW (every active
-        // synapse's written once, in reference order)
+    if (grouped || (dw_units && !dz)) {
+        // the grouped row-sliced walk for dz (when grouped and dz is still wanted) beside the
+        // active columns' dW over the units (every active synapse's written once, in reference
+        // order)
         ActDense act{z, dz, t->n_cols, counts};
         GsArgs ga{t->n_cols, (t->n_cols + kGsCols - 1) / kGsCols, B, cmp ? oc.gs_seg : t->gs_seg,
                   cmp ? oc.gs_pw : t->gs_pw, G};
         SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->dwu, t->n_dwu,
                      t->col_ptr, cmp ? oc.ps : t->ps, t->order, G, dw};
-        const int LG = Bp / 4;
+        const int LG = grouped ? Bp / 4 : 2;   // no walk blocks when not grouped
         const int walk_blocks = dz ? static_cast<int>(ceil_div(t->n_groups * LG, kBlock)) : 0;
         const int dw_blocks = dw ? static_cast<int>(ceil_div(t->n_dwu, kBlock / kWave)) : 0;
         const dim3 grid(walk_blocks + dw_blocks);
@@ -717,6 +735,16 @@ int syn_bwd_run(const Table *t, const float *z, const float *dy, int32_t B, int3
         else hipLaunchKernelGGL(k_syn_bwd_gs<4>, grid, dim3(kBlock), 0, s, ga, act, walk_blocks, da);
         GLIF_HIP(hipGetLastError());
         return GLIF_OK;
+    }
+    if (dw_units) {
+        // dW over the units (filled beside G), dz by the column walk below (the cell's
+        // per-step backward gives no room for partial sums)
+        SynDwArgs da{t->n_cols, B, cmp ? 1 : t->n_post, cmp ? rows : 1, Bp, counts, z, t->dwu, t->n_dwu,
+                     t->col_ptr, cmp ? oc.ps : t->ps, t->order, G, dw};
+        hipLaunchKernelGGL(k_syn_dw_units, dim3(static_cast<unsigned>(ceil_div(t->n_dwu, kBlock / kWave))),
+                           dim3(kBlock), 0, s, da);
+        GLIF_HIP(hipGetLastError());
+        dw = nullptr;
     }
     // the type-phased column walk writes the active columns' synapses; the rest stay 0
     if (dw && (rc = launch_fill_u32(dw, 0u, static_cast<size_t>(t->n_syn), s))) return rc;
