@@ -80,8 +80,13 @@ def _args():
                          "type-major (a row per type and neuron)")
     ap.add_argument("--op", action="store_true",
                     help="time the op-level entry points instead (calculate_synaptic_currents forward in "
-                         "both modes and its custom gradient) on the config-2 recurrent table, B=5, "
-                         "z_buf spikes at 5 Hz")
+                         "both modes and its custom gradient) on a config-2 table (--op-table, default "
+                         "the recurrent one with z_buf spikes at 5 Hz), B = --op-batch")
+    ap.add_argument("--op-table", default="rec", choices=["rec", "lgn", "bkg"],
+                    help="with --op: the config-2 table the op runs on: rec (z_buf spikes at 5 Hz), lgn "
+                         "(one tick of the config's LGN spikes) or bkg (one tick of its Poisson "
+                         "background counts, counts mode)")
+    ap.add_argument("--op-batch", type=int, default=5, help="with --op: the batch size (1-32)")
     ap.add_argument("--step-loop", action="store_true",
                     help="time the Keras-RNN form of the config-2 training step instead: a loop of T "
                          "V1Column.call steps differentiated by autograd step by step (glif_step_backward "
@@ -361,8 +366,10 @@ def bench_step_loop(args):
 
 
 def bench_op(args):
-    """Op-level timing (glif_syn_fwd / glif_syn_bwd, models.py:103-263) on the config-2
-    recurrent table: z_buf [5][D*N] Bernoulli(0.005) spikes, dy [5*N][nb] normal."""
+    """Op-level timing (glif_syn_fwd / glif_syn_bwd, models.py:103-263) on a config-2 table:
+    the recurrent one with z_buf [B][D*N] Bernoulli(0.005) spikes, or an input table with one
+    tick of the config's LGN spikes / background counts (models.py:814-940); dy [B*N][nb]
+    normal."""
     import numpy as np
     import torch
     from v1_glif_model_amd import synthetic as sy
@@ -375,19 +382,30 @@ def bench_op(args):
     if args.class_types:
         net = sy.class_types(net, n_classes=args.class_types)
     tb = build_cell_tables(net)
-    N, D, B, nb = tb.n_neurons, tb.max_delay, 5, tb.n_basis
-    t = SynapseTable(np.stack([tb.rec.post, tb.rec.col], -1), tb.rec.syn_id, (N, tb.rec.n_cols), tb.basis,
-                     n_delay_slots=D)
-    t.set_weights(torch.tensor(tb.rec.weight, device="cuda"))
+    N, D, B, nb = tb.n_neurons, tb.max_delay, args.op_batch, tb.n_basis
+    if not 1 <= B <= 32:
+        raise SystemExit("--op-batch must be in [1, 32]")
+    pop = {"rec": tb.rec, "lgn": tb.lgn, "bkg": tb.bkg}[args.op_table]
+    counts = args.op_table == "bkg"
+    t = SynapseTable(np.stack([pop.post, pop.col], -1), pop.syn_id, (N, pop.n_cols), tb.basis,
+                     n_delay_slots=D if args.op_table == "rec" else 1)
+    t.set_weights(torch.tensor(pop.weight, device="cuda"))
     rng = np.random.default_rng(3)
-    z = torch.tensor((rng.uniform(size=(B, D * N)) < 0.005).astype(np.float32), device="cuda")
+    if args.op_table == "rec":
+        zc = (rng.uniform(size=(B, D * N)) < 0.005).astype(np.float32)
+        inputs = "z_buf density 0.005"
+    else:
+        lgn, bkg = sy.make_inputs(cfg, seed=1, seq_len=1, batch=B)
+        zc = (lgn if args.op_table == "lgn" else bkg)[0].astype(np.float32)
+        inputs = ("one tick of the config's LGN spikes" if args.op_table == "lgn" else
+                  "one tick of the config's Poisson background counts (counts mode)")
+    z = torch.tensor(zc, device="cuda")
     dy = torch.tensor(rng.normal(0, 1, (B * N, nb)).astype(np.float32), device="cuda")
-    zc = z.cpu().numpy()
-    events = int(sum(np.count_nonzero(zc[b][tb.rec.col]) for b in range(B)))
+    events = int(sum(np.count_nonzero(zc[b][pop.col]) for b in range(B)))
     out = {}
-    for name, fn in (("fwd_event", lambda: t.forward(z, mode="event")),
-                     ("fwd_deterministic", lambda: t.forward(z, mode="deterministic")),
-                     ("bwd", lambda: t.backward(z, dy))):
+    for name, fn in (("fwd_event", lambda: t.forward(z, counts=counts, mode="event")),
+                     ("fwd_deterministic", lambda: t.forward(z, counts=counts, mode="deterministic")),
+                     ("bwd", lambda: t.backward(z, dy, counts=counts))):
         for _ in range(max(args.warmup, 1)):
             fn()
         torch.cuda.synchronize()
@@ -398,16 +416,18 @@ def bench_op(args):
         e1.record()
         torch.cuda.synchronize()
         out[name] = e0.elapsed_time(e1) * 1000.0 / args.steps
-    S = tb.rec.n_syn
+    S = pop.n_syn
+    what = {"rec": f"config-2 recurrent table: {N} posts, {D} delay slots",
+            "lgn": f"config-2 LGN table: {N} posts, {pop.n_cols} inputs",
+            "bkg": f"config-2 background table: {N} posts, {pop.n_cols} inputs"}[args.op_table]
     print(json.dumps({
         "metric": "op-level synaptic-current forward / custom gradient, us per call",
         "value": round(out["fwd_event"] + out["bwd"], 2), "unit": "us per fwd+bwd call", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "higher_is_better": False, "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"config-2 recurrent table: {N} posts, {D} delay slots, {S} synapses, B={B}, "
-                               f"z_buf density 0.005 ({events} synapse events per call)",
-                   "neurons": N, "synapses": S, "batch": B, "syn_types": int(tb.basis.shape[0]),
-                   "receptors": int(nb)},
+        "config": {"workload": f"{what}, {S} synapses, B={B}, {inputs} ({events} synapse events per call)",
+                   "table": args.op_table, "neurons": N, "synapses": S, "batch": B,
+                   "syn_types": int(tb.basis.shape[0]), "receptors": int(nb)},
         "us_per_call": {k: round(v, 2) for k, v in out.items()},
         "synaptic_events_per_s": {"fwd_event": round(events / (out["fwd_event"] * 1e-6), 1),
                                   "fwd_deterministic": round(events / (out["fwd_deterministic"] * 1e-6), 1)},

@@ -473,8 +473,10 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
     const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     const int64_t nI = static_cast<int64_t>(B) * t->n_post;
     if (mode == GLIF_MODE_DETERMINISTIC) {
-        if (!counts && t->pidx && t->chunk_desc) {
-            // the resident chunk pull over activity bitmaps built from z (one step, t = 0)
+        if (!counts) {
+            // the row pulls over batch masks and activity bitmaps built from z (one step, t = 0):
+            // the resident chunk form where it fits, else the half-wave row pull (B * nb > 64,
+            // or bitmaps beyond LDS), which reads each entry once for all batch entries
             const int32_t pre_pad = static_cast<int32_t>((static_cast<int64_t>(t->n_pre) + 63) / 64 * 64);
             PullArgs pa{};
             pa.t = 0;
@@ -490,10 +492,11 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
             pa.os_n = t->n_basis;
             pa.W = pre_pad / 64;
             pa.Wl = 0;
-            pa.rec_chunks = t->n_chunks;
+            pa.rec_chunks = t->chunk_desc ? t->n_chunks : 0;
             pa.rec_cdesc = t->chunk_desc;
             pa.rec_row = t->row_ptr;
-            pa.rec_pidx = t->pidx;
+            pa.rec_pd = t->pd;
+            pa.rec_pidx = t->chunk_desc ? t->pidx : nullptr;   // no chunk form without both
             pa.rec_sid = t->sid_row;
             pa.rec_w = t->w_row;
             pa.zmask = w.cm;
@@ -501,25 +504,18 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
             pa.lbits = w.cbits;
             pa.basis = t->basis;
             pa.I = I;
-            if (pull_chunked(pa)) {
-                const int64_t n_mask = static_cast<int64_t>(t->n_slots) * pre_pad;
-                hipLaunchKernelGGL(k_op_colmask, dim3(ceil_div(n_mask, kBlock)), dim3(kBlock), 0, s, z, B, t->n_cols,
-                                   t->n_pre, t->n_slots, pre_pad, w.cm, w.cbits);
-                GLIF_HIP(hipGetLastError());
-                launch_pull_chunks(pa, s);
-                GLIF_HIP(hipGetLastError());
-                return GLIF_OK;
-            }
+            const int64_t n_mask = static_cast<int64_t>(t->n_slots) * pre_pad;
+            hipLaunchKernelGGL(k_op_colmask, dim3(ceil_div(n_mask, kBlock)), dim3(kBlock), 0, s, z, B, t->n_cols,
+                               t->n_pre, t->n_slots, pre_pad, w.cm, w.cbits);
+            GLIF_HIP(hipGetLastError());
+            launch_pull(pa, lds, s);
+            GLIF_HIP(hipGetLastError());
+            return GLIF_OK;
         }
+        // Poisson counts scale the weights: a thread per (b, post) over the post's row
         dim3 grid(ceil_div(nI, kBlock));
-        if (counts)
-            hipLaunchKernelGGL((k_syn_pull_dense<true>), grid, dim3(kBlock), lds, s, z, B, t->n_cols,
-                               t->n_post, t->n_pre, t->row_ptr, t->pd, t->sid_row, t->w_row, t->basis,
-                               t->n_types, t->n_basis, I);
-        else
-            hipLaunchKernelGGL((k_syn_pull_dense<false>), grid, dim3(kBlock), lds, s, z, B, t->n_cols,
-                               t->n_post, t->n_pre, t->row_ptr, t->pd, t->sid_row, t->w_row, t->basis,
-                               t->n_types, t->n_basis, I);
+        hipLaunchKernelGGL((k_syn_pull_dense<true>), grid, dim3(kBlock), lds, s, z, B, t->n_cols, t->n_post,
+                           t->n_pre, t->row_ptr, t->pd, t->sid_row, t->w_row, t->basis, t->n_types, t->n_basis, I);
         GLIF_HIP(hipGetLastError());
         return GLIF_OK;
     }
