@@ -54,7 +54,7 @@ def test_where_matches_argwhere(rows, cols, p):
 
 
 @pytest.mark.parametrize("seed", [0, 1])
-@pytest.mark.parametrize("B", [1, 3, 8, 20])
+@pytest.mark.parametrize("B", [1, 3, 8, 20, 32])
 def test_syn_fwd_deterministic_is_bit_exact(seed, B):
     tb, t, _ = _setup(seed=seed)
     rng = np.random.default_rng(100 + seed)
@@ -72,7 +72,7 @@ def test_syn_fwd_deterministic_input_table_bit_exact():
     t = SynapseTable(tb.lgn.indices, tb.lgn.syn_id, (tb.n_neurons, tb.lgn.n_cols), tb.basis)
     t.set_weights(torch.tensor(tb.lgn.weight, device="cuda"))
     rng = np.random.default_rng(12)
-    for B in (2, 9):
+    for B in (2, 9, 32):   # 32 x 5 receptors: the half-wave row pull, not the chunk form
         z = _spikes(rng, B, tb.lgn.n_cols, 0.1)
         got = t.forward(torch.tensor(z, device="cuda"), mode="deterministic").cpu().numpy()
         ref = orc.syn_fwd(tb.lgn, z, tb.basis)
