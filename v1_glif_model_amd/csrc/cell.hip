@@ -2131,7 +2131,6 @@ int glif_cell_backward(glif_cell *cc, int32_t B, int32_t T, const float *gz, con
     if (dw_lgn && (rc = launch_fill_u32(w.dw_lgn, 0u, tl->n_syn, s))) return rc;
     if (dw_bkg && (rc = launch_fill_u32(w.dw_bkg, 0u, tb->n_syn, s))) return rc;
 
-    const size_t lds = sizeof(float) * c->n_types * c->nb;
     const int Wwin = win_width(B), ring = ring_size(c), Rg = g_row(Wwin, B);
     if (static_cast<int64_t>(c->g_rows) * c->N * Rg * 4 >= (int64_t(1) << 32))
         return fail(GLIF_ERANGE, "G rows per neuron * n_neurons * G row * 4 bytes must be < 4 GiB");
