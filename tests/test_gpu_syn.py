@@ -265,28 +265,57 @@ def test_syn_fwd_long_columns(B):
 def test_syn_fwd_event_column_scan():
     """The event push's column scan (a wave per 64 columns), taken by tables of at least
     131,072 columns with no long column: 150,001 columns of 0-3 synapses."""
-    from v1_glif_model_amd.tables import SynapseTable as Tab
     from v1_glif_model_amd.ops import SynapseTable
-    rng = np.random.default_rng(11)
-    n_post, n_cols = 2000, 150001
-    lens = rng.integers(0, 4, n_cols)
-    col = np.repeat(np.arange(n_cols), lens)
-    post = rng.integers(0, n_post, col.size)
-    key = post * n_cols + col
-    _, first = np.unique(key, return_index=True)      # distinct (post, column) pairs
-    post, col = post[first], col[first]
-    o = np.lexsort((col, post))
-    tab = Tab(post=post[o].astype(np.int64), col=col[o].astype(np.int64),
-              weight=rng.normal(0, 1, o.size).astype(np.float32),
-              syn_id=rng.integers(0, 3, o.size).astype(np.uint8), n_post=n_post, n_cols=n_cols)
+    tab = _wide_table()
+    rng = np.random.default_rng(12)
     basis = rng.random((3, 2)).astype(np.float32)
-    t = SynapseTable(tab.indices, tab.syn_id, (n_post, n_cols), basis)
+    t = SynapseTable(tab.indices, tab.syn_id, (tab.n_post, tab.n_cols), basis)
     t.set_weights(torch.tensor(tab.weight, device="cuda"))
-    z = (rng.random((3, n_cols)) < 0.05).astype(np.float32)
+    z = (rng.random((3, tab.n_cols)) < 0.05).astype(np.float32)
     got = t.forward(torch.tensor(z, device="cuda"), mode="event").cpu().numpy()
     ref = orc.syn_fwd(tab, z, basis)
     scale = dense.syn_fwd_abs(tab, z, basis)
     assert np.max(np.abs(got - ref) - 1e-5 * scale) <= 1e-6
+
+
+def _wide_table(seed=11, n_post=2000, n_cols=150001, n_types=3):
+    """A table of many short columns (0-3 synapses each): its dz walk has enough lanes at every
+    batch width, so the op walks it (grouped or type-phased) instead of using the work units."""
+    from v1_glif_model_amd.tables import SynapseTable as Tab
+    rng = np.random.default_rng(seed)
+    col = np.repeat(np.arange(n_cols), rng.integers(0, 4, n_cols))
+    post = rng.integers(0, n_post, col.size)
+    _, first = np.unique(post * n_cols + col, return_index=True)   # distinct (post, column) pairs
+    post, col = post[first], col[first]
+    o = np.lexsort((col, post))
+    return Tab(post=post[o].astype(np.int64), col=col[o].astype(np.int64),
+               weight=rng.normal(0, 1, o.size).astype(np.float32),
+               syn_id=rng.integers(0, n_types, o.size).astype(np.uint8), n_post=n_post, n_cols=n_cols)
+
+
+@pytest.mark.parametrize("B", [2, 12, 32])
+def test_syn_bwd_wide_table_walks(B):
+    """The op's dz walks on a 150,001-column table: the type-phased column walk at 4- and
+    32-float G rows (B = 2, 32; dW in the same walk) and the grouped row-sliced walk at 16-float
+    rows (B = 12, dW over the work units beside it); spike and count inputs."""
+    from v1_glif_model_amd.ops import SynapseTable
+    tab = _wide_table()
+    rng = np.random.default_rng(B + 140)
+    basis = rng.random((3, 2)).astype(np.float32)
+    t = SynapseTable(tab.indices, tab.syn_id, (tab.n_post, tab.n_cols), basis)
+    t.set_weights(torch.tensor(tab.weight, device="cuda"))
+    for counts in (False, True):
+        z = (rng.random((B, tab.n_cols)) < 0.05).astype(np.float32)
+        if counts:
+            z *= rng.integers(1, 4, z.shape)
+        dy = rng.normal(0, 1, (B * tab.n_post, 2)).astype(np.float32)
+        dz, dw = t.backward(torch.tensor(z, device="cuda"), torch.tensor(dy, device="cuda"), counts=counts)
+        dz, dw = dz.cpu().numpy(), dw.cpu().numpy()
+        rdz, rdw = orc.syn_bwd(tab, z, basis, dy, use_count=counts)
+        _, _, dz_abs, dw_abs = dense.syn_bwd_f64(tab, z, basis, dy, use_count=counts)
+        assert np.max(np.abs(dz - rdz) - 1e-5 * dz_abs) <= 1e-6
+        assert np.max(np.abs(dw - rdw) - 1e-5 * dw_abs) <= 1e-6
+        assert np.count_nonzero(dw) > 0
 
 
 @pytest.mark.parametrize("B", [5, 9])
