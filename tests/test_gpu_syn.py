@@ -190,14 +190,15 @@ def test_syn_bwd_counts_and_partial_requests(B):
     np.testing.assert_array_equal(dw_only.cpu().numpy(), dw)
 
 
-def _long_column_table(seed=3, n_post=6000):
+def _long_column_table(seed=3, n_post=6000, lens=None):
     """A table with columns longer than the dz walk handles well (the background table's
     shape) beside the other work-unit kinds: long columns split into 1024-synapse chunks
     (4097 entries: a 1-synapse last chunk), columns of 1025-2049, single columns too long to
     share a run (700), runs of up to 64 short columns, and empty columns among them."""
     from v1_glif_model_amd.tables import SynapseTable as Tab
     rng = np.random.default_rng(seed)
-    lens = [5000, 0, 700, 700, 4097, 1025, 3, 0] + list(rng.integers(0, 40, 70)) + [2049, 1024, 0, 6000]
+    if lens is None:
+        lens = [5000, 0, 700, 700, 4097, 1025, 3, 0] + list(rng.integers(0, 40, 70)) + [2049, 1024, 0, 6000]
     post, col = [], []
     for c, n in enumerate(lens):
         p = rng.choice(n_post, size=int(n), replace=False)
@@ -240,8 +241,9 @@ def test_syn_bwd_long_columns(B):
 
 @pytest.mark.parametrize("B", [1, 5, 17])
 def test_syn_fwd_long_columns(B):
-    """Both forwards on the long-column table: the event push over the work units (a chunked
-    column's chunks on waves of their own), spikes and Poisson counts; the pull bit-exact."""
+    """Both forwards on the long-column table (event mode pulls there as well: each active
+    input would cost an atomic per synapse of its column), spikes and Poisson counts; the
+    deterministic pull bit-exact."""
     from v1_glif_model_amd.ops import SynapseTable
     tab = _long_column_table(seed=4)
     rng = np.random.default_rng(B + 90)
@@ -260,6 +262,29 @@ def test_syn_fwd_long_columns(B):
         assert np.max(np.abs(got - dense.syn_fwd_f64(tab, z, basis, use_count=counts)) - 1e-5 * scale) <= 1e-6
         det = t.forward(zt, counts=counts, mode="deterministic").cpu().numpy()
         np.testing.assert_array_equal(det.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("B", [1, 5, 32])
+def test_syn_fwd_event_medium_columns(B):
+    """The event push over work units on a table whose longest column (2048 synapses) still
+    pushes: columns of 1025-2048 split into 1024-synapse chunks on waves of their own, runs of
+    short columns, empty columns; spikes and Poisson counts."""
+    from v1_glif_model_amd.ops import SynapseTable
+    rng0 = np.random.default_rng(21)
+    lens = [2048, 0, 1025, 700, 700, 1500, 3, 0] + list(rng0.integers(0, 40, 70)) + [1024, 2000, 0]
+    tab = _long_column_table(seed=6, lens=lens)
+    rng = np.random.default_rng(B + 120)
+    basis = rng.random((5, 3)).astype(np.float32)
+    t = SynapseTable(tab.indices, tab.syn_id, (tab.n_post, tab.n_cols), basis)
+    t.set_weights(torch.tensor(tab.weight, device="cuda"))
+    for counts in (False, True):
+        z = (rng.random((B, tab.n_cols)) < 0.5).astype(np.float32)
+        if counts:
+            z *= rng.integers(1, 4, z.shape)
+        got = t.forward(torch.tensor(z, device="cuda"), counts=counts, mode="event").cpu().numpy()
+        ref = orc.syn_fwd(tab, z, basis, use_count=counts)
+        scale = dense.syn_fwd_abs(tab, z, basis, use_count=counts)
+        assert np.max(np.abs(got - ref) - 1e-5 * scale) <= 1e-6
 
 
 def test_syn_fwd_event_column_scan():

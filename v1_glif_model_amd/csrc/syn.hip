@@ -12,14 +12,15 @@
 
 namespace glif {
 
-// Tables with a column longer than this take the event push and dz over work units (the
+// Tables with a column longer than this take dz over work units and pull in event mode too (the
 // background table's shape).  The dz walk sums a column on one lane per 4 batch entries and the
 // column scan pushes it on one wave, so their time is the longest column's serial chain (a
 // 6600-synapse column: ~4 ms for dz, ~5 ms for the push); the units split long columns over many
 // waves and cost at most ~1.5x the walk on short ones (runs of short columns use few lanes).
 constexpr int32_t kUnitDzMinColLen = 2 * kDwUnitEntries;
-// The event push takes the units too when the column scan (a wave per 64 columns) would run on
-// fewer waves than this (the LGN table's 17,400 columns: 272 waves).
+// The event push takes the units when the column scan (a wave per 64 columns) would run on fewer
+// waves than this (the LGN table's 17,400 columns: 272 waves) or a column has more synapses than
+// one unit (its chunks then go to waves of their own).
 constexpr int64_t kPushUnitsMaxScanWaves = 2048;
 // dz takes the units too when the walk would run on fewer lanes than this.
 constexpr int64_t kUnitDzMaxWalkLanes = 1024 * kWave;
@@ -472,7 +473,11 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
                    const SynWs &w, hipStream_t s) {
     const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     const int64_t nI = static_cast<int64_t>(B) * t->n_post;
-    if (mode == GLIF_MODE_DETERMINISTIC) {
+    // Event mode pulls too on a table with long columns: each active input would cost one
+    // atomic per synapse of its column and batch entry (the background's Poisson counts: ~2.4
+    // atomics per (b, post, receptor) and call, 67 against 24 us for its pull at B = 5), while
+    // the pull reads each synapse once; its sums are the reference's, well within the event bar.
+    if (mode == GLIF_MODE_DETERMINISTIC || t->max_col_len > kUnitDzMinColLen) {
         if (!counts) {
             // the row pulls over batch masks and activity bitmaps built from z (one step, t = 0):
             // the resident chunk form where it fits, else the half-wave row pull (B * nb > 64,
@@ -521,7 +526,7 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
     }
     int rc = launch_fill_u32(I, 0u, static_cast<size_t>(nI) * t->n_basis, s);
     if (rc) return rc;
-    if (t->n_dwu > 0 && (ceil_div(t->n_cols, kWave) < kPushUnitsMaxScanWaves || t->max_col_len > kUnitDzMinColLen)) {
+    if (t->n_dwu > 0 && (ceil_div(t->n_cols, kWave) < kPushUnitsMaxScanWaves || t->max_col_len > kDwUnitEntries)) {
         const dim3 grid(static_cast<unsigned>(ceil_div(t->n_dwu, kBlock / kWave)));
         if (counts)
             hipLaunchKernelGGL(k_syn_push_units<true>, grid, dim3(kBlock), lds, s, z, B, t->n_cols, t->dwu, t->n_dwu,
