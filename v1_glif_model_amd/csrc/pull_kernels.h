@@ -61,6 +61,18 @@ __device__ inline void pull_row(const PullArgs &a, const float *basis_lds, int l
             const int32_t j = base + 32 * u + lane32;
             e[u] = j < j1 ? pd[j] : 0u;
         }
+        // recurrent entries test their slot's activity bit first (64 columns per word, so the
+        // words stay in the L1 / L2) and gather the 4-byte batch mask only where it is set
+        uint64_t bw[UC];
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int32_t j = base + 32 * u + lane32;
+            bw[u] = 0u;
+            if (REC && j < j1) {
+                const int d = static_cast<int>(e[u] >> 24) + 1;
+                bw[u] = a.abits[static_cast<int64_t>(a.t - d + a.D) * a.W + ((e[u] & kLow24) >> 6)];
+            }
+        }
 #pragma unroll
         for (int u = 0; u < UC; ++u) {
             const int32_t j = base + 32 * u + lane32;
@@ -68,7 +80,8 @@ __device__ inline void pull_row(const PullArgs &a, const float *basis_lds, int l
             if (j < j1) {
                 if (REC) {
                     const int d = static_cast<int>(e[u] >> 24) + 1;
-                    m[u] = a.zmask[static_cast<int64_t>(a.t - d + a.D) * a.Np + (e[u] & kLow24)];
+                    if ((bw[u] >> (e[u] & 63u)) & 1u)
+                        m[u] = a.zmask[static_cast<int64_t>(a.t - d + a.D) * a.Np + (e[u] & kLow24)];
                 } else {
                     m[u] = a.lmask[static_cast<int64_t>(a.t) * a.n_lgn + (e[u] & kLow24)];
                 }
