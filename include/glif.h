@@ -37,7 +37,10 @@ typedef enum {
 } glif_status;
 
 typedef enum {
-    GLIF_MODE_EVENT = 0,         /* event-driven push of active columns, fp32 atomics      */
+    GLIF_MODE_EVENT = 0,         /* event-driven push of active columns, fp32 atomics;     */
+                                 /* sums order-free, within 1e-5 of the reference's (a     */
+                                 /* table with columns > 2048 synapses, whose inputs each  */
+                                 /* fan out to thousands of posts, is pulled instead)      */
     GLIF_MODE_DETERMINISTIC = 1  /* post-row pull in the reference's accumulation order   */
 } glif_mode;
 
