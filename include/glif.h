@@ -95,7 +95,11 @@ int glif_table_set_weights(glif_table *t, const float *w, void *stream);
  * calculate_synaptic_currents (models.py:103-263).
  * Forward: z [B][n_cols] float32 device (event where z > 0; with counts != 0 the
  * value scales the weight as the background current does, models.py:917-931);
- * out: I [B*n_post][n_basis] float32 (overwritten).  mode: glif_mode. */
+ * out: I [B*n_post][n_basis] float32 (overwritten).  mode: glif_mode.
+ * ws: glif_syn_workspace(t, B) bytes of device memory.  The calls that pull spikes -- mode
+ * GLIF_MODE_DETERMINISTIC, or a table with a column longer than 2048 synapses, with counts == 0
+ * -- build batch masks in it and return GLIF_ENOMEM without it; the event push and the pull of
+ * counts use none and accept ws = NULL. */
 size_t glif_syn_workspace(const glif_table *t, int32_t B);
 int glif_syn_fwd(const glif_table *t, const float *z, int32_t B, int32_t counts, int32_t mode,
                  float *I, void *ws, size_t ws_bytes, void *stream);

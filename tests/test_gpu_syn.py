@@ -287,6 +287,45 @@ def test_syn_fwd_event_medium_columns(B):
         assert np.max(np.abs(got - ref) - 1e-5 * scale) <= 1e-6
 
 
+def test_syn_fwd_workspace_rules():
+    """glif_syn_fwd refuses a NULL or short workspace wherever its pull builds batch masks
+    there (spikes in deterministic mode; spikes on a table with columns over 2048 synapses in
+    event mode too) before any launch, and runs without one where nothing uses it (the event
+    push, the pull of counts), with the results of a call that has one."""
+    from v1_glif_model_amd import _lib
+    from v1_glif_model_amd.ops import MODES, SynapseTable
+    rng = np.random.default_rng(33)
+    long_tab = _long_column_table(seed=8)
+    long_basis = rng.random((5, 3)).astype(np.float32)
+    t_long = SynapseTable(long_tab.indices, long_tab.syn_id, (long_tab.n_post, long_tab.n_cols), long_basis)
+    t_long.set_weights(torch.tensor(long_tab.weight, device="cuda"))
+    tb, t_short, _ = _setup(seed=4)
+    B = 3
+    for tab, t, basis, long_cols in ((long_tab, t_long, long_basis, True), (tb.rec, t_short, tb.basis, False)):
+        for mode in ("event", "deterministic"):
+            for counts in (False, True):
+                z = (rng.random((B, tab.n_cols)) < 0.2).astype(np.float32)
+                zt = torch.tensor(z, device="cuda")
+                I = torch.empty((B * t.n_post, t.n_basis), dtype=torch.float32, device="cuda")
+                ws = t.workspace(B, zt.device)
+                needs = not counts and (mode == "deterministic" or long_cols)
+                for w_ptr, w_bytes in ((None, 0), (_lib.ptr(ws), 1)):   # none, and one byte short of all
+                    rc = _lib.lib().glif_syn_fwd(t.handle, _lib.ptr(zt), B, int(counts), MODES[mode],
+                                                 _lib.ptr(I), w_ptr, w_bytes, _lib.stream_ptr())
+                    what = (long_cols, mode, counts, w_bytes)
+                    if needs:
+                        assert rc == -12, what   # GLIF_ENOMEM, nothing launched
+                        continue
+                    assert rc == 0, (what, _lib.lib().glif_last_error())
+                    got = I.cpu().numpy()
+                    ref = orc.syn_fwd(tab, z, basis, use_count=counts)
+                    if mode == "deterministic" or long_cols:   # pulled: the reference's sums
+                        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+                    else:
+                        scale = dense.syn_fwd_abs(tab, z, basis, use_count=counts)
+                        assert np.max(np.abs(got - ref) - 1e-5 * scale) <= 1e-6
+
+
 def test_syn_fwd_event_column_scan():
     """The event push's column scan (a wave per 64 columns), taken by tables of at least
     131,072 columns with no long column: 150,001 columns of 0-3 synapses."""

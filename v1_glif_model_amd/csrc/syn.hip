@@ -467,18 +467,26 @@ static SynWs carve_syn(void *ws, const Table *t, int32_t B, size_t *bytes, bool 
     return w;
 }
 
+// Whether the op forward pulls (deterministic mode, or event mode on a table with long
+// columns: each active input would cost an atomic per synapse of its column and batch entry,
+// and with the background's Poisson counts ~2.4 of them land on each (b, post, receptor) per
+// call, 67 against 24 us pulled at B = 5), and whether that pull uses the workspace (batch
+// masks and activity bits built from z; Poisson counts take the dense-row pull, which needs
+// none).  glif_syn_fwd validates the workspace with the same predicate syn_fwd dispatches on.
+static bool fwd_pulls(const Table *t, int32_t mode) {
+    return mode == GLIF_MODE_DETERMINISTIC || t->max_col_len > kUnitDzMinColLen;
+}
+static bool fwd_uses_ws(const Table *t, int32_t counts, int32_t mode) { return fwd_pulls(t, mode) && !counts; }
+
 // The op forward on a carved workspace (every buffer it reads is written first by this call,
 // so nothing in it has to start at zero).  Launches only; no allocation, no synchronisation.
 static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, int32_t mode, float *I,
                    const SynWs &w, hipStream_t s) {
     const size_t lds = sizeof(float) * t->n_types * t->n_basis;
     const int64_t nI = static_cast<int64_t>(B) * t->n_post;
-    // Event mode pulls too on a table with long columns: each active input would cost one
-    // atomic per synapse of its column and batch entry (the background's Poisson counts: ~2.4
-    // atomics per (b, post, receptor) and call, 67 against 24 us for its pull at B = 5), while
-    // the pull reads each synapse once; its sums are the reference's, well within the event bar.
-    if (mode == GLIF_MODE_DETERMINISTIC || t->max_col_len > kUnitDzMinColLen) {
-        if (!counts) {
+    // the pull's sums are the reference's, well within the event mode's bar
+    if (fwd_pulls(t, mode)) {
+        if (fwd_uses_ws(t, counts, mode)) {
             // the row pulls over batch masks and activity bitmaps built from z (one step, t = 0):
             // the resident chunk form where it fits, else the half-wave row pull (B * nb > 64,
             // or bitmaps beyond LDS), which reads each entry once for all batch entries
@@ -600,10 +608,10 @@ int glif_syn_fwd(const glif_table *tt, const float *z, int32_t B, int32_t counts
     if (mode != GLIF_MODE_EVENT && mode != GLIF_MODE_DETERMINISTIC) return fail(GLIF_EINVAL, "unknown mode");
     const Table *t = reinterpret_cast<const Table *>(tt);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // only the chunk pull (deterministic, spikes, a table with the chunk form) uses the
-    // workspace: the event push and the dense-row pull need none
-    const bool needs_ws = mode == GLIF_MODE_DETERMINISTIC && !counts && t->pidx && t->chunk_desc;
-    if (needs_ws && (!ws || ws_bytes < glif_syn_workspace(tt, B))) return fail(GLIF_ENOMEM, "workspace too small");
+    // the row pulls of spikes use the workspace (batch masks and activity bits); the event
+    // push and the dense-row pull of counts need none
+    if (fwd_uses_ws(t, counts, mode) && (!ws || ws_bytes < glif_syn_workspace(tt, B)))
+        return fail(GLIF_ENOMEM, "workspace too small");
     ProfScope prof(kProfSynFwd, s);
     return syn_fwd(t, z, B, counts, mode, I, carve_syn(ws, t, B, nullptr), s);
 }
