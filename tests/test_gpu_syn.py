@@ -64,6 +64,26 @@ def test_syn_fwd_deterministic_is_bit_exact(seed, B):
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+def test_syn_fwd_deterministic_widest_accumulators():
+    """B = 32 and 8 receptors: 256 (batch, receptor) sums per row, all 8 accumulator slots of
+    every lane of the half-wave row pull; bit-exact with the oracle, spikes and counts."""
+    import dataclasses
+    from v1_glif_model_amd.ops import SynapseTable
+    cfg = dataclasses.replace(tiny_config(n=257), n_basis=8)
+    _, tb = network(cfg, seed=13, dense_basis=True)
+    t = SynapseTable(tb.rec.indices, tb.rec.syn_id, (tb.n_neurons, tb.rec.n_cols), tb.basis,
+                     n_delay_slots=tb.max_delay)
+    t.set_weights(torch.tensor(tb.rec.weight, device="cuda"))
+    rng = np.random.default_rng(14)
+    for counts in (False, True):
+        z = _spikes(rng, 32, tb.rec.n_cols, 0.05)
+        if counts:
+            z *= rng.integers(1, 4, z.shape)
+        got = t.forward(torch.tensor(z, device="cuda"), counts=counts, mode="deterministic").cpu().numpy()
+        ref = orc.syn_fwd(tb.rec, z, tb.basis, use_count=counts)
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_syn_fwd_deterministic_input_table_bit_exact():
     """The op on an input population's table (one delay slot, n_pre != n_post)."""
     from v1_glif_model_amd.ops import SynapseTable
