@@ -26,10 +26,11 @@ constexpr int64_t kPushUnitsMaxScanWaves = 2048;
 constexpr int64_t kUnitDzMaxWalkLanes = 1024 * kWave;
 
 // ---------------------------------------------------------------- forward ----
-// Deterministic pull: thread per (b, post) walks the post's row in ascending
-// (column, synapse id) -- the order in which TF's CPU UnsortedSegmentSum meets the
-// events of this (b, post) -- and writes I[b][post][:] (models.py:141-169).
-template <bool COUNTS>
+// Deterministic pull of Poisson-count inputs (the background form, models.py:917-931): thread
+// per (b, post) walks the post's row in ascending (column, synapse id) -- the order in which
+// TF's CPU UnsortedSegmentSum meets the events of this (b, post) -- scaling each weight by its
+// input's count, and writes I[b][post][:] (models.py:141-169).  Spike inputs take the row
+// pulls over batch masks (pull_kernels.h), which read each entry once for all batch entries.
 __global__ void __launch_bounds__(kBlock)
     k_syn_pull_dense(const float *__restrict__ z, int32_t B, int64_t n_cols, int32_t n_post,
                      int32_t n_pre, const int32_t *__restrict__ row_ptr,
@@ -50,7 +51,7 @@ __global__ void __launch_bounds__(kBlock)
         const int64_t c = static_cast<int64_t>(q & kLow24) + static_cast<int64_t>(q >> 24) * n_pre;
         const float a = zb[c];
         if (!(a > 0.0f)) continue;
-        const float wv = COUNTS ? w[j] * a : w[j];
+        const float wv = w[j] * a;
         const float *bs = basis_lds + sid[j] * nb;
         for (int r = 0; r < nb; ++r) acc[r] = acc[r] + wv * bs[r];
     }
@@ -527,7 +528,7 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
         }
         // Poisson counts scale the weights: a thread per (b, post) over the post's row
         dim3 grid(ceil_div(nI, kBlock));
-        hipLaunchKernelGGL((k_syn_pull_dense<true>), grid, dim3(kBlock), lds, s, z, B, t->n_cols, t->n_post,
+        hipLaunchKernelGGL(k_syn_pull_dense, grid, dim3(kBlock), lds, s, z, B, t->n_cols, t->n_post,
                            t->n_pre, t->row_ptr, t->pd, t->sid_row, t->w_row, t->basis, t->n_types, t->n_basis, I);
         GLIF_HIP(hipGetLastError());
         return GLIF_OK;
