@@ -340,6 +340,41 @@ def test_config2_class_types_compact_rows():
         assert_grads_per_element(g[k], og[k], scale[k], what=k)
 
 
+@pytest.mark.parametrize("name,B", [("lgn", 5), ("lgn", 32), ("bkg", 5), ("bkg", 32)])
+def test_config2_op_level_inputs(config2, name, B):
+    """calculate_synaptic_currents on config 2's input tables at full size (LGN: 17,400 inputs,
+    2.64M synapses; background: 100 inputs of ~6,600 synapses, Poisson counts), one tick of the
+    config's inputs at B = 5 and 32 -- the work-unit paths (the LGN's unit push and unit dz at
+    B = 5, the background's long-column pull and chunked dz): deterministic forward bit-exact
+    with the oracle, event forward, dz and dW within the bar of assert_grads_per_element."""
+    from oracle import dense
+    from v1_glif_model_amd.ops import SynapseTable
+    tb = config2["tb"]
+    pop = tb.lgn if name == "lgn" else tb.bkg
+    counts = name == "bkg"
+    t = SynapseTable(np.stack([pop.post, pop.col], -1), pop.syn_id, (tb.n_neurons, pop.n_cols), tb.basis)
+    t.set_weights(torch.tensor(pop.weight, device="cuda"))
+    lgn, bkg = sy.make_inputs(config2["cfg"], seed=7, seq_len=1, batch=B)
+    z = (lgn if name == "lgn" else bkg)[0].astype(np.float32)
+    rng = np.random.default_rng(8)
+    dy = rng.normal(0, 1, (B * tb.n_neurons, tb.n_basis)).astype(np.float32)
+    zt, dyt = torch.tensor(z, device="cuda"), torch.tensor(dy, device="cuda")
+    det = t.forward(zt, counts=counts, mode="deterministic").cpu().numpy()
+    ev = t.forward(zt, counts=counts, mode="event").cpu().numpy()
+    dz, dw = t.backward(zt, dyt, counts=counts)
+    dz, dw = dz.cpu().numpy(), dw.cpu().numpy()
+    ref = orc.syn_fwd(pop, z, tb.basis, use_count=counts)
+    np.testing.assert_array_equal(det.view(np.uint32), ref.view(np.uint32))
+    scale = dense.syn_fwd_abs(pop, z, tb.basis, use_count=counts)
+    assert_grads_per_element(ev, ref, scale, what=f"{name} event currents")
+    rdz, rdw = orc.syn_bwd(pop, z, tb.basis, dy, use_count=counts)
+    _, _, dz_abs, dw_abs = dense.syn_bwd_f64(pop, z, tb.basis, dy, use_count=counts)
+    assert np.count_nonzero(rdw) > 0
+    say(f"op level {name} B={B}: dz", error_summary(dz, rdz, dz_abs), "dW", error_summary(dw, rdw, dw_abs))
+    assert_grads_per_element(dz, rdz, dz_abs, what=f"{name} dz")
+    assert_grads_per_element(dw, rdw, dw_abs, what=f"{name} dW")
+
+
 def test_config2_op_level(config2):
     """calculate_synaptic_currents on the full config-2 recurrent table (models.py:103-263):
     z_buf [5][D*N] at 5 Hz, dy [5*N][nb] normal.  Deterministic forward bit-exact with the
