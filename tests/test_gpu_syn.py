@@ -84,6 +84,27 @@ def test_syn_fwd_deterministic_widest_accumulators():
         np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("B,nb", [(13, 5), (20, 5), (32, 5), (32, 8)])
+def test_syn_fwd_deterministic_long_rows(B, nb):
+    """The op's row pull with a whole wave per post row, taken by tables whose rows average at
+    least 64 synapses when B * nb exceeds the chunk form's 64 lanes (2 and 4 slots per lane):
+    bit-exact with the oracle."""
+    import dataclasses
+    from v1_glif_model_amd.ops import SynapseTable
+    cfg = dataclasses.replace(tiny_config(n=300, fanin=100), n_basis=nb)
+    _, tb = network(cfg, seed=17, dense_basis=True)
+    assert tb.rec.n_syn >= 64 * tb.n_neurons
+    t = SynapseTable(tb.rec.indices, tb.rec.syn_id, (tb.n_neurons, tb.rec.n_cols), tb.basis,
+                     n_delay_slots=tb.max_delay)
+    t.set_weights(torch.tensor(tb.rec.weight, device="cuda"))
+    rng = np.random.default_rng(B * 10 + nb)
+    for p in (0.01, 0.2):
+        z = _spikes(rng, B, tb.rec.n_cols, p)
+        got = t.forward(torch.tensor(z, device="cuda"), mode="deterministic").cpu().numpy()
+        ref = orc.syn_fwd(tb.rec, z, tb.basis)
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_syn_fwd_deterministic_input_table_bit_exact():
     """The op on an input population's table (one delay slot, n_pre != n_post)."""
     from v1_glif_model_amd.ops import SynapseTable

@@ -146,6 +146,118 @@ __global__ void __launch_bounds__(kBlock) k_pull(PullArgs a) {
     }
 }
 
+// The row pull with a whole wave per post row, for B * nb > 32 accumulator slots: lane a (+64 g)
+// holds the pair a = b * nb + r.  A hit's batch mask is then the same in every lane, read with
+// readlane, so a slot holding none of its batch entries is skipped by a scalar branch and the
+// slots that are visited add by a select on the lane's batch bit -- where the half-wave form's
+// two rows per wave make every slot test divergent, and its exec-mask handling bounds it on the
+// CU's scalar unit.  Each (b, r) sums its hits in entry order from +0, as the half-wave form.
+template <int G, bool REC>
+__device__ inline void pull_row_w(const PullArgs &a, const float *basis_lds, int lane, int32_t j0, int32_t j1,
+                                  const uint32_t (&gmask)[G], const uint32_t (&bm)[G], const int (&rq)[G],
+                                  float (&acc)[G]) {
+    constexpr int UC = 4;  // chunks of 64 entries whose loads are issued together
+    const uint32_t *pd = REC ? a.rec_pd : a.lgn_pd;
+    const uint8_t *sid = REC ? a.rec_sid : a.lgn_sid;
+    const float *w = REC ? a.rec_w : a.lgn_w;
+    for (int32_t base = j0; base < j1; base += kWave * UC) {
+        uint32_t e[UC], m[UC];
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int32_t j = base + kWave * u + lane;
+            e[u] = j < j1 ? pd[j] : 0u;
+        }
+        uint64_t bw[UC];
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int32_t j = base + kWave * u + lane;
+            bw[u] = 0u;
+            if (REC && j < j1) {
+                const int d = static_cast<int>(e[u] >> 24) + 1;
+                bw[u] = a.abits[static_cast<int64_t>(a.t - d + a.D) * a.W + ((e[u] & kLow24) >> 6)];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int32_t j = base + kWave * u + lane;
+            m[u] = 0u;
+            if (j < j1) {
+                if (REC) {
+                    const int d = static_cast<int>(e[u] >> 24) + 1;
+                    if ((bw[u] >> (e[u] & 63u)) & 1u)
+                        m[u] = a.zmask[static_cast<int64_t>(a.t - d + a.D) * a.Np + (e[u] & kLow24)];
+                } else {
+                    m[u] = a.lmask[static_cast<int64_t>(a.t) * a.n_lgn + (e[u] & kLow24)];
+                }
+            }
+        }
+        float wj[UC];
+        int sj[UC];
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            const int32_t j = base + kWave * u + lane;
+            wj[u] = m[u] ? w[j] : 0.0f;
+            sj[u] = m[u] ? sid[j] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < UC; ++u) {
+            uint64_t act = __ballot(m[u] != 0u);
+            while (act) {
+                const int src = __builtin_ctzll(act);
+                act &= act - 1ull;
+                const uint32_t mm = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m[u]), src));
+                const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj[u]), src));
+                const int sv = __builtin_amdgcn_readlane(sj[u], src);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    if (mm & gmask[g]) {
+                        const float nv = acc[g] + wv * basis_lds[sv * a.nb + rq[g]];
+                        acc[g] = (mm & bm[g]) ? nv : acc[g];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int G>
+__global__ void __launch_bounds__(kBlock) k_pull_w(PullArgs a) {
+    extern __shared__ float basis_lds[];
+    load_basis_lds(basis_lds, a.basis, a.n_types * a.nb);
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+    if (row >= a.N) return;  // the whole wave leaves together
+    const int lane = threadIdx.x & (kWave - 1);
+    const int32_t n = static_cast<int32_t>(row);
+    const int BNB = a.B * a.nb;
+    // slot g: the batch entries its lanes hold (the same in every lane), this lane's batch bit
+    // (none past B * nb, so the select never takes it) and basis column
+    uint32_t gmask[G], bm[G];
+    int rq[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int lo = kWave * g, hi = min(BNB, kWave * (g + 1)) - 1;
+        gmask[g] = lo < BNB ? static_cast<uint32_t>(((uint64_t(2) << (hi / a.nb)) - 1u) & ~((uint64_t(1) << (lo / a.nb)) - 1u))
+                            : 0u;
+        const int ai = lane + kWave * g;
+        bm[g] = ai < BNB ? 1u << (ai / a.nb) : 0u;
+        rq[g] = ai < BNB ? ai - (ai / a.nb) * a.nb : 0;
+    }
+    float ar[G], al[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) ar[g] = al[g] = 0.0f;
+    pull_row_w<G, true>(a, basis_lds, lane, a.rec_row[n], a.rec_row[n + 1], gmask, bm, rq, ar);
+    const bool lgn = a.lgn_row != nullptr;
+    if (lgn) pull_row_w<G, false>(a, basis_lds, lane, a.lgn_row[n], a.lgn_row[n + 1], gmask, bm, rq, al);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int ai = lane + kWave * g;
+        if (ai < BNB) {
+            const int b = ai / a.nb, r = ai - b * a.nb;
+            a.I[r * a.os_r + b * a.os_b + n * a.os_n] = lgn ? ar[g] + al[g] : ar[g];
+        }
+    }
+}
+
 // Resident chunk form, used when the step's activity bitmaps fit in LDS: bits_lds holds
 // the "active in some batch entry" bits of steps t-D..t-1 (D planes of W 64-bit words,
 // slot t-d at plane D-d) and of the LGN inputs of step t.  A wave takes row-aligned
@@ -470,15 +582,31 @@ static bool launch_pull_chunks(const PullArgs &pa, hipStream_t s) {
     return true;
 }
 
-static void launch_pull(const PullArgs &pa, size_t lds, hipStream_t s) {
+// wave_rows: a whole wave per post row when B * nb > 32 (k_pull_w), for tables whose rows
+// average at least 64 entries and a post-major output (the op's [B*N][nb]), where it measured
+// faster: the recurrent table at B = 20 and 32, 175 -> 128 and 269 -> 185 us.  Otherwise two
+// rows per wave: the cell's receptor-major [nb][B][N] output then gets two neighbouring posts
+// per store line (config 4's pull at 5 Hz 270 against 302 us per tick with a wave per row), and
+// short rows (the LGN table's 40 entries) do not leave most of a 64-lane chunk idle.
+static void launch_pull(const PullArgs &pa, size_t lds, hipStream_t s, bool wave_rows = false) {
     if (launch_pull_chunks(pa, s)) return;
-    const int G = (pa.B * pa.nb + 31) / 32;
-    const dim3 grid(ceil_div(static_cast<int64_t>(pa.N) * 32, kBlock));
-    switch (G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8) {
-        case 1: GLIF_PROF_LAUNCH(k_pull<1>, grid, dim3(kBlock), lds, s, pa); break;
-        case 2: GLIF_PROF_LAUNCH(k_pull<2>, grid, dim3(kBlock), lds, s, pa); break;
-        case 4: GLIF_PROF_LAUNCH(k_pull<4>, grid, dim3(kBlock), lds, s, pa); break;
-        default: GLIF_PROF_LAUNCH(k_pull<8>, grid, dim3(kBlock), lds, s, pa); break;
+    const int BNB = pa.B * pa.nb;   // <= 32 * kMaxBasis = 256 (checked at the entry points)
+    if (BNB <= 32 || !wave_rows) {
+        const int G = (BNB + 31) / 32;
+        const dim3 grid(ceil_div(static_cast<int64_t>(pa.N) * 32, kBlock));
+        switch (G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8) {
+            case 1: GLIF_PROF_LAUNCH(k_pull<1>, grid, dim3(kBlock), lds, s, pa); break;
+            case 2: GLIF_PROF_LAUNCH(k_pull<2>, grid, dim3(kBlock), lds, s, pa); break;
+            case 4: GLIF_PROF_LAUNCH(k_pull<4>, grid, dim3(kBlock), lds, s, pa); break;
+            default: GLIF_PROF_LAUNCH(k_pull<8>, grid, dim3(kBlock), lds, s, pa); break;
+        }
+        return;
+    }
+    const dim3 grid(ceil_div(static_cast<int64_t>(pa.N) * kWave, kBlock));
+    switch (BNB <= 64 ? 1 : BNB <= 128 ? 2 : 4) {
+        case 1: GLIF_PROF_LAUNCH(k_pull_w<1>, grid, dim3(kBlock), lds, s, pa); break;
+        case 2: GLIF_PROF_LAUNCH(k_pull_w<2>, grid, dim3(kBlock), lds, s, pa); break;
+        default: GLIF_PROF_LAUNCH(k_pull_w<4>, grid, dim3(kBlock), lds, s, pa); break;
     }
 }
 

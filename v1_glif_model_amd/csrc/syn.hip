@@ -522,7 +522,9 @@ static int syn_fwd(const Table *t, const float *z, int32_t B, int32_t counts, in
             hipLaunchKernelGGL(k_op_colmask, dim3(ceil_div(n_mask, kBlock)), dim3(kBlock), 0, s, z, B, t->n_cols,
                                t->n_pre, t->n_slots, pre_pad, w.cm, w.cbits);
             GLIF_HIP(hipGetLastError());
-            launch_pull(pa, lds, s);
+            // a wave per row on tables whose rows average 64 entries or more (the op's output is
+            // post-major)
+            launch_pull(pa, lds, s, t->n_syn >= static_cast<int64_t>(kWave) * t->n_post);
             GLIF_HIP(hipGetLastError());
             return GLIF_OK;
         }
