@@ -2075,7 +2075,7 @@ int glif_cell_forward(glif_cell *cc, int32_t B, int32_t T, int32_t mode, const u
             pl.t = t;
             {
                 ProfScope p(kProfPush, s, true);
-                launch_pull(pl, lds, s);
+                launch_pull(pl, lds, s, true);   // a wave per post row above 32 (b, r) slots
             }
             StepArgs x = sa;
             if (ahead) x.I2 = ring_slot(t);

@@ -220,14 +220,27 @@ __device__ inline void pull_row_w(const PullArgs &a, const float *basis_lds, int
     }
 }
 
+// Rows per k_pull_w workgroup (a wave each); with a receptor-major output their sums leave
+// through LDS together, the neighbouring posts of one (b, r) in one store run.
+constexpr int kPullWaveRows = kBlock / kWave;
+
+// Floats of k_pull_w's dynamic LDS: the basis, then the staged sums of the workgroup's rows.
+static size_t pull_w_lds_floats(int n_types, int nb, int G) {
+    return ((static_cast<size_t>(n_types) * nb + 3) & ~size_t(3)) + static_cast<size_t>(kPullWaveRows) * G * kWave;
+}
+
 template <int G>
 __global__ void __launch_bounds__(kBlock) k_pull_w(PullArgs a) {
-    extern __shared__ float basis_lds[];
+    extern __shared__ float smem[];
+    float *basis_lds = smem;
+    float *stage = smem + ((a.n_types * a.nb + 3) & ~3);   // [kPullWaveRows][G * 64]
     load_basis_lds(basis_lds, a.basis, a.n_types * a.nb);
-    const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-    if (row >= a.N) return;  // the whole wave leaves together
-    const int lane = threadIdx.x & (kWave - 1);
-    const int32_t n = static_cast<int32_t>(row);
+    const int wv_i = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kPullWaveRows;
+    const int64_t row = n0 + wv_i;
+    // a wave past the last row runs no entries and still reaches the workgroup barrier below
+    const bool live = row < a.N;
+    const int32_t n = live ? static_cast<int32_t>(row) : 0;
     const int BNB = a.B * a.nb;
     // slot g: the batch entries its lanes hold (the same in every lane), this lane's batch bit
     // (none past B * nb, so the select never takes it) and basis column
@@ -245,16 +258,39 @@ __global__ void __launch_bounds__(kBlock) k_pull_w(PullArgs a) {
     float ar[G], al[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) ar[g] = al[g] = 0.0f;
-    pull_row_w<G, true>(a, basis_lds, lane, a.rec_row[n], a.rec_row[n + 1], gmask, bm, rq, ar);
+    pull_row_w<G, true>(a, basis_lds, lane, live ? a.rec_row[n] : 0, live ? a.rec_row[n + 1] : 0, gmask, bm, rq,
+                        ar);
     const bool lgn = a.lgn_row != nullptr;
-    if (lgn) pull_row_w<G, false>(a, basis_lds, lane, a.lgn_row[n], a.lgn_row[n + 1], gmask, bm, rq, al);
+    if (lgn)
+        pull_row_w<G, false>(a, basis_lds, lane, live ? a.lgn_row[n] : 0, live ? a.lgn_row[n + 1] : 0, gmask, bm,
+                             rq, al);
+    if (a.os_n != 1) {
+        // post-major output (the op's [B*N][nb]): each wave stores its row, a run of nb floats
+        // per batch entry (staging it with the workgroup's other rows measured slower: the
+        // waves then wait for the slowest row, 129 against 144 us at B = 20)
+        if (!live) return;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const int ai = lane + kWave * g;
-        if (ai < BNB) {
-            const int b = ai / a.nb, r = ai - b * a.nb;
-            a.I[r * a.os_r + b * a.os_b + n * a.os_n] = lgn ? ar[g] + al[g] : ar[g];
+        for (int g = 0; g < G; ++g) {
+            const int ai = lane + kWave * g;
+            if (ai < BNB) {
+                const int b = ai / a.nb, r = ai - b * a.nb;
+                a.I[r * a.os_r + b * a.os_b + n * a.os_n] = lgn ? ar[g] + al[g] : ar[g];
+            }
         }
+        return;
+    }
+    // receptor-major output (the cell's [nb][B][N]): the workgroup's rows leave together, the
+    // neighbouring posts of one (b, r) in one store run (os_n is the same for the whole grid,
+    // so every wave reaches the barrier)
+#pragma unroll
+    for (int g = 0; g < G; ++g) stage[wv_i * (G * kWave) + lane + kWave * g] = lgn ? ar[g] + al[g] : ar[g];
+    __syncthreads();
+    const int rows = static_cast<int>(min<int64_t>(kPullWaveRows, a.N - n0));
+    for (int v = threadIdx.x; v < BNB * kPullWaveRows; v += blockDim.x) {
+        const int pair = v / kPullWaveRows, q = v - pair * kPullWaveRows;
+        if (q >= rows) continue;
+        const int b = pair / a.nb, r = pair - b * a.nb;
+        a.I[r * a.os_r + b * a.os_b + (n0 + q) * a.os_n] = stage[q * (G * kWave) + pair];
     }
 }
 
@@ -582,12 +618,11 @@ static bool launch_pull_chunks(const PullArgs &pa, hipStream_t s) {
     return true;
 }
 
-// wave_rows: a whole wave per post row when B * nb > 32 (k_pull_w), for tables whose rows
-// average at least 64 entries and a post-major output (the op's [B*N][nb]), where it measured
-// faster: the recurrent table at B = 20 and 32, 175 -> 128 and 269 -> 185 us.  Otherwise two
-// rows per wave: the cell's receptor-major [nb][B][N] output then gets two neighbouring posts
-// per store line (config 4's pull at 5 Hz 270 against 302 us per tick with a wave per row), and
-// short rows (the LGN table's 40 entries) do not leave most of a 64-lane chunk idle.
+// wave_rows: a whole wave per post row when B * nb > 32 (k_pull_w), measured faster for the
+// cell (config 4's pull at B = 32: 270 -> 216 us per tick at 5 Hz) and for the op on tables whose
+// rows average at least 64 entries (the recurrent table at B = 20 and 32: 175 -> 128 and
+// 269 -> 189 us); otherwise two rows per wave, so that short rows (the LGN table's 40 entries)
+// do not leave most of a 64-lane chunk idle.
 static void launch_pull(const PullArgs &pa, size_t lds, hipStream_t s, bool wave_rows = false) {
     if (launch_pull_chunks(pa, s)) return;
     const int BNB = pa.B * pa.nb;   // <= 32 * kMaxBasis = 256 (checked at the entry points)
@@ -602,11 +637,13 @@ static void launch_pull(const PullArgs &pa, size_t lds, hipStream_t s, bool wave
         }
         return;
     }
-    const dim3 grid(ceil_div(static_cast<int64_t>(pa.N) * kWave, kBlock));
-    switch (BNB <= 64 ? 1 : BNB <= 128 ? 2 : 4) {
-        case 1: GLIF_PROF_LAUNCH(k_pull_w<1>, grid, dim3(kBlock), lds, s, pa); break;
-        case 2: GLIF_PROF_LAUNCH(k_pull_w<2>, grid, dim3(kBlock), lds, s, pa); break;
-        default: GLIF_PROF_LAUNCH(k_pull_w<4>, grid, dim3(kBlock), lds, s, pa); break;
+    const dim3 grid(ceil_div(static_cast<int64_t>(pa.N), kPullWaveRows));
+    const int G = BNB <= 64 ? 1 : BNB <= 128 ? 2 : 4;
+    const size_t lw = sizeof(float) * pull_w_lds_floats(pa.n_types, pa.nb, G);
+    switch (G) {
+        case 1: GLIF_PROF_LAUNCH(k_pull_w<1>, grid, dim3(kBlock), lw, s, pa); break;
+        case 2: GLIF_PROF_LAUNCH(k_pull_w<2>, grid, dim3(kBlock), lw, s, pa); break;
+        default: GLIF_PROF_LAUNCH(k_pull_w<4>, grid, dim3(kBlock), lw, s, pa); break;
     }
 }
 
