@@ -375,6 +375,8 @@ def bench_op(args):
     from v1_glif_model_amd import synthetic as sy
     from v1_glif_model_amd.ops import SynapseTable
     from v1_glif_model_amd.tables import build_cell_tables
+    if not 1 <= args.op_batch <= 32:
+        raise SystemExit("--op-batch must be in [1, 32]")
     cfg = sy.config(2)
     if args.n_basis:
         cfg = dataclasses.replace(cfg, n_basis=args.n_basis)
@@ -383,8 +385,6 @@ def bench_op(args):
         net = sy.class_types(net, n_classes=args.class_types)
     tb = build_cell_tables(net)
     N, D, B, nb = tb.n_neurons, tb.max_delay, args.op_batch, tb.n_basis
-    if not 1 <= B <= 32:
-        raise SystemExit("--op-batch must be in [1, 32]")
     pop = {"rec": tb.rec, "lgn": tb.lgn, "bkg": tb.bkg}[args.op_table]
     counts = args.op_table == "bkg"
     t = SynapseTable(np.stack([pop.post, pop.col], -1), pop.syn_id, (N, pop.n_cols), tb.basis,
