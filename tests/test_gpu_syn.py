@@ -105,6 +105,32 @@ def test_syn_fwd_deterministic_long_rows(B, nb):
         np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("B", [4, 8, 20])
+def test_syn_fwd_deterministic_bitmaps_beyond_lds(B):
+    """An input table whose activity bitmap exceeds LDS (1.5M inputs: 183 KB of bits), so the
+    row pulls read it from global memory: two rows per wave at B * nb = 20, a wave per row (rows
+    of ~100 synapses) at 40 and 100; bit-exact with the oracle."""
+    from v1_glif_model_amd.tables import SynapseTable as Tab
+    from v1_glif_model_amd.ops import SynapseTable
+    rng = np.random.default_rng(19)
+    n_post, n_cols, fan = 600, 1500000, 100
+    post = np.repeat(np.arange(n_post), fan)
+    col = rng.integers(0, n_cols, post.size)
+    _, first = np.unique(post * n_cols + col, return_index=True)
+    post, col = post[first], col[first]
+    o = np.lexsort((col, post))
+    tab = Tab(post=post[o].astype(np.int64), col=col[o].astype(np.int64),
+              weight=rng.normal(0, 1, o.size).astype(np.float32),
+              syn_id=rng.integers(0, 5, o.size).astype(np.uint8), n_post=n_post, n_cols=n_cols)
+    basis = rng.random((5, 5)).astype(np.float32)
+    t = SynapseTable(tab.indices, tab.syn_id, (n_post, n_cols), basis)
+    t.set_weights(torch.tensor(tab.weight, device="cuda"))
+    z = _spikes(rng, B, tab.n_cols, 0.01)
+    got = t.forward(torch.tensor(z, device="cuda"), mode="deterministic").cpu().numpy()
+    ref = orc.syn_fwd(tab, z, basis)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_syn_fwd_deterministic_input_table_bit_exact():
     """The op on an input population's table (one delay slot, n_pre != n_post)."""
     from v1_glif_model_amd.ops import SynapseTable
